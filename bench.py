@@ -1,0 +1,291 @@
+"""Benchmark: gpt-oss-120b-shape MoE expert-stack decode on one MI355X.
+
+Workload (one step): 36 MoE layers x 128 MXFP4 experts (2880 x 2880 gate, up,
+down; ~60 GiB resident in HBM, generated on the device from a seeded hash),
+int8 routers 128 x 2880 with f32 row scales, top-4 softmax routing, clamped
+SwiGLU, weighted sum and residual, for a batch of tokens (default 1).
+Attention and the dense trunk are excluded. Every step starts from a fresh
+seeded hidden state, so routing - and the experts read - differ per step.
+
+Prints ONE JSON line. `value` is decode tokens per second. `roofline` is the
+dominant kernel (the fused expert gate/up + SwiGLU launch) timed with HIP
+events on the library stream: algorithmic bytes per launch / average launch
+duration, against 8 TB/s. `cpu_baseline` is the reference engine (built from
+its own sources into oracle/_ref) running moe() on the host cores over one
+resident 128-expert layer, scaled to 36 layers.
+
+    python bench.py [--steps K] [--warmup W] [--batch B] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "MoE decode tok/s (gpt-oss-120b shape, 1 GPU) + MXFP4 GEMV % HBM peak"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class HipEvents:
+    """hipEvent timing on a given stream (the library's), via the HIP runtime
+    the library already loaded."""
+
+    def __init__(self):
+        self.hip = C.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def event(self):
+        e = C.c_void_p()
+        assert self.hip.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def record(self, e, stream: int) -> None:
+        assert self.hip.hipEventRecord(e, C.c_void_p(stream)) == 0
+
+    def elapsed_ms(self, a, b) -> float:
+        assert self.hip.hipEventSynchronize(b) == 0
+        ms = C.c_float()
+        assert self.hip.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return float(ms.value)
+
+
+def build_stack(shape, seed: int, max_batch: int):
+    """Resident 36-layer expert table + per-layer routers, all generated on device."""
+    from midge_amd import DT_Q8R, DevBuf, _lib, synth
+    from midge_amd.kern import WT
+    from midge_amd.moe import MoELayer, Stack
+
+    keys = synth.Keys(seed)
+    L = shape.layout
+    table = DevBuf(L.layer_stride * shape.n_layers)
+    proto = MoELayer(shape, table.ptr, WT(DT_Q8R, shape.n_experts, shape.hidden, 1, 1), 1, 1).c()
+    _lib.call("mh_synth_expert_table_dev", table.ptr, C.byref(proto), shape.n_layers, keys.table,
+              synth.EXPERT_EMIN, synth.EXPERT_EMAX, float(synth.normal_c(synth.EXPERT_BIAS_STD)))
+    E, H = shape.n_experts, shape.hidden
+    layers, bufs = [], [table]
+    for l in range(shape.n_layers):
+        rw, rs, rb, nw = DevBuf(E * H), DevBuf(E * 4), DevBuf(E * 4), DevBuf(H * 4)
+        _lib.call("mh_synth_i8_dev", rw.ptr, E * H, keys.layer(keys.router_w, l))
+        _lib.call("mh_synth_uniform_dev", rs.ptr, E, keys.layer(keys.router_s, l), synth.ROUTER_SCALE_LO,
+                  float(synth.uniform_c(synth.ROUTER_SCALE_LO, synth.ROUTER_SCALE_HI)))
+        _lib.call("mh_synth_normal_dev", rb.ptr, E, keys.layer(keys.router_b, l),
+                  float(synth.normal_c(synth.ROUTER_BIAS_STD)))
+        _lib.call("mh_synth_uniform_dev", nw.ptr, H, keys.layer(keys.norm, l), synth.NORM_LO,
+                  float(synth.uniform_c(synth.NORM_LO, synth.NORM_HI)))
+        bufs += [rw, rs, rb, nw]
+        layers.append(MoELayer(shape, table.ptr + l * L.layer_stride, WT(DT_Q8R, E, H, rw.ptr, rs.ptr),
+                               rb.ptr, nw.ptr))
+    return Stack(layers, max_batch), bufs, keys
+
+
+def gu_bytes_per_launch(shape, assignments: int) -> int:
+    """Algorithmic bytes of one expert gate/up launch: per routed (token,
+    expert) pair the gate and up data + f16 scales + f32 bias, the normed input
+    and the activation written."""
+    L = shape.layout
+    per_mat = L.rows[0] * L.cols[0] // 2 + L.rows[0] * (L.cols[0] // 32) * 2 + L.rows[0] * 4
+    return assignments * (2 * per_mat + shape.ffn * 4) + assignments * shape.hidden * 4
+
+
+def step_bytes(shape, batch: int, unique_per_layer: float) -> float:
+    """Algorithmic HBM bytes of one decode step: every routed expert's three
+    matrices (data + scales + bias) once, plus the routers and norm weights."""
+    L = shape.layout
+    router = shape.n_experts * shape.hidden + shape.n_experts * 4 * 2 + shape.hidden * 4
+    return shape.n_layers * (unique_per_layer * L.expert_stride + router) + 2 * batch * shape.hidden * 4
+
+
+def run_gpu(args, shape):
+    import midge_amd
+    from midge_amd import DevBuf, _lib, synth
+    from midge_amd.device import profile_enable, profile_query, profile_reset, stream
+
+    midge_amd.init(0)
+    t0 = time.time()
+    st, bufs, keys = build_stack(shape, args.seed, max(args.batch, 16))
+    midge_amd.sync()
+    log(f"expert table {shape.n_layers} x {shape.n_experts} experts "
+        f"({shape.layout.layer_stride * shape.n_layers / 2**30:.2f} GiB) generated in {time.time() - t0:.1f}s")
+    ev = HipEvents()
+    s = stream()
+
+    def inputs(n_steps: int, batch: int, salt: int) -> DevBuf:
+        xs = DevBuf(n_steps * batch * shape.hidden * 4)
+        _lib.call("mh_synth_normal_dev", xs.ptr, n_steps * batch * shape.hidden,
+                  synth.hash64_int(keys.x, salt), float(synth.normal_c(1.0)))
+        return xs
+
+    def timed(batch: int, steps: int, warmup: int, salt: int, sel=None):
+        xs = inputs(steps + warmup, batch, salt)
+        stride = batch * shape.hidden * 4
+        for i in range(warmup):
+            st.decode(xs.ptr + i * stride, batch)
+        midge_amd.sync()
+        a, b = ev.event(), ev.event()
+        ev.record(a, s)
+        for i in range(steps):
+            st.decode(xs.ptr + (warmup + i) * stride, batch, sel)
+        ev.record(b, s)
+        ms = ev.elapsed_ms(a, b)
+        midge_amd.sync()
+        xs.free()
+        return ms
+
+    ms = timed(args.batch, args.steps, args.warmup, 1)
+    log(f"batch {args.batch}: {ms / args.steps:.3f} ms/step")
+
+    # unique experts per layer actually touched (for the step's algorithmic bytes)
+    nl, k = shape.n_layers, shape.top_k
+    sel = DevBuf(nl * args.batch * k * 4)
+    xs = inputs(1, args.batch, 7)
+    st.decode(xs.ptr, args.batch, sel.ptr)
+    routed = sel.download(np.int32, (nl, args.batch, k))
+    unique = float(np.mean([len(np.unique(routed[l])) for l in range(nl)]))
+    sel.free()
+    xs.free()
+
+    extra = {}
+    if args.batch == 1:
+        ms16 = timed(16, max(args.steps // 2, 5), 2, 2)
+        sel = DevBuf(nl * 16 * k * 4)
+        xs = inputs(1, 16, 8)
+        st.decode(xs.ptr, 16, sel.ptr)
+        r16 = sel.download(np.int32, (nl, 16, k))
+        u16 = float(np.mean([len(np.unique(r16[l])) for l in range(nl)]))
+        sel.free()
+        xs.free()
+        n16 = max(args.steps // 2, 5)
+        extra["batch16"] = {"tok_per_s": 16 * n16 / (ms16 / 1e3), "ms_per_step": ms16 / n16,
+                            "unique_experts_per_layer": u16,
+                            "hbm_GBps": step_bytes(shape, 16, u16) / (ms16 / n16 / 1e3) / 1e9}
+        log(f"batch 16: {ms16 / n16:.3f} ms/step, {u16:.1f} unique experts/layer")
+
+    # dominant kernel: per-launch HIP-event timing of the fused gate/up launch
+    profile_reset()
+    profile_enable(True)
+    xs = inputs(args.prof_steps, args.batch, 3)
+    for i in range(args.prof_steps):
+        st.decode(xs.ptr + i * args.batch * shape.hidden * 4, args.batch)
+    midge_amd.sync()
+    kern = {}
+    for name in ("expert_gu", "expert_down", "gemv", "topk", "rmsnorm", "combine_decode"):
+        tot, n = profile_query(name)
+        kern[name] = {"avg_us": 1e3 * tot / max(n, 1), "launches": n}
+    profile_enable(False)
+    xs.free()
+    gu = kern["expert_gu"]
+    gu_bytes = gu_bytes_per_launch(shape, args.batch * k)
+    achieved = gu_bytes / (gu["avg_us"] * 1e-6) / 1e9
+    for b in bufs:
+        b.free()
+    st.destroy()
+    return ms, unique, kern, achieved, gu_bytes, extra
+
+
+def run_cpu(shape, seed: int, seconds: float):
+    """The reference engine's moe() (AVX2+OpenMP, built from its sources) over
+    one resident gpt-oss-120b layer (128 experts, 1.8 GB host RAM)."""
+    from midge_amd import synth
+    from oracle import pyoracle as po
+
+    kind = "reference" if po.have_ref() else "port"
+    keys = synth.Keys(seed)
+    L = shape.layout
+    table = np.empty(L.layer_stride, np.uint8)
+    lib = po.oracle()
+
+    def gen(e: int) -> int:   # ctypes releases the GIL: experts generate in parallel
+        sl = table[e * L.expert_stride:(e + 1) * L.expert_stride]
+        return lib.mo_synth_expert(sl.ctypes.data, shape.expert_dt, shape.hidden, shape.ffn, shape.n_experts, 0, e,
+                                   keys.table, synth.EXPERT_EMIN, synth.EXPERT_EMAX,
+                                   float(synth.normal_c(synth.EXPERT_BIAS_STD)))
+
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+        assert all(rc == 0 for rc in pool.map(gen, range(shape.n_experts)))
+    w, s, b, nw = synth.host_router(shape, keys, 0)
+    Ls = po.layer_struct(shape, table, w, s, b, nw)
+    xs = synth.host_x(shape, keys, 64, step=11)
+    run = (lambda x: po.ref_moe_decode(Ls, x)) if kind == "reference" else (lambda x: po.moe_decode(Ls, x))
+    for i in range(3):
+        run(xs[i])
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        run(xs[n % 64])
+        n += 1
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)) if kind == "reference" else 1
+    return {"value": n / dt / shape.n_layers, "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"{n} moe() calls on one resident 128-expert gpt-oss-120b layer (batch 1, {dt:.1f}s), "
+                      f"tok/s = calls/s / 36 layers"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--experts", type=int, default=128)
+    ap.add_argument("--seed", type=int, default=120)
+    ap.add_argument("--prof-steps", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the expert stack "
+              "fits one MI355X); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    from midge_amd.synth import MoEShape
+    shape = MoEShape(hidden=2880, ffn=2880, n_experts=args.experts, top_k=4, n_layers=args.layers)
+    ms, unique, kern, achieved, gu_bytes, extra = run_gpu(args, shape)
+    ms_step = ms / args.steps
+    value = args.batch * args.steps / (ms / 1e3)
+    step_b = step_bytes(shape, args.batch, unique)
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = run_cpu(shape, args.seed, args.cpu_seconds)
+    out = {
+        "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"gpt-oss-120b expert-stack decode: {shape.n_layers} layers x {shape.n_experts} "
+                               f"MXFP4 experts (2880x2880 gate/up/down), int8 routers, top-4, "
+                               f"batch {args.batch}; attention/trunk excluded",
+                   "layers": shape.n_layers, "experts": shape.n_experts, "top_k": 4, "hidden": 2880,
+                   "ffn": 2880, "batch": args.batch, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "expert_gu (fused gate/up MXFP4 GEMV + clamped SwiGLU)",
+                     "bytes_per_launch": gu_bytes},
+        "step": {"hbm_bytes": step_b, "hbm_GBps": step_b / (ms_step / 1e3) / 1e9,
+                 "hbm_frac": step_b / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS,
+                 "unique_experts_per_layer": unique, "kernels": kern},
+        "cpu_baseline": cpu,
+    }
+    out.update(extra)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,195 @@
+// mh_internal.h — host-side state and helpers shared by libmidge_hip's
+// translation units, plus the device-side primitives every kernel uses.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/midge_hip.h"
+
+// ------------------------------------------------------------------ host
+
+namespace mh {
+
+// Record a failure message for mh_last_error() and return `code`.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clear the last-error message (called on entry by public functions).
+void clear_error();
+
+// Returns 0, or records the HIP error and returns MH_E_HIP.
+int hip_check(hipError_t e, const char *what);
+#define MH_HIP(call)                                              \
+    do {                                                          \
+        int _rc = ::mh::hip_check((call), #call);                 \
+        if (_rc) return _rc;                                      \
+    } while (0)
+#define MH_TRY(expr)                                              \
+    do {                                                          \
+        int _rc = (expr);                                         \
+        if (_rc) return _rc;                                      \
+    } while (0)
+
+bool initialised();
+int require_init();
+hipStream_t stream();
+int device_cus();   // compute units on the current device
+
+// Pointer resolution. Weights: a host pointer inside a registered region
+// (translated) or device memory. Activations (_dev calls): device memory
+// only. Both check [p, p+bytes) lies inside one allocation/region.
+int resolve_weight(const void *p, uint64_t bytes, const void **dev, const char *what);
+int resolve_dev(const void *p, uint64_t bytes, const char *what);
+
+// Library-owned device scratch that grows on demand (slot = purpose id).
+// Contents are not preserved across growth.
+enum Scratch { S_X = 0, S_Y, S_XB, S_H, S_YE, S_RL, S_SEL, S_W, S_PLAN, S_MISC, S_COUNT };
+int scratch(Scratch slot, uint64_t bytes, void **p);
+
+// Bytes per element class for a tensor view.
+int wt_bytes(int dt, int64_t rows, int64_t cols, uint64_t *data_bytes, uint64_t *scale_bytes);
+
+// Resolve a tensor view's data/scales to device pointers after checks.
+struct DevWT {
+    int dt;
+    int64_t rows, cols;
+    const uint8_t *data;
+    const void *scales;
+};
+int resolve_wt(const mh_wt *t, DevWT *out, const char *what);
+
+// Launch helpers implemented in mh_gemv.hip / mh_moe.hip.
+int launch_gemv(const DevWT &w, const float *x, float *y, int batch, hipStream_t s);
+int launch_rmsnorm(const float *x, const float *w, float *out, int64_t n, float eps,
+                   int batch, hipStream_t s);
+
+// A fully resolved MoE layer (device pointers).
+struct DevLayer {
+    int64_t hidden, ffn;
+    int n_experts, top_k;
+    float alpha, limit, norm_eps;
+    int act_plain, router_norm, expert_dt;
+    uint64_t expert_stride;
+    uint64_t off[9];
+    const uint8_t *experts;
+    DevWT router;
+    const float *router_b, *mlp_norm;
+};
+// Shape/layout checks of a layer description (no pointer access, no HIP).
+int validate_layer(const mh_moe_layer *L);
+int resolve_layer(const mh_moe_layer *L, DevLayer *out);
+
+// Kernel timing (mh_profile_*): while enabled, every launch made through
+// MH_LAUNCH is bracketed by HIP events on its stream and accounted under its
+// name. Off by default; costs nothing when off.
+bool profiling();
+void prof_begin(const char *name, hipStream_t s);
+void prof_end(hipStream_t s);
+
+}  // namespace mh
+
+#define MH_LAUNCH(name, kernel, grid, block, lds, strm, ...)                  \
+    do {                                                                    \
+        const bool _prof = ::mh::profiling();                               \
+        if (_prof) ::mh::prof_begin(name, strm);                            \
+        hipLaunchKernelGGL(kernel, grid, block, lds, strm, __VA_ARGS__);    \
+        if (_prof) ::mh::prof_end(strm);                                    \
+    } while (0)
+
+// ---------------------------------------------------------------- device
+
+typedef float mh_v2f __attribute__((ext_vector_type(2)));
+// 16 bytes of packed weights as four dwords (a native vector, so it can be
+// loaded with the non-temporal builtin).
+typedef uint32_t mh_u4 __attribute__((ext_vector_type(4)));
+
+// binary16 bits -> f32 (exact for every encoding; v_cvt_f32_f16).
+__device__ __forceinline__ float mh_f16(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+
+// Dot of one 16-byte MXFP4 chunk (32 E2M1 codes, low nibble = even column)
+// with xr[0..31]. The codes are converted exactly by the CDNA4 FP4 converter
+// (scale 1.0), accumulated in f32.
+__device__ __forceinline__ float mh_dot_mxfp4(mh_u4 q, const float *xr) {
+    float a = 0.f, b = 0.f;
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        mh_v2f p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 0);
+        mh_v2f p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 1);
+        mh_v2f p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 2);
+        mh_v2f p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 3);
+        a = __builtin_fmaf(p0.x, xr[8 * d + 0], a);
+        b = __builtin_fmaf(p0.y, xr[8 * d + 1], b);
+        a = __builtin_fmaf(p1.x, xr[8 * d + 2], a);
+        b = __builtin_fmaf(p1.y, xr[8 * d + 3], b);
+        a = __builtin_fmaf(p2.x, xr[8 * d + 4], a);
+        b = __builtin_fmaf(p2.y, xr[8 * d + 5], b);
+        a = __builtin_fmaf(p3.x, xr[8 * d + 6], a);
+        b = __builtin_fmaf(p3.y, xr[8 * d + 7], b);
+    }
+    return a + b;
+}
+
+// Dot of one 16-byte q4g32 chunk ((nibble - 8), low nibble = even column).
+__device__ __forceinline__ float mh_dot_q4(mh_u4 q, const float *xr) {
+    float a = 0.f, b = 0.f;
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float lo = (float)((int)((w[d] >> (8 * j)) & 15u) - 8);
+            float hi = (float)((int)((w[d] >> (8 * j + 4)) & 15u) - 8);
+            a = __builtin_fmaf(lo, xr[8 * d + 2 * j], a);
+            b = __builtin_fmaf(hi, xr[8 * d + 2 * j + 1], b);
+        }
+    }
+    return a + b;
+}
+
+// Dot of one 16-byte int8 chunk (16 weights) with xr[0..15].
+__device__ __forceinline__ float mh_dot_i8(mh_u4 q, const float *xr) {
+    float a = 0.f, b = 0.f;
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+            a = __builtin_fmaf((float)(int8_t)(w[d] >> (8 * j)), xr[4 * d + j], a);
+            b = __builtin_fmaf((float)(int8_t)(w[d] >> (8 * j + 8)), xr[4 * d + j + 1], b);
+        }
+    }
+    return a + b;
+}
+
+// Dot of one 16-byte f32 chunk (4 weights).
+__device__ __forceinline__ float mh_dot_f32(mh_u4 q, const float *xr) {
+    float a = __builtin_fmaf(__uint_as_float(q.x), xr[0], __uint_as_float(q.y) * xr[1]);
+    float b = __builtin_fmaf(__uint_as_float(q.z), xr[2], __uint_as_float(q.w) * xr[3]);
+    return a + b;
+}
+
+// Elements per 16-byte chunk, per dtype.
+template <int DT> struct mh_chunk;
+template <> struct mh_chunk<MH_DT_F32> { static constexpr int E = 4; };
+template <> struct mh_chunk<MH_DT_Q8R> { static constexpr int E = 16; };
+template <> struct mh_chunk<MH_DT_Q4G32> { static constexpr int E = 32; };
+template <> struct mh_chunk<MH_DT_MXFP4> { static constexpr int E = 32; };
+
+template <int DT>
+__device__ __forceinline__ float mh_dot_chunk(mh_u4 q, const float *xr) {
+    if constexpr (DT == MH_DT_MXFP4) return mh_dot_mxfp4(q, xr);
+    else if constexpr (DT == MH_DT_Q4G32) return mh_dot_q4(q, xr);
+    else if constexpr (DT == MH_DT_Q8R) return mh_dot_i8(q, xr);
+    else return mh_dot_f32(q, xr);
+}
+
+// Wave64 sum (all lanes get the result).
+__device__ __forceinline__ float mh_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}

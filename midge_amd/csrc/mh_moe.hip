@@ -1,0 +1,634 @@
+// mh_moe.hip — the MoE layer on the GPU: router top-k and weights, the
+// routed experts' fused gate/up + clamped SwiGLU, the down projection, the
+// deterministic weighted combine, and the layer / stack entry points.
+//   mh_moe, mh_moe_dev          moe(), engine/midge.c:469-549
+//   mh_moe_prefill(_dev)        forward_batch() MoE half, engine/midge.c:591-611
+//   mh_topk_dev                 route_topk() selection, engine/midge.c:410-433
+//   mh_expert_major_dev         expert-major loop + expert_apply, midge.c:595-611, 437-467
+//   mh_stack_*                  forward()'s layer loop, MoE half, midge.c:557-560
+#include <vector>
+
+#include "mh_gemv.cuh"
+
+namespace mh {
+namespace {
+
+constexpr int kMaxTopK = 16;       // engine/midge.c:44 MAX_TOPK
+constexpr int kMaxExperts = 1024;  // one wave holds 16 logits per lane
+
+// ------------------------------------------------------------- top-k
+
+// One wave per token: v = logits + bias; the k largest values > -1e30 in
+// descending order, ties to the lower expert index (the insertion lists of
+// engine/midge.c:476-486 and 410-422 produce exactly this). Unfilled slots
+// get sel = `unfilled` (-1 for moe(), 0 for route_topk()) and value -1e30.
+// Weights as engine/midge.c:502-512. usage (may be NULL) += 1 per filled slot.
+__global__ void __launch_bounds__(256)
+k_topk(const float *__restrict__ rl, const float *__restrict__ bias, int n, int E, int k, int router_norm,
+       int unfilled, int32_t *__restrict__ sel, float *__restrict__ w, uint32_t *__restrict__ usage) {
+    const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= n) return;
+    constexpr int PER = kMaxExperts / 64;
+    float v[PER];
+    bool taken[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        int e = lane + 64 * j;
+        v[j] = -INFINITY;
+        taken[j] = true;
+        if (e < E) {
+            v[j] = bias ? rl[(size_t)t * E + e] + bias[e] : rl[(size_t)t * E + e];
+            taken[j] = false;
+        }
+    }
+    float val[kMaxTopK];
+    int idx[kMaxTopK];
+    for (int i = 0; i < k; ++i) {
+        // lane-local best eligible (value > -1e30, strict), lowest index on ties
+        float bv = -1e30f;
+        int bi = INT32_MAX;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            if (!taken[j] && v[j] > bv) {   // strict: NaN and <= -1e30 never win
+                bv = v[j];
+                bi = lane + 64 * j;
+            }
+        }
+        // wave argmax: larger value, then lower index
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            float ov = __shfl_xor(bv, o, 64);
+            int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (bi == INT32_MAX) {
+            val[i] = -1e30f;
+            idx[i] = unfilled;
+        } else {
+            val[i] = bv;
+            idx[i] = bi;
+            if ((bi & 63) == lane) {
+#pragma unroll
+                for (int j = 0; j < PER; ++j)
+                    if (lane + 64 * j == bi) taken[j] = true;
+            }
+        }
+    }
+    float fmx = 0.f, fden = 0.f;
+    if (!router_norm) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (lane + 64 * j < E) m = fmaxf(m, v[j]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (lane + 64 * j < E) s += expf(v[j] - m);
+        fden = mh_wave_sum(s);
+        fmx = m;
+    }
+    if (lane == 0) {
+        float wt[kMaxTopK];
+        if (router_norm) {
+            const float mx = val[0];
+            float den = 0.f;
+            for (int i = 0; i < k; ++i) {
+                wt[i] = expf(val[i] - mx);
+                den += wt[i];
+            }
+            for (int i = 0; i < k; ++i) wt[i] /= den;
+        } else {
+            for (int i = 0; i < k; ++i) wt[i] = expf(val[i] - fmx) / fden;
+        }
+        for (int i = 0; i < k; ++i) {
+            sel[(size_t)t * k + i] = idx[i];
+            w[(size_t)t * k + i] = wt[i];
+            if (usage && idx[i] >= 0 && idx[i] < E && val[i] > -1e30f) atomicAdd(&usage[idx[i]], 1u);
+        }
+    }
+}
+
+// ------------------------------------------------------- expert FFN
+
+struct ExpertArgs {
+    const uint8_t *experts;     // layer base
+    uint64_t stride;
+    uint64_t off[9];
+    int E, k;
+    int64_t hidden, ffn;
+    float alpha, limit;
+    int act_plain;
+};
+
+__device__ __forceinline__ float act_fn(float g, float u, float alpha, float limit, int plain) {
+    if (plain) return g / (1.0f + expf(-g)) * u;
+    if (g > limit) g = limit;
+    if (u > limit) u = limit;
+    if (u < -limit) u = -limit;
+    const float a = g / (1.0f + expf(-alpha * g));
+    return a * (u + 1.0f);
+}
+
+// Gate and up rows of the expert routed for assignment a = blockIdx.y
+// (token a / k), rows [blockIdx.x * rpb, +rpb): h[a][r] = act(g + bg, u + bu).
+// Flat row f interleaves the two matrices: f = 2i (gate row i), 2i+1 (up row i).
+template <int DT>
+__global__ void __launch_bounds__(kGemvThreads)
+k_expert_gu(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restrict__ xb,
+            float *__restrict__ h, int ns, int rpb) {
+    constexpr int CE = mh_chunk<DT>::E;
+    extern __shared__ float lds[];
+    const int a = blockIdx.y;
+    const int e = sel[a];
+    const int r0 = blockIdx.x * rpb;
+    const int nr = (int)min((int64_t)rpb, A.ffn - r0);
+    float *hout = h + (size_t)a * A.ffn;
+    if (e < 0 || e >= A.E) {   // unroutable slot contributes nothing
+        for (int i = threadIdx.x; i < nr; i += blockDim.x) hout[r0 + i] = 0.f;
+        return;
+    }
+    const int C = (int)(A.hidden / CE);
+    float *res = lds;              // [2 * rpb]
+    float *red = lds + 2 * rpb;    // [U][ns][C]
+    const uint8_t *base = A.experts + (uint64_t)e * A.stride;
+    const size_t rowbytes = (size_t)C * 16;
+    const size_t srow = (DT == MH_DT_Q8R) ? 0 : (size_t)C;   // f16 scales per row (4-bit)
+    float xr[CE];
+    load_x<DT>(xb + (size_t)(a / A.k) * A.hidden, C, ns, xr);
+    block_gemv<DT>(
+        [&](int f) {
+            const int m = f & 1, r = r0 + (f >> 1);
+            return RowRef{base + A.off[3 * m] + (size_t)r * rowbytes,
+                          (const uint16_t *)(base + A.off[3 * m + 1]) + (size_t)r * srow};
+        },
+        2 * nr, C, ns, xr, red, res);
+    const float *bg = (const float *)(base + A.off[2]);
+    const float *bu = (const float *)(base + A.off[5]);
+    const float *rsg = (const float *)(base + A.off[1]);
+    const float *rsu = (const float *)(base + A.off[4]);
+    for (int i = threadIdx.x; i < nr; i += blockDim.x) {
+        float g = res[2 * i], u = res[2 * i + 1];
+        if constexpr (DT == MH_DT_Q8R) {
+            g *= rsg[r0 + i];
+            u *= rsu[r0 + i];
+        }
+        g += bg[r0 + i];
+        u += bu[r0 + i];
+        hout[r0 + i] = act_fn(g, u, A.alpha, A.limit, A.act_plain);
+    }
+}
+
+// Down rows of the expert for assignment a = blockIdx.y:
+// ye[a][r] = Wd[r] . h[a] + bd[r].
+template <int DT>
+__global__ void __launch_bounds__(kGemvThreads)
+k_expert_down(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restrict__ h,
+              float *__restrict__ ye, int ns, int rpb) {
+    constexpr int CE = mh_chunk<DT>::E;
+    extern __shared__ float lds[];
+    const int a = blockIdx.y;
+    const int e = sel[a];
+    const int r0 = blockIdx.x * rpb;
+    const int nr = (int)min((int64_t)rpb, A.hidden - r0);
+    float *yout = ye + (size_t)a * A.hidden;
+    if (e < 0 || e >= A.E) {
+        for (int i = threadIdx.x; i < nr; i += blockDim.x) yout[r0 + i] = 0.f;
+        return;
+    }
+    const int C = (int)(A.ffn / CE);
+    float *res = lds;
+    float *red = lds + rpb;
+    const uint8_t *base = A.experts + (uint64_t)e * A.stride;
+    const size_t rowbytes = (size_t)C * 16;
+    const size_t srow = (DT == MH_DT_Q8R) ? 0 : (size_t)C;
+    float xr[CE];
+    load_x<DT>(h + (size_t)a * A.ffn, C, ns, xr);
+    block_gemv<DT>(
+        [&](int f) {
+            const int r = r0 + f;
+            return RowRef{base + A.off[6] + (size_t)r * rowbytes,
+                          (const uint16_t *)(base + A.off[7]) + (size_t)r * srow};
+        },
+        nr, C, ns, xr, red, res);
+    const float *bd = (const float *)(base + A.off[8]);
+    const float *rsd = (const float *)(base + A.off[7]);
+    for (int i = threadIdx.x; i < nr; i += blockDim.x) {
+        float v = res[i];
+        if constexpr (DT == MH_DT_Q8R) v *= rsd[r0 + i];
+        yout[r0 + i] = v + bd[r0 + i];
+    }
+}
+
+// Decode combine (engine/midge.c:514, 544, 548): moe = sum_i w_i y_i in
+// selection order, then x += moe; mul and add rounded separately.
+__global__ void __launch_bounds__(256)
+k_combine_decode(float *__restrict__ x, const float *__restrict__ ye, const float *__restrict__ w, int64_t H,
+                 int k) {
+    const int t = blockIdx.y;
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= H) return;
+    float moe = 0.f;
+    for (int i = 0; i < k; ++i)
+        moe = __fadd_rn(moe, __fmul_rn(w[(size_t)t * k + i], ye[((size_t)t * k + i) * H + r]));
+    x[(size_t)t * H + r] = __fadd_rn(x[(size_t)t * H + r], moe);
+}
+
+// Prefill combine (engine/midge.c:595-611, 465-466): each token's
+// contributions are added straight into its residual in ascending expert
+// order (slot order among equal ids, as the reference's loops give).
+__global__ void __launch_bounds__(256)
+k_combine_prefill(float *__restrict__ x, const float *__restrict__ ye, const int32_t *__restrict__ sel,
+                  const float *__restrict__ w, int64_t H, int k) {
+    const int t = blockIdx.y;
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= H) return;
+    int order[kMaxTopK];
+    for (int i = 0; i < k; ++i) order[i] = i;
+    for (int i = 1; i < k; ++i) {   // insertion sort by expert id, stable
+        int j = i, oi = order[i];
+        while (j > 0 && sel[(size_t)t * k + order[j - 1]] > sel[(size_t)t * k + oi]) {
+            order[j] = order[j - 1];
+            --j;
+        }
+        order[j] = oi;
+    }
+    float acc = x[(size_t)t * H + r];
+    for (int j = 0; j < k; ++j) {
+        const int i = order[j];
+        acc = __fadd_rn(acc, __fmul_rn(w[(size_t)t * k + i], ye[((size_t)t * k + i) * H + r]));
+    }
+    x[(size_t)t * H + r] = acc;
+}
+
+template <int DT>
+int launch_experts_t(const DevLayer &L, int A, const int32_t *sel, const float *xb, float *h, float *ye,
+                     hipStream_t s) {
+    constexpr int CE = mh_chunk<DT>::E;
+    ExpertArgs ea;
+    ea.experts = L.experts;
+    ea.stride = L.expert_stride;
+    for (int i = 0; i < 9; i++) ea.off[i] = L.off[i];
+    ea.E = L.n_experts;
+    ea.k = L.top_k;
+    ea.hidden = L.hidden;
+    ea.ffn = L.ffn;
+    ea.alpha = L.alpha;
+    ea.limit = L.limit;
+    ea.act_plain = L.act_plain;
+    const int64_t target = (int64_t)device_cus() * 2;
+    {   // gate/up: 2 * ffn flat rows per assignment
+        const int C = (int)(L.hidden / CE);
+        int ns, nt;
+        gemv_shape(C, &ns, &nt);
+        int64_t per = (L.ffn * A + target - 1) / target;   // rows per block
+        int64_t step = (ns + 1) / 2;
+        int64_t rpb = ((per + step - 1) / step) * step;
+        if (rpb < step) rpb = step;
+        if (rpb > 2048) rpb = 2048;
+        const int64_t nblk = (L.ffn + rpb - 1) / rpb;
+        const size_t lds = ((size_t)2 * rpb + gemv_lds_floats(ns, C)) * sizeof(float);
+        MH_LAUNCH("expert_gu", k_expert_gu<DT>, dim3((unsigned)nblk, (unsigned)A), dim3(nt), lds, s, ea, sel, xb, h,
+                           ns, (int)rpb);
+        MH_TRY(hip_check(hipGetLastError(), "expert gate/up launch"));
+    }
+    {   // down: hidden rows per assignment
+        const int C = (int)(L.ffn / CE);
+        int ns, nt;
+        gemv_shape(C, &ns, &nt);
+        int64_t per = (L.hidden * A + target - 1) / target;
+        int64_t rpb = ((per + ns - 1) / ns) * ns;
+        if (rpb < ns) rpb = ns;
+        if (rpb > 4096) rpb = 4096;
+        const int64_t nblk = (L.hidden + rpb - 1) / rpb;
+        const size_t lds = ((size_t)rpb + gemv_lds_floats(ns, C)) * sizeof(float);
+        MH_LAUNCH("expert_down", k_expert_down<DT>, dim3((unsigned)nblk, (unsigned)A), dim3(nt), lds, s, ea, sel, h, ye,
+                           ns, (int)rpb);
+        MH_TRY(hip_check(hipGetLastError(), "expert down launch"));
+    }
+    return MH_OK;
+}
+
+int launch_experts(const DevLayer &L, int A, const int32_t *sel, const float *xb, float *h, float *ye,
+                   hipStream_t s) {
+    switch (L.expert_dt) {
+    case MH_DT_F32: return launch_experts_t<MH_DT_F32>(L, A, sel, xb, h, ye, s);
+    case MH_DT_Q8R: return launch_experts_t<MH_DT_Q8R>(L, A, sel, xb, h, ye, s);
+    case MH_DT_Q4G32: return launch_experts_t<MH_DT_Q4G32>(L, A, sel, xb, h, ye, s);
+    case MH_DT_MXFP4: return launch_experts_t<MH_DT_MXFP4>(L, A, sel, xb, h, ye, s);
+    }
+    return fail(MH_E_DTYPE, "unknown expert dtype %d", L.expert_dt);
+}
+
+int launch_topk(const float *rl, const float *bias, int n, int E, int k, int router_norm, int unfilled,
+                int32_t *sel, float *w, uint32_t *usage, hipStream_t s) {
+    const int per_block = 4;
+    MH_LAUNCH("topk", k_topk, dim3((unsigned)((n + per_block - 1) / per_block)), dim3(64 * per_block), 0, s, rl,
+                       bias, n, E, k, router_norm, unfilled, sel, w, usage);
+    return hip_check(hipGetLastError(), "topk launch");
+}
+
+// Scratch for a layer call of n tokens.
+struct LayerBufs {
+    float *xb, *rl, *h, *ye;
+    int32_t *sel;
+    float *w;
+};
+
+int layer_bufs(const DevLayer &L, int n, LayerBufs *b) {
+    void *p;
+    MH_TRY(scratch(S_XB, (uint64_t)n * L.hidden * 4, &p));
+    b->xb = (float *)p;
+    MH_TRY(scratch(S_RL, (uint64_t)n * L.n_experts * 4, &p));
+    b->rl = (float *)p;
+    MH_TRY(scratch(S_H, (uint64_t)n * L.top_k * L.ffn * 4, &p));
+    b->h = (float *)p;
+    MH_TRY(scratch(S_YE, (uint64_t)n * L.top_k * L.hidden * 4, &p));
+    b->ye = (float *)p;
+    MH_TRY(scratch(S_SEL, (uint64_t)n * L.top_k * 4, &p));
+    b->sel = (int32_t *)p;
+    MH_TRY(scratch(S_W, (uint64_t)n * L.top_k * 4, &p));
+    b->w = (float *)p;
+    return MH_OK;
+}
+
+// Router (rmsnorm, logits, top-k) for n tokens into b->xb / b->sel / b->w.
+int run_router(const DevLayer &L, const float *x, int n, int unfilled, const LayerBufs &b, uint32_t *usage,
+               hipStream_t s) {
+    MH_TRY(launch_rmsnorm(x, L.mlp_norm, b.xb, L.hidden, L.norm_eps, n, s));
+    MH_TRY(launch_gemv(L.router, b.xb, b.rl, n, s));
+    return launch_topk(b.rl, L.router_b, n, L.n_experts, L.top_k, L.router_norm, unfilled, b.sel, b.w, usage, s);
+}
+
+int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uint32_t *usage, hipStream_t s) {
+    MH_TRY(run_router(L, x, n, -1, b, usage, s));
+    MH_TRY(launch_experts(L, n * L.top_k, b.sel, b.xb, b.h, b.ye, s));
+    MH_LAUNCH("combine_decode", k_combine_decode, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s, x,
+                       b.ye, b.w, L.hidden, L.top_k);
+    return hip_check(hipGetLastError(), "combine launch");
+}
+
+int run_expert_major(const DevLayer &L, int n, const float *xb, const int32_t *sel, const float *w, float *x,
+                     const LayerBufs &b, hipStream_t s) {
+    MH_TRY(launch_experts(L, n * L.top_k, sel, xb, b.h, b.ye, s));
+    MH_LAUNCH("combine_prefill", k_combine_prefill, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s,
+                       x, b.ye, sel, w, L.hidden, L.top_k);
+    return hip_check(hipGetLastError(), "prefill combine launch");
+}
+
+int check_tokens(int n, const char *what) {
+    if (n < 1 || n > 65535) return fail(MH_E_ARG, "%s: token count %d out of range [1, 65535]", what, n);
+    return MH_OK;
+}
+
+}  // namespace
+
+int validate_layer(const mh_moe_layer *L) {
+    if (!L) return fail(MH_E_ARG, "NULL layer");
+    if (L->hidden < 1 || L->ffn < 1 || L->n_experts < 1)
+        return fail(MH_E_ARG, "layer: hidden=%lld ffn=%lld experts=%d", (long long)L->hidden, (long long)L->ffn,
+                    L->n_experts);
+    if (L->top_k < 1 || L->top_k > kMaxTopK || L->top_k > L->n_experts)
+        return fail(MH_E_ARG, "layer: top_k=%d must be in [1, min(16, experts=%d)]", L->top_k, L->n_experts);
+    if (L->n_experts > kMaxExperts) return fail(MH_E_UNSUPPORTED, "layer: %d experts > %d", L->n_experts, kMaxExperts);
+    // the layout must be wt_expert_layout()'s (engine/mten.h:136-150)
+    uint64_t off[9], pos = 0;
+    int64_t rows[3] = {L->ffn, L->ffn, L->hidden}, cols[3] = {L->hidden, L->hidden, L->ffn};
+    for (int m = 0; m < 3; m++) {
+        uint64_t db, sb;
+        MH_TRY(wt_bytes(L->expert_dt, rows[m], cols[m], &db, &sb));
+        off[3 * m] = pos;
+        pos = (pos + db + 63) & ~63ull;
+        off[3 * m + 1] = pos;
+        pos = (pos + sb + 63) & ~63ull;
+        off[3 * m + 2] = pos;
+        pos = (pos + (uint64_t)rows[m] * 4 + 63) & ~63ull;
+    }
+    for (int i = 0; i < 9; i++)
+        if (off[i] != L->off[i])
+            return fail(MH_E_ARG, "layer: off[%d]=%llu, expected %llu from the expert layout", i,
+                        (unsigned long long)L->off[i], (unsigned long long)off[i]);
+    if (L->expert_stride != ((pos + 63) & ~63ull))
+        return fail(MH_E_ARG, "layer: expert_stride=%llu, expected %llu", (unsigned long long)L->expert_stride,
+                    (unsigned long long)((pos + 63) & ~63ull));
+    const int ce = (L->expert_dt == MH_DT_F32) ? 4 : (L->expert_dt == MH_DT_Q8R) ? 16 : 32;
+    if (L->hidden % ce || L->ffn % ce || L->hidden / ce > kGemvThreads || L->ffn / ce > kGemvThreads)
+        return fail(MH_E_UNSUPPORTED, "layer: hidden=%lld / ffn=%lld not a multiple of %d elements or wider "
+                    "than %d chunks", (long long)L->hidden, (long long)L->ffn, ce, kGemvThreads);
+    if (L->router.rows != L->n_experts || L->router.cols != L->hidden)
+        return fail(MH_E_ARG, "layer: router is %lld x %lld, expected %d x %lld", (long long)L->router.rows,
+                    (long long)L->router.cols, L->n_experts, (long long)L->hidden);
+    return MH_OK;
+}
+
+int resolve_layer(const mh_moe_layer *L, DevLayer *out) {
+    MH_TRY(validate_layer(L));
+    out->hidden = L->hidden;
+    out->ffn = L->ffn;
+    out->n_experts = L->n_experts;
+    out->top_k = L->top_k;
+    out->alpha = L->alpha;
+    out->limit = L->limit;
+    out->norm_eps = L->norm_eps;
+    out->act_plain = L->act_plain ? 1 : 0;
+    out->router_norm = L->router_norm ? 1 : 0;
+    out->expert_dt = L->expert_dt;
+    out->expert_stride = L->expert_stride;
+    for (int i = 0; i < 9; i++) out->off[i] = L->off[i];
+    const void *p;
+    MH_TRY(resolve_weight(L->experts, L->expert_stride * (uint64_t)L->n_experts, &p, "layer experts"));
+    out->experts = (const uint8_t *)p;
+    MH_TRY(resolve_wt(&L->router, &out->router, "layer router"));
+    MH_TRY(resolve_weight(L->router_b, (uint64_t)L->n_experts * 4, &p, "layer router_b"));
+    out->router_b = (const float *)p;
+    MH_TRY(resolve_weight(L->mlp_norm, (uint64_t)L->hidden * 4, &p, "layer mlp_norm"));
+    out->mlp_norm = (const float *)p;
+    return MH_OK;
+}
+
+}  // namespace mh
+
+struct mh_stack {
+    std::vector<mh::DevLayer> layers;
+    int max_batch;
+};
+
+using namespace mh;
+
+extern "C" {
+
+int mh_moe_dev(const mh_moe_layer *Lh, float *x, int batch, int32_t *sel, float *w) {
+    clear_error();
+    MH_TRY(check_tokens(batch, "mh_moe_dev"));
+    MH_TRY(validate_layer(Lh));
+    MH_TRY(require_init());
+    DevLayer L;
+    MH_TRY(resolve_layer(Lh, &L));
+    MH_TRY(resolve_dev(x, (uint64_t)batch * L.hidden * 4, "mh_moe_dev x"));
+    if (sel) MH_TRY(resolve_dev(sel, (uint64_t)batch * L.top_k * 4, "mh_moe_dev sel"));
+    if (w) MH_TRY(resolve_dev(w, (uint64_t)batch * L.top_k * 4, "mh_moe_dev w"));
+    LayerBufs b;
+    MH_TRY(layer_bufs(L, batch, &b));
+    hipStream_t s = stream();
+    MH_TRY(run_decode_layer(L, x, batch, b, nullptr, s));
+    if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, (size_t)batch * L.top_k * 4, hipMemcpyDeviceToDevice, s));
+    if (w) MH_HIP(hipMemcpyAsync(w, b.w, (size_t)batch * L.top_k * 4, hipMemcpyDeviceToDevice, s));
+    return MH_OK;
+}
+
+int mh_moe(const mh_moe_layer *Lh, float *x, int32_t *sel, float *w) {
+    clear_error();
+    if (!x) return fail(MH_E_ARG, "mh_moe: NULL x");
+    MH_TRY(validate_layer(Lh));
+    MH_TRY(require_init());
+    DevLayer L;
+    MH_TRY(resolve_layer(Lh, &L));
+    void *dx;
+    MH_TRY(scratch(S_X, (uint64_t)L.hidden * 4, &dx));
+    LayerBufs b;
+    MH_TRY(layer_bufs(L, 1, &b));
+    hipStream_t s = stream();
+    MH_HIP(hipMemcpyAsync(dx, x, (size_t)L.hidden * 4, hipMemcpyHostToDevice, s));
+    MH_TRY(run_decode_layer(L, (float *)dx, 1, b, nullptr, s));
+    MH_HIP(hipMemcpyAsync(x, dx, (size_t)L.hidden * 4, hipMemcpyDeviceToHost, s));
+    if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, (size_t)L.top_k * 4, hipMemcpyDeviceToHost, s));
+    if (w) MH_HIP(hipMemcpyAsync(w, b.w, (size_t)L.top_k * 4, hipMemcpyDeviceToHost, s));
+    MH_HIP(hipStreamSynchronize(s));
+    return MH_OK;
+}
+
+int mh_topk_dev(const float *logits, int n, int E, int k, int router_norm, int32_t *sel, float *w) {
+    clear_error();
+    MH_TRY(check_tokens(n, "mh_topk_dev"));
+    if (E < 1 || E > kMaxExperts) return fail(MH_E_ARG, "mh_topk_dev: experts=%d out of [1, %d]", E, kMaxExperts);
+    if (k < 1 || k > kMaxTopK || k > E) return fail(MH_E_ARG, "mh_topk_dev: k=%d out of [1, min(16, %d)]", k, E);
+    MH_TRY(require_init());
+    MH_TRY(resolve_dev(logits, (uint64_t)n * E * 4, "mh_topk_dev logits"));
+    MH_TRY(resolve_dev(sel, (uint64_t)n * k * 4, "mh_topk_dev sel"));
+    MH_TRY(resolve_dev(w, (uint64_t)n * k * 4, "mh_topk_dev w"));
+    return launch_topk(logits, nullptr, n, E, k, router_norm ? 1 : 0, 0, sel, w, nullptr, stream());
+}
+
+int mh_expert_major_dev(const mh_moe_layer *Lh, int n, const float *xb, const int32_t *sel, const float *w,
+                        float *x) {
+    clear_error();
+    MH_TRY(check_tokens(n, "mh_expert_major_dev"));
+    MH_TRY(validate_layer(Lh));
+    MH_TRY(require_init());
+    DevLayer L;
+    MH_TRY(resolve_layer(Lh, &L));
+    MH_TRY(resolve_dev(xb, (uint64_t)n * L.hidden * 4, "mh_expert_major_dev xb"));
+    MH_TRY(resolve_dev(sel, (uint64_t)n * L.top_k * 4, "mh_expert_major_dev sel"));
+    MH_TRY(resolve_dev(w, (uint64_t)n * L.top_k * 4, "mh_expert_major_dev w"));
+    MH_TRY(resolve_dev(x, (uint64_t)n * L.hidden * 4, "mh_expert_major_dev x"));
+    LayerBufs b;
+    MH_TRY(layer_bufs(L, n, &b));
+    return run_expert_major(L, n, xb, sel, w, x, b, stream());
+}
+
+int mh_moe_prefill_dev(const mh_moe_layer *Lh, int n, float *x, int32_t *sel, float *w) {
+    clear_error();
+    MH_TRY(check_tokens(n, "mh_moe_prefill_dev"));
+    MH_TRY(validate_layer(Lh));
+    MH_TRY(require_init());
+    DevLayer L;
+    MH_TRY(resolve_layer(Lh, &L));
+    MH_TRY(resolve_dev(x, (uint64_t)n * L.hidden * 4, "mh_moe_prefill_dev x"));
+    if (sel) MH_TRY(resolve_dev(sel, (uint64_t)n * L.top_k * 4, "mh_moe_prefill_dev sel"));
+    if (w) MH_TRY(resolve_dev(w, (uint64_t)n * L.top_k * 4, "mh_moe_prefill_dev w"));
+    LayerBufs b;
+    MH_TRY(layer_bufs(L, n, &b));
+    hipStream_t s = stream();
+    MH_TRY(run_router(L, x, n, 0, b, nullptr, s));
+    MH_TRY(run_expert_major(L, n, b.xb, b.sel, b.w, x, b, s));
+    if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, (size_t)n * L.top_k * 4, hipMemcpyDeviceToDevice, s));
+    if (w) MH_HIP(hipMemcpyAsync(w, b.w, (size_t)n * L.top_k * 4, hipMemcpyDeviceToDevice, s));
+    return MH_OK;
+}
+
+int mh_moe_prefill(const mh_moe_layer *Lh, int n, float *x, int32_t *sel, float *w) {
+    clear_error();
+    MH_TRY(check_tokens(n, "mh_moe_prefill"));
+    if (!x) return fail(MH_E_ARG, "mh_moe_prefill: NULL x");
+    MH_TRY(validate_layer(Lh));
+    MH_TRY(require_init());
+    DevLayer L;
+    MH_TRY(resolve_layer(Lh, &L));
+    void *dx;
+    MH_TRY(scratch(S_X, (uint64_t)n * L.hidden * 4, &dx));
+    LayerBufs b;
+    MH_TRY(layer_bufs(L, n, &b));
+    hipStream_t s = stream();
+    const size_t xbytes = (size_t)n * L.hidden * 4, kbytes = (size_t)n * L.top_k * 4;
+    MH_HIP(hipMemcpyAsync(dx, x, xbytes, hipMemcpyHostToDevice, s));
+    MH_TRY(run_router(L, (float *)dx, n, 0, b, nullptr, s));
+    MH_TRY(run_expert_major(L, n, b.xb, b.sel, b.w, (float *)dx, b, s));
+    MH_HIP(hipMemcpyAsync(x, dx, xbytes, hipMemcpyDeviceToHost, s));
+    if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, kbytes, hipMemcpyDeviceToHost, s));
+    if (w) MH_HIP(hipMemcpyAsync(w, b.w, kbytes, hipMemcpyDeviceToHost, s));
+    MH_HIP(hipStreamSynchronize(s));
+    return MH_OK;
+}
+
+int mh_stack_create(const mh_moe_layer *layers, int n_layers, int max_batch, mh_stack **out) {
+    clear_error();
+    if (!layers || !out || n_layers < 1) return fail(MH_E_ARG, "mh_stack_create: NULL layers/out or n_layers < 1");
+    MH_TRY(check_tokens(max_batch, "mh_stack_create"));
+    for (int i = 0; i < n_layers; i++) MH_TRY(validate_layer(&layers[i]));
+    MH_TRY(require_init());
+    mh_stack *st = new mh_stack();
+    st->max_batch = max_batch;
+    st->layers.resize((size_t)n_layers);
+    for (int i = 0; i < n_layers; i++) {
+        int rc = resolve_layer(&layers[i], &st->layers[(size_t)i]);
+        if (rc) {
+            delete st;
+            return rc;
+        }
+        const DevLayer &a = st->layers[0], &b = st->layers[(size_t)i];
+        if (b.hidden != a.hidden || b.top_k != a.top_k || b.n_experts != a.n_experts || b.ffn != a.ffn) {
+            delete st;
+            return fail(MH_E_ARG, "mh_stack_create: layer %d shape differs from layer 0", i);
+        }
+    }
+    *out = st;
+    return MH_OK;
+}
+
+int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, uint32_t *usage) {
+    clear_error();
+    if (!st) return fail(MH_E_ARG, "mh_stack_decode: NULL stack");
+    if (batch < 1 || batch > st->max_batch)
+        return fail(MH_E_ARG, "mh_stack_decode: batch %d outside [1, %d]", batch, st->max_batch);
+    MH_TRY(require_init());
+    const DevLayer &L0 = st->layers[0];
+    const int nl = (int)st->layers.size(), k = L0.top_k;
+    MH_TRY(resolve_dev(x, (uint64_t)batch * L0.hidden * 4, "mh_stack_decode x"));
+    if (sel) MH_TRY(resolve_dev(sel, (uint64_t)nl * batch * k * 4, "mh_stack_decode sel"));
+    if (w) MH_TRY(resolve_dev(w, (uint64_t)nl * batch * k * 4, "mh_stack_decode w"));
+    if (usage) MH_TRY(resolve_dev(usage, (uint64_t)nl * L0.n_experts * 4, "mh_stack_decode usage"));
+    LayerBufs b;
+    MH_TRY(layer_bufs(L0, batch, &b));
+    hipStream_t s = stream();
+    for (int l = 0; l < nl; l++) {
+        LayerBufs bl = b;
+        if (sel) bl.sel = sel + (size_t)l * batch * k;
+        if (w) bl.w = w + (size_t)l * batch * k;
+        MH_TRY(run_decode_layer(st->layers[(size_t)l], x, batch, bl,
+                                usage ? usage + (size_t)l * L0.n_experts : nullptr, s));
+    }
+    return MH_OK;
+}
+
+int mh_stack_destroy(mh_stack *st) {
+    clear_error();
+    delete st;
+    return MH_OK;
+}
+
+}  // extern "C"

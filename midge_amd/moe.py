@@ -1,0 +1,146 @@
+"""Layer-level interface, named after the reference's MoE functions.
+
+    moe(layer, x)                  moe()                 engine/midge.c:469-549
+    moe_prefill(layer, x)          forward_batch() MoE   engine/midge.c:591-611
+    route_topk_dev / topk_dev      route_topk()          engine/midge.c:404-434
+    expert_major_dev               expert-major block    engine/midge.c:595-611
+    Stack.decode                   forward() layer loop, MoE half, midge.c:557-560
+
+A `MoELayer` carries what the reference's Model holds for one layer: the
+layer's slice of the expert table (experts.midge at wt_expert_layout()
+offsets), the router, its bias and the mlp norm weight.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib, synth
+from .device import DevBuf, Region
+from .kern import WT
+from .synth import Keys, MoEShape
+
+
+class MoELayer:
+    def __init__(self, shape: MoEShape, experts, router: WT, router_b, mlp_norm):
+        self.shape = shape
+        self.experts = experts
+        self.router = router
+        self.router_b = router_b
+        self.mlp_norm = mlp_norm
+        self._keep: list = []
+
+    @staticmethod
+    def _p(a) -> int:
+        if isinstance(a, np.ndarray):
+            return int(a.ctypes.data)
+        return int(a)
+
+    def c(self) -> _lib.MhMoeLayer:
+        s, L = self.shape, self.shape.layout
+        c = _lib.MhMoeLayer()
+        c.hidden, c.ffn, c.n_experts, c.top_k = s.hidden, s.ffn, s.n_experts, s.top_k
+        c.alpha, c.limit, c.norm_eps = s.alpha, s.limit, s.norm_eps
+        c.act_plain, c.router_norm, c.expert_dt = s.act_plain, s.router_norm, s.expert_dt
+        c.expert_stride = L.expert_stride
+        for i, o in enumerate(L.off):
+            c.off[i] = o
+        c.experts = self._p(self.experts)
+        c.router = self.router.c()
+        c.router_b = self._p(self.router_b)
+        c.mlp_norm = self._p(self.mlp_norm)
+        return c
+
+    # ------------------------------------------------------------ builders
+
+    @classmethod
+    def host(cls, shape: MoEShape, experts: np.ndarray, router_w: np.ndarray, router_s: np.ndarray | None,
+             router_b: np.ndarray, mlp_norm: np.ndarray, register: bool = True) -> "MoELayer":
+        """A layer over host arrays; with register=True every array is uploaded
+        through mh_register_region (the drop-in path for mmap'd blobs)."""
+        router = WT(shape.router_dt, shape.n_experts, shape.hidden, router_w, router_s)
+        lay = cls(shape, experts, router, router_b, mlp_norm)
+        if register:
+            for a in (experts, router_w, router_s, router_b, mlp_norm):
+                if isinstance(a, np.ndarray) and a.nbytes:
+                    lay._keep.append(Region(a))
+        return lay
+
+    @classmethod
+    def synthetic_host(cls, shape: MoEShape, seed: int, layer: int = 0, register: bool = True) -> "MoELayer":
+        keys = Keys(seed)
+        experts = synth.host_layer_experts(shape, keys, layer)
+        w, s, b, nw = synth.host_router(shape, keys, layer)
+        return cls.host(shape, experts, w, s, b, nw, register=register)
+
+    def release(self) -> None:
+        for r in self._keep:
+            if isinstance(r, Region):
+                r.release()
+            elif isinstance(r, DevBuf):
+                r.free()
+        self._keep.clear()
+
+
+def moe(layer: MoELayer, x: np.ndarray):
+    """moe() on host x[hidden]: returns (x_out, sel[k], w[k])."""
+    s = layer.shape
+    x = np.array(x, dtype=np.float32, copy=True).reshape(s.hidden)
+    sel = np.empty(s.top_k, dtype=np.int32)
+    w = np.empty(s.top_k, dtype=np.float32)
+    c = layer.c()
+    _lib.call("mh_moe", C.byref(c), x.ctypes.data, sel.ctypes.data, w.ctypes.data)
+    return x, sel, w
+
+
+def moe_dev(layer: MoELayer, x, batch: int, sel=None, w=None) -> None:
+    c = layer.c()
+    _lib.call("mh_moe_dev", C.byref(c), int(x), int(batch), int(sel or 0), int(w or 0))
+
+
+def moe_prefill(layer: MoELayer, x: np.ndarray):
+    """forward_batch()'s MoE half on host x[n][hidden]: returns (x_out, sel[n][k], w[n][k])."""
+    s = layer.shape
+    x = np.array(x, dtype=np.float32, copy=True).reshape(-1, s.hidden)
+    n = x.shape[0]
+    sel = np.empty((n, s.top_k), dtype=np.int32)
+    w = np.empty((n, s.top_k), dtype=np.float32)
+    c = layer.c()
+    _lib.call("mh_moe_prefill", C.byref(c), n, x.ctypes.data, sel.ctypes.data, w.ctypes.data)
+    return x, sel, w
+
+
+def moe_prefill_dev(layer: MoELayer, x, n: int, sel=None, w=None) -> None:
+    c = layer.c()
+    _lib.call("mh_moe_prefill_dev", C.byref(c), int(n), int(x), int(sel or 0), int(w or 0))
+
+
+def topk_dev(logits, n: int, n_experts: int, k: int, router_norm: int, sel, w) -> None:
+    _lib.call("mh_topk_dev", int(logits), int(n), int(n_experts), int(k), int(router_norm), int(sel), int(w))
+
+
+def expert_major_dev(layer: MoELayer, n: int, xb, sel, w, x) -> None:
+    c = layer.c()
+    _lib.call("mh_expert_major_dev", C.byref(c), int(n), int(xb), int(sel), int(w), int(x))
+
+
+class Stack:
+    """A device-resident multi-layer decode plan (mh_stack_*)."""
+
+    def __init__(self, layers: list[MoELayer], max_batch: int):
+        self._cl = (_lib.MhMoeLayer * len(layers))(*[l.c() for l in layers])
+        p = C.c_void_p()
+        _lib.call("mh_stack_create", self._cl, len(layers), int(max_batch), C.byref(p))
+        self.handle = int(p.value)
+        self.n_layers = len(layers)
+        self.layers = layers
+
+    def decode(self, x, batch: int, sel=None, w=None, usage=None) -> None:
+        _lib.call("mh_stack_decode", self.handle, int(x), int(batch), int(sel or 0), int(w or 0),
+                  int(usage or 0))
+
+    def destroy(self) -> None:
+        if self.handle:
+            _lib.call("mh_stack_destroy", self.handle)
+            self.handle = 0

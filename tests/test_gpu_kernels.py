@@ -1,0 +1,214 @@
+"""GPU parity of the kernel-level entry points (through the C ABI) against the
+oracle: exact dequantization, GEMVs of every dtype, batched GEMVs, the
+fallback path, and the device synthetic generators."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import make_golden as mg
+from conftest import rel_l2, say
+from midge_amd import DT_F32, DT_MXFP4, DT_Q4G32, DT_Q8R, DevBuf, synth
+from midge_amd.kern import WT, dequant_dev, matvec_dev, rmsnorm_dev, wk_matvec, wk_row
+from oracle import pyoracle as po
+from test_oracle_kernels import closed_form_dequant, make_tensor, pow2_f16
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(355)
+
+
+def registered(dt, data, sc, rows, cols) -> WT:
+    return WT(dt, rows, cols, data, sc).register()
+
+
+def test_dequant_all_codes_all_exponents(mh):
+    say("dequant MXFP4 all codes x exponents -24..15")
+    exps = np.arange(-24, 16)
+    codes = np.arange(16, dtype=np.uint8)
+    data = np.repeat(np.tile(codes[0::2] | (codes[1::2] << 4), 4).reshape(1, 32), len(exps), axis=0)
+    sc = np.repeat(pow2_f16(exps)[:, None], 2, axis=1)
+    t = registered(DT_MXFP4, data, sc, len(exps), 64)
+    want = closed_form_dequant(DT_MXFP4, data, sc, len(exps), 64)
+    for r in range(len(exps)):
+        got = wk_row(t, r)
+        assert (got.view(np.uint32) == want[r].view(np.uint32)).all(), r   # -0.0 included
+    out = DevBuf(len(exps) * 64 * 4)
+    dequant_dev(t, 0, len(exps), out)
+    got = out.download(np.float32, (len(exps), 64))
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    t.release()
+    out.free()
+
+
+@pytest.mark.parametrize("dt", [DT_F32, DT_Q8R, DT_Q4G32, DT_MXFP4])
+def test_dequant_dtypes(mh, dt):
+    say(f"dequant dt={dt}")
+    rows, cols = 9, 2880
+    data, sc = make_tensor(dt, rows, cols, rng=RNG, sub=True)
+    t = registered(dt, data, sc, rows, cols)
+    for r in (0, 4, 8):
+        want = po.dequant_row(dt, data, sc, cols, r)
+        assert (wk_row(t, r).view(np.uint32) == want.view(np.uint32)).all()
+    t.release()
+
+
+SHAPES = [(1, 32), (13, 64), (40, 2880), (2880, 2880), (5120, 2880), (2880, 4096)]
+
+
+@pytest.mark.parametrize("dt", [DT_F32, DT_Q8R, DT_Q4G32, DT_MXFP4])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_matvec_vs_oracle(mh, dt, shape):
+    rows, cols = shape
+    if dt in (DT_Q4G32, DT_MXFP4) and cols % 32:
+        pytest.skip("4-bit types need cols % 32 == 0")
+    say(f"matvec dt={dt} {rows}x{cols}")
+    data, sc = make_tensor(dt, rows, cols, rng=RNG)
+    x = RNG.standard_normal(cols).astype(np.float32)
+    t = registered(dt, data, sc, rows, cols)
+    y = wk_matvec(t, x)
+    want = po.matvec(dt, data, sc, x, rows, cols)
+    assert rel_l2(y, want) < 1e-5
+    mag = np.abs(closed_form_dequant(dt, data, sc, rows, cols)) @ np.abs(x)
+    assert (np.abs(y - want) <= 1e-5 * mag + 1e-30).all()
+    t.release()
+
+
+@pytest.mark.parametrize("i", range(len(mg.KERNEL_CASES)))
+def test_matvec_golden(mh, i):
+    KG = np.load(mg.os.path.join(mg.HERE, "kernels.npz"))
+    dt, rows, cols, seed = (int(v) for v in KG[f"k{i}_meta"])
+    say(f"matvec golden {i} dt={dt} {rows}x{cols}")
+    data, sc, x = mg.kernel_inputs(dt, rows, cols, seed)
+    t = registered(dt, data, sc, rows, cols)
+    assert rel_l2(wk_matvec(t, x), KG[f"k{i}_y_ref"]) < 1e-5
+    assert rel_l2(wk_matvec(t, x), KG[f"k{i}_y_ref_scalar"]) < 1e-5
+    for j, r in enumerate((0, rows // 2, rows - 1)):
+        assert (wk_row(t, r).view(np.uint32) == KG[f"k{i}_rows"][j].view(np.uint32)).all()
+    t.release()
+
+
+@pytest.mark.parametrize("dt", [DT_Q8R, DT_MXFP4])
+@pytest.mark.parametrize("batch", [1, 3, 32])
+def test_matvec_dev_batch(mh, dt, batch):
+    rows, cols = 2880, 2880
+    say(f"matvec_dev dt={dt} batch={batch}")
+    data, sc = make_tensor(dt, rows, cols, rng=RNG)
+    X = RNG.standard_normal((batch, cols)).astype(np.float32)
+    wd, sd = DevBuf.from_array(data), DevBuf.from_array(sc)
+    xd, yd = DevBuf.from_array(X), DevBuf(batch * rows * 4)
+    t = WT(dt, rows, cols, wd.ptr, sd.ptr)
+    matvec_dev(t, xd, yd, batch)
+    Y = yd.download(np.float32, (batch, rows))
+    for b in range(batch):
+        assert rel_l2(Y[b], po.matvec(dt, data, sc, X[b], rows, cols)) < 1e-5
+    for d in (wd, sd, xd, yd):
+        d.free()
+
+
+@pytest.mark.parametrize("dt,rows,cols", [(DT_F32, 7, 37), (DT_Q8R, 5, 100), (DT_F32, 3, 8192)])
+def test_matvec_fallback_shapes(mh, dt, rows, cols):
+    say(f"matvec fallback dt={dt} {rows}x{cols}")
+    data, sc = make_tensor(dt, rows, cols, rng=RNG)
+    x = RNG.standard_normal(cols).astype(np.float32)
+    t = registered(dt, data, sc, rows, cols)
+    assert rel_l2(wk_matvec(t, x), po.matvec(dt, data, sc, x, rows, cols)) < 1e-5
+    t.release()
+
+
+def test_matvec_unaligned_view(mh):
+    # a view starting 4 bytes into a registered region takes the general path
+    rows, cols = 6, 64
+    buf = RNG.standard_normal(rows * cols + 1).astype(np.float32)
+    say("matvec unaligned f32 view")
+    x = RNG.standard_normal(cols).astype(np.float32)
+    t = WT(DT_F32, rows, cols, buf).register()
+    view = WT(DT_F32, rows, cols, int(buf.ctypes.data) + 4)
+    assert rel_l2(wk_matvec(view, x), po.matvec(DT_F32, buf[1:].copy(), None, x, rows, cols)) < 1e-6
+    t.release()
+
+
+def test_lm_head_sampled_rows(mh):
+    # int8 lm_head at gpt-oss shape (201088 x 2880): every row on the GPU, a
+    # random sample of rows on the oracle, plus the full output's checksum of
+    # row sums against the weights' closed form
+    rows, cols = 201088, 2880
+    say("lm_head q8r 201088x2880 batch 1")
+    k = synth.Keys(77)
+    data = po.synth_i8(k.router_w, rows * cols)   # C generator: no 64-bit temporaries
+    sc = synth.synth_uniform(k.router_s, rows, 1e-3, synth.uniform_c(1e-3, 1e-2))
+    x = synth.synth_normal(k.x, cols, synth.normal_c(1.0))
+    t = registered(DT_Q8R, data, sc, rows, cols)
+    y = wk_matvec(t, x)
+    idx = np.sort(RNG.choice(rows, 512, replace=False))
+    W = data.reshape(rows, cols)
+    sub = np.ascontiguousarray(W[idx])
+    want = po.matvec(DT_Q8R, sub, np.ascontiguousarray(sc[idx]), x, len(idx), cols)
+    assert rel_l2(y[idx], want) < 1e-5
+    # linearity over all rows: sum_r y_r / s_r = (sum_r W_r) . x
+    colsum = W.sum(axis=0, dtype=np.int64).astype(np.float64)
+    lhs = float(np.sum(y.astype(np.float64) / sc.astype(np.float64)))
+    rhs = float(colsum @ x.astype(np.float64))
+    assert abs(lhs - rhs) <= 1e-5 * float(np.abs(colsum) @ np.abs(x))
+    t.release()
+
+
+def test_rmsnorm_dev(mh):
+    say("rmsnorm_dev batch 3")
+    x = RNG.standard_normal((3, 2880)).astype(np.float32) * 4
+    w = RNG.uniform(0.5, 1.5, 2880).astype(np.float32)
+    xd, od, wd = DevBuf.from_array(x), DevBuf(x.nbytes), DevBuf.from_array(w)
+    rmsnorm_dev(xd, wd, od, 2880, 1e-5, 3)
+    got = od.download(np.float32, x.shape)
+    for b in range(3):
+        assert rel_l2(got[b], po.rmsnorm(x[b], w, 1e-5)) < 1e-6
+    for d in (xd, od, wd):
+        d.free()
+
+
+def test_device_synth_matches_host(mh):
+    from midge_amd import _lib
+    say("device synth vs numpy")
+    n = 100003
+    for key in (0, 12345, 2 ** 63 + 11):
+        b = DevBuf(n + 64)
+        _lib.call("mh_synth_bytes_dev", b.ptr, n, key)
+        assert (b.download(np.uint8, n) == synth.synth_bytes(key, n)).all()
+        _lib.call("mh_synth_scales_dev", b.ptr, n // 2, key, -8, -4)
+        assert (b.download(np.uint16, n // 2) == synth.synth_scales(key, n // 2, -8, -4)).all()
+        _lib.call("mh_synth_i8_dev", b.ptr, n, key)
+        assert (b.download(np.int8, n) == synth.synth_i8(key, n)).all()
+        c = synth.normal_c(0.02)
+        _lib.call("mh_synth_normal_dev", b.ptr, n // 4, key, float(c))
+        assert (b.download(np.uint32, n // 4) == synth.synth_normal(key, n // 4, c).view(np.uint32)).all()
+        c = synth.uniform_c(1e-3, 1e-2)
+        _lib.call("mh_synth_uniform_dev", b.ptr, n // 4, key, 1e-3, float(c))
+        assert (b.download(np.uint32, n // 4) == synth.synth_uniform(key, n // 4, 1e-3, c).view(np.uint32)).all()
+        b.free()
+
+
+def test_error_paths_on_device(mh):
+    from midge_amd import _lib
+    say("error paths with a device")
+    host = np.zeros(1024, np.uint8)   # never registered
+    t = _lib.MhWT(DT_Q8R, 4, 64, host.ctypes.data, host.ctypes.data)
+    x = np.zeros(64, np.float32)
+    y = np.zeros(4, np.float32)
+    lib = _lib.load()
+    assert lib.mh_matvec(C.byref(t), x.ctypes.data, y.ctypes.data) == _lib.MH_E_UNREGISTERED
+    d = DevBuf(256)
+    t = _lib.MhWT(DT_Q8R, 4, 64, d.ptr, d.ptr)   # 256 data bytes + scales: fits
+    assert lib.mh_matvec(C.byref(t), x.ctypes.data, y.ctypes.data) == 0
+    t = _lib.MhWT(DT_Q8R, 8, 64, d.ptr, d.ptr)   # 512 bytes of data: overruns
+    assert lib.mh_matvec(C.byref(t), x.ctypes.data, y.ctypes.data) == _lib.MH_E_RANGE
+    # _dev activations must be device memory
+    t = _lib.MhWT(DT_Q8R, 4, 64, d.ptr, d.ptr)
+    assert lib.mh_matvec_dev(C.byref(t), x.ctypes.data, d.ptr, 1) == _lib.MH_E_UNREGISTERED
+    d.free()
+    import os
+    os.environ["MIDGE_HIP_MAX_BYTES"] = "1"
+    try:
+        with pytest.raises(_lib.MidgeHipError) as ei:
+            DevBuf(1 << 20)
+        assert ei.value.code == _lib.MH_E_NOMEM
+    finally:
+        del os.environ["MIDGE_HIP_MAX_BYTES"]

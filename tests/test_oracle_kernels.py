@@ -1,0 +1,213 @@
+"""Pin the oracle's kernels (engine/mkern.h restated in oracle/midge_oracle.c).
+
+Each check uses something other than the oracle's own formula: numpy closed
+forms written from the format definitions, float64 brute-force dot products,
+a stable argsort, float64 softmax / SwiGLU, the closed-form layout at gpt-oss
+shapes, and the reference engine compiled from its sources (bit-exact on its
+scalar path, within f32 rounding on its AVX2+FMA path).
+"""
+import numpy as np
+import pytest
+
+from midge_amd import DT_F32, DT_MXFP4, DT_Q4G32, DT_Q8R
+from oracle import pyoracle as po
+
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float32)
+RNG = np.random.default_rng(20261201)
+
+
+def fp4_values(codes: np.ndarray) -> np.ndarray:
+    mag = E2M1[codes & 7]
+    return np.where(codes & 8, -mag, mag).astype(np.float32)
+
+
+def pow2_f16(e: np.ndarray) -> np.ndarray:
+    """f16 bits of 2^e, e in [-24, 15] (normal and subnormal powers of two)."""
+    e = np.asarray(e, np.int64)
+    return np.where(e >= -14, (e + 15) << 10, 1 << np.clip(e + 24, 0, 30)).astype(np.uint16)
+
+
+def make_tensor(dt: int, rows: int, cols: int, rng=RNG, sub=False):
+    if dt == DT_F32:
+        return rng.standard_normal((rows, cols)).astype(np.float32), None
+    if dt == DT_Q8R:
+        return (rng.integers(-127, 128, (rows, cols)).astype(np.int8),
+                rng.uniform(1e-3, 1e-2, rows).astype(np.float32))
+    data = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+    if dt == DT_MXFP4:
+        lo, hi = (-24, 15) if sub else (-8, -4)
+        sc = pow2_f16(rng.integers(lo, hi + 1, (rows, cols // 32)))
+    else:
+        sc = rng.uniform(0.01, 2.0, (rows, cols // 32)).astype(np.float16).view(np.uint16)
+    return data, sc
+
+
+def closed_form_dequant(dt, data, scales, rows, cols):
+    if dt == DT_F32:
+        return data.astype(np.float32)
+    if dt == DT_Q8R:
+        return data.astype(np.float32) * scales[:, None]
+    codes = np.empty((rows, cols), np.uint8)
+    codes[:, 0::2] = data & 15        # low nibble = even column (engine/mten.h:26-30)
+    codes[:, 1::2] = data >> 4
+    vals = fp4_values(codes) if dt == DT_MXFP4 else (codes.astype(np.int32) - 8).astype(np.float32)
+    s = scales.view(np.float16).astype(np.float32)
+    return (vals.reshape(rows, cols // 32, 32) * s[:, :, None]).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("dt", [DT_F32, DT_Q8R, DT_Q4G32, DT_MXFP4])
+def test_dequant_closed_form(dt):
+    rows, cols = 7, 96
+    data, sc = make_tensor(dt, rows, cols, sub=True)
+    want = closed_form_dequant(dt, data, sc, rows, cols)
+    for r in range(rows):
+        got = po.dequant_row(dt, data, sc, cols, r)
+        assert (got.view(np.uint32) == want[r].view(np.uint32)).all(), r
+
+
+def test_dequant_all_codes_all_exponents():
+    # every FP4 code under every f16-exact power-of-two scale, bit for bit (incl. -0.0)
+    exps = np.arange(-24, 16)
+    codes = np.arange(16, dtype=np.uint8)
+    data = np.tile((codes[0::2] | (codes[1::2] << 4)), 4).reshape(1, 32)   # 64 columns = 2 groups
+    data = np.repeat(data, len(exps), axis=0)
+    sc = np.repeat(pow2_f16(exps)[:, None], 2, axis=1)
+    want = closed_form_dequant(DT_MXFP4, data, sc, len(exps), 64)
+    for r in range(len(exps)):
+        got = po.dequant_row(DT_MXFP4, data, sc, 64, r)
+        assert (got.view(np.uint32) == want[r].view(np.uint32)).all()
+    assert np.signbit(want[:, 8]).all() and (want[:, 8] == 0).all()   # code 8 -> -0.0
+
+
+@pytest.mark.skipif(not po.have_ref(), reason="reference engine not built here")
+@pytest.mark.parametrize("dt", [DT_F32, DT_Q8R, DT_Q4G32, DT_MXFP4])
+def test_dequant_vs_reference(dt):
+    rows, cols = 5, 128
+    data, sc = make_tensor(dt, rows, cols, sub=True)
+    for r in range(rows):
+        a = po.dequant_row(dt, data, sc, cols, r)
+        b = po.ref_row(dt, data, sc, rows, cols, r)
+        assert (a.view(np.uint32) == b.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("dt", [DT_F32, DT_Q8R, DT_Q4G32, DT_MXFP4])
+@pytest.mark.parametrize("shape", [(1, 32), (13, 64), (40, 2880)])
+def test_matvec_brute_force(dt, shape):
+    rows, cols = shape
+    data, sc = make_tensor(dt, rows, cols)
+    x = RNG.standard_normal(cols).astype(np.float32)
+    W = closed_form_dequant(dt, data, sc, rows, cols).astype(np.float64)
+    want = W @ x.astype(np.float64)
+    mag = np.abs(W) @ np.abs(x.astype(np.float64))
+    got = po.matvec(dt, data, sc, x, rows, cols)
+    assert (np.abs(got - want) <= 1e-5 * mag + 1e-30).all()
+
+
+@pytest.mark.skipif(not po.have_ref(), reason="reference engine not built here")
+@pytest.mark.parametrize("dt", [DT_F32, DT_Q8R, DT_Q4G32, DT_MXFP4])
+def test_matvec_vs_reference(dt):
+    rows, cols = 33, 2880
+    data, sc = make_tensor(dt, rows, cols)
+    x = RNG.standard_normal(cols).astype(np.float32)
+    got = po.matvec(dt, data, sc, x, rows, cols)
+    scalar = po.ref_matvec(dt, data, sc, x, rows, cols, scalar=True)
+    assert (got.view(np.uint32) == scalar.view(np.uint32)).all()   # same order, no FMA
+    simd = po.ref_matvec(dt, data, sc, x, rows, cols, scalar=False)
+    mag = np.abs(closed_form_dequant(dt, data, sc, rows, cols)) @ np.abs(x)
+    assert (np.abs(got - simd) <= 1e-5 * mag).all()
+
+
+def test_rmsnorm_closed_form():
+    x = RNG.standard_normal(2880).astype(np.float32) * 3
+    w = RNG.uniform(0.5, 1.5, 2880).astype(np.float32)
+    eps = 1e-5
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 * x64).mean() + eps) * w
+    got = po.rmsnorm(x, w, eps)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    if po.have_ref():
+        r = po.ref_rmsnorm(x, w, eps)
+        assert (got.view(np.uint32) == r.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("decode", [True, False])
+def test_topk_stable_argsort(decode):
+    for trial in range(200):
+        E = int(RNG.choice([4, 8, 32, 128]))
+        k = int(RNG.integers(1, min(16, E) + 1))
+        rl = RNG.standard_normal(E).astype(np.float32)
+        if trial % 3 == 0:   # force ties
+            rl = np.round(rl * 2) / 2
+        sel, val = po.topk(rl, k, decode=decode)
+        want = np.argsort(-rl, kind="stable")[:k]
+        assert (sel == want).all(), (rl, k, sel, want)
+        assert (val == rl[want]).all()
+
+
+def test_topk_unfillable_slots():
+    rl = np.array([-np.inf, 0.5, np.nan, -2e30], np.float32)
+    sel, val = po.topk(rl, 3, decode=True)
+    assert list(sel) == [1, -1, -1] and val[0] == np.float32(0.5)   # moe(): unfilled = -1
+    sel, val = po.topk(rl, 3, decode=False)
+    assert list(sel) == [1, 0, 0]                                    # route_topk(): unfilled = 0
+
+
+def test_router_weights_softmax():
+    rl = RNG.standard_normal(32).astype(np.float32) * 3
+    sel, val = po.topk(rl, 4)
+    w = po.router_weights(rl, val, 1)
+    v = val.astype(np.float64)
+    want = np.exp(v - v.max()) / np.exp(v - v.max()).sum()
+    assert np.allclose(w, want, rtol=1e-6)
+    w0 = po.router_weights(rl, val, 0)
+    full = np.exp(rl.astype(np.float64) - rl.max())
+    assert np.allclose(w0, full[sel] / full.sum(), rtol=1e-6)
+
+
+def test_clamped_swiglu_closed_form():
+    g = np.linspace(-12, 12, 1001).astype(np.float32)
+    u = np.linspace(9, -9, 1001).astype(np.float32)
+    alpha, limit = 1.702, 7.0
+    got = po.act(g, u, alpha, limit)
+    g64 = np.minimum(g.astype(np.float64), limit)      # upper clamp only
+    u64 = np.clip(u.astype(np.float64), -limit, limit)
+    want = g64 / (1 + np.exp(-alpha * g64)) * (u64 + 1)
+    assert np.abs(got - want).max() <= 2e-6 * np.abs(want).max()
+    plain = po.act(g, u, alpha, limit, plain=1)
+    g64 = g.astype(np.float64)
+    assert np.allclose(plain, g64 / (1 + np.exp(-g64)) * u, rtol=1e-5, atol=1e-6)
+
+
+# closed-form offsets of wt_expert_layout at gpt-oss hidden = ffn = 2880 (MXFP4)
+GPT_OSS_OFF = [0, 4147200, 4665600, 4677120, 8824320, 9342720, 9354240, 13501440, 14019840]
+
+
+def test_layout_gpt_oss():
+    off, es, ls = po.expert_layout(DT_MXFP4, 2880, 2880, 128)
+    assert off == GPT_OSS_OFF
+    assert es == 14031360
+    assert 36 * ls == 64656506880            # gpt-oss-120b expert table
+    _, es20, ls20 = po.expert_layout(DT_MXFP4, 2880, 2880, 32)
+    assert 24 * ls20 == 10776084480          # gpt-oss-20b expert table
+
+
+@pytest.mark.skipif(not po.have_ref(), reason="reference engine not built here")
+def test_layout_vs_reference():
+    import ctypes as C
+    r = po.ref()
+    for dt in (DT_F32, DT_Q8R, DT_Q4G32, DT_MXFP4):
+        for hidden, ffn, E in ((64, 64, 4), (2880, 2880, 128), (4096, 14336, 8), (96, 32, 3)):
+            off = np.zeros(9, np.uint64)
+            es, ls = C.c_uint64(), C.c_uint64()
+            r.ref_expert_layout(dt, hidden, ffn, E, off.ctypes.data, C.addressof(es), C.addressof(ls))
+            o2, es2, ls2 = po.expert_layout(dt, hidden, ffn, E)
+            assert [int(v) for v in off] == o2 and es.value == es2 and ls.value == ls2
+
+
+def test_layout_mirror_matches_oracle():
+    from midge_amd.layout import ExpertLayout
+    for dt in (DT_F32, DT_Q8R, DT_Q4G32, DT_MXFP4):
+        for hidden, ffn, E in ((64, 64, 4), (2880, 2880, 128), (96, 32, 3)):
+            L = ExpertLayout(dt, hidden, ffn, E)
+            off, es, ls = po.expert_layout(dt, hidden, ffn, E)
+            assert list(L.off) == off and L.expert_stride == es and L.layer_stride == ls
