@@ -65,35 +65,6 @@ class HipEvents:
         return float(ms.value)
 
 
-def build_stack(shape, seed: int, max_batch: int):
-    """Resident 36-layer expert table + per-layer routers, all generated on device."""
-    from midge_amd import DT_Q8R, DevBuf, _lib, synth
-    from midge_amd.kern import WT
-    from midge_amd.moe import MoELayer, Stack
-
-    keys = synth.Keys(seed)
-    L = shape.layout
-    table = DevBuf(L.layer_stride * shape.n_layers)
-    proto = MoELayer(shape, table.ptr, WT(DT_Q8R, shape.n_experts, shape.hidden, 1, 1), 1, 1).c()
-    _lib.call("mh_synth_expert_table_dev", table.ptr, C.byref(proto), shape.n_layers, keys.table,
-              synth.EXPERT_EMIN, synth.EXPERT_EMAX, float(synth.normal_c(synth.EXPERT_BIAS_STD)))
-    E, H = shape.n_experts, shape.hidden
-    layers, bufs = [], [table]
-    for l in range(shape.n_layers):
-        rw, rs, rb, nw = DevBuf(E * H), DevBuf(E * 4), DevBuf(E * 4), DevBuf(H * 4)
-        _lib.call("mh_synth_i8_dev", rw.ptr, E * H, keys.layer(keys.router_w, l))
-        _lib.call("mh_synth_uniform_dev", rs.ptr, E, keys.layer(keys.router_s, l), synth.ROUTER_SCALE_LO,
-                  float(synth.uniform_c(synth.ROUTER_SCALE_LO, synth.ROUTER_SCALE_HI)))
-        _lib.call("mh_synth_normal_dev", rb.ptr, E, keys.layer(keys.router_b, l),
-                  float(synth.normal_c(synth.ROUTER_BIAS_STD)))
-        _lib.call("mh_synth_uniform_dev", nw.ptr, H, keys.layer(keys.norm, l), synth.NORM_LO,
-                  float(synth.uniform_c(synth.NORM_LO, synth.NORM_HI)))
-        bufs += [rw, rs, rb, nw]
-        layers.append(MoELayer(shape, table.ptr + l * L.layer_stride, WT(DT_Q8R, E, H, rw.ptr, rs.ptr),
-                               rb.ptr, nw.ptr))
-    return Stack(layers, max_batch), bufs, keys
-
-
 def gu_bytes_per_launch(shape, assignments: int) -> int:
     """Algorithmic bytes of one expert gate/up launch: per routed (token,
     expert) pair the gate and up data + f16 scales + f32 bias, the normed input
@@ -118,7 +89,8 @@ def run_gpu(args, shape):
 
     midge_amd.init(0)
     t0 = time.time()
-    st, bufs, keys = build_stack(shape, args.seed, max(args.batch, 16))
+    from midge_amd.moe import Stack
+    st, bufs, keys = Stack.synthetic(shape, args.seed, max(args.batch, 16))
     midge_amd.sync()
     log(f"expert table {shape.n_layers} x {shape.n_experts} experts "
         f"({shape.layout.layer_stride * shape.n_layers / 2**30:.2f} GiB) generated in {time.time() - t0:.1f}s")

@@ -226,17 +226,18 @@ k_expert_down(ExpertArgs A, const int32_t *__restrict__ sel, const float *__rest
 }
 
 // Decode combine (engine/midge.c:514, 544, 548): moe = sum_i w_i y_i in
-// selection order, then x += moe; mul and add rounded separately.
+// selection order, then x += moe; mul and add rounded separately (no FMA).
 __global__ void __launch_bounds__(256)
 k_combine_decode(float *__restrict__ x, const float *__restrict__ ye, const float *__restrict__ w, int64_t H,
                  int k) {
+#pragma clang fp contract(off)
     const int t = blockIdx.y;
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= H) return;
     float moe = 0.f;
     for (int i = 0; i < k; ++i)
-        moe = __fadd_rn(moe, __fmul_rn(w[(size_t)t * k + i], ye[((size_t)t * k + i) * H + r]));
-    x[(size_t)t * H + r] = __fadd_rn(x[(size_t)t * H + r], moe);
+        moe = moe + w[(size_t)t * k + i] * ye[((size_t)t * k + i) * H + r];
+    x[(size_t)t * H + r] = x[(size_t)t * H + r] + moe;
 }
 
 // Prefill combine (engine/midge.c:595-611, 465-466): each token's
@@ -245,6 +246,7 @@ k_combine_decode(float *__restrict__ x, const float *__restrict__ ye, const floa
 __global__ void __launch_bounds__(256)
 k_combine_prefill(float *__restrict__ x, const float *__restrict__ ye, const int32_t *__restrict__ sel,
                   const float *__restrict__ w, int64_t H, int k) {
+#pragma clang fp contract(off)
     const int t = blockIdx.y;
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= H) return;
@@ -261,7 +263,7 @@ k_combine_prefill(float *__restrict__ x, const float *__restrict__ ye, const int
     float acc = x[(size_t)t * H + r];
     for (int j = 0; j < k; ++j) {
         const int i = order[j];
-        acc = __fadd_rn(acc, __fmul_rn(w[(size_t)t * k + i], ye[((size_t)t * k + i) * H + r]));
+        acc = acc + w[(size_t)t * k + i] * ye[((size_t)t * k + i) * H + r];
     }
     x[(size_t)t * H + r] = acc;
 }

@@ -36,7 +36,7 @@ __device__ __forceinline__ void fill_scales(uint16_t *dst, uint64_t n, uint64_t 
 __device__ __forceinline__ float normal_at(uint64_t key, uint64_t i, float c) {
     const uint64_t h = hash64(key, i);
     const int s = (int)(h & 0xffff) + (int)((h >> 16) & 0xffff) + (int)((h >> 32) & 0xffff) + (int)(h >> 48);
-    return __fmul_rn((float)(s - 131070), c);
+    return (float)(s - 131070) * c;
 }
 
 __global__ void k_bytes(uint8_t *dst, uint64_t n, uint64_t key) {
@@ -62,9 +62,10 @@ __global__ void k_normal(float *dst, uint64_t n, uint64_t key, float c) {
 }
 
 __global__ void k_uniform(float *dst, uint64_t n, uint64_t key, float lo, float c) {
+#pragma clang fp contract(off)   // lo + h * c rounded twice, as on the CPU
     const uint64_t nth = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += nth)
-        dst[i] = __fadd_rn(lo, __fmul_rn((float)(hash64(key, i) >> 40), c));
+        dst[i] = lo + (float)(hash64(key, i) >> 40) * c;
 }
 
 struct TableArgs {

@@ -75,6 +75,7 @@ class MoELayer:
         return cls.host(shape, experts, w, s, b, nw, register=register)
 
     def release(self) -> None:
+        """Unregister / free what this layer uploaded (idempotent)."""
         for r in self._keep:
             if isinstance(r, Region):
                 r.release()
@@ -127,6 +128,34 @@ def expert_major_dev(layer: MoELayer, n: int, xb, sel, w, x) -> None:
 
 class Stack:
     """A device-resident multi-layer decode plan (mh_stack_*)."""
+
+    @classmethod
+    def synthetic(cls, shape: MoEShape, seed: int, max_batch: int):
+        """A stack whose expert table (all layers, one allocation at the
+        experts.midge layout), routers and norm weights are generated on the
+        device from `seed` (include/midge_hip_synth.h). Returns (stack,
+        buffers to free, keys); synth's host functions regenerate any slice."""
+        keys = Keys(seed)
+        L = shape.layout
+        table = DevBuf(L.layer_stride * shape.n_layers)
+        proto = MoELayer(shape, table.ptr, WT(shape.router_dt, shape.n_experts, shape.hidden, 1, 1), 1, 1).c()
+        _lib.call("mh_synth_expert_table_dev", table.ptr, C.byref(proto), shape.n_layers, keys.table,
+                  synth.EXPERT_EMIN, synth.EXPERT_EMAX, float(synth.normal_c(synth.EXPERT_BIAS_STD)))
+        E, H = shape.n_experts, shape.hidden
+        layers, bufs = [], [table]
+        for l in range(shape.n_layers):
+            rw, rs, rb, nw = DevBuf(E * H), DevBuf(E * 4), DevBuf(E * 4), DevBuf(H * 4)
+            _lib.call("mh_synth_i8_dev", rw.ptr, E * H, keys.layer(keys.router_w, l))
+            _lib.call("mh_synth_uniform_dev", rs.ptr, E, keys.layer(keys.router_s, l), synth.ROUTER_SCALE_LO,
+                      float(synth.uniform_c(synth.ROUTER_SCALE_LO, synth.ROUTER_SCALE_HI)))
+            _lib.call("mh_synth_normal_dev", rb.ptr, E, keys.layer(keys.router_b, l),
+                      float(synth.normal_c(synth.ROUTER_BIAS_STD)))
+            _lib.call("mh_synth_uniform_dev", nw.ptr, H, keys.layer(keys.norm, l), synth.NORM_LO,
+                      float(synth.uniform_c(synth.NORM_LO, synth.NORM_HI)))
+            bufs += [rw, rs, rb, nw]
+            layers.append(MoELayer(shape, table.ptr + l * L.layer_stride,
+                                   WT(shape.router_dt, E, H, rw.ptr, rs.ptr), rb.ptr, nw.ptr))
+        return cls(layers, max_batch), bufs, keys
 
     def __init__(self, layers: list[MoELayer], max_batch: int):
         self._cl = (_lib.MhMoeLayer * len(layers))(*[l.c() for l in layers])

@@ -17,8 +17,20 @@ pytestmark = pytest.mark.gpu
 RNG = np.random.default_rng(355)
 
 
+_LIVE: list = []
+
+
+@pytest.fixture(autouse=True)
+def _release_tensors():
+    yield
+    while _LIVE:
+        _LIVE.pop().release()
+
+
 def registered(dt, data, sc, rows, cols) -> WT:
-    return WT(dt, rows, cols, data, sc).register()
+    t = WT(dt, rows, cols, data, sc).register()
+    _LIVE.append(t)
+    return t
 
 
 def test_dequant_all_codes_all_exponents(mh):
@@ -122,6 +134,7 @@ def test_matvec_unaligned_view(mh):
     say("matvec unaligned f32 view")
     x = RNG.standard_normal(cols).astype(np.float32)
     t = WT(DT_F32, rows, cols, buf).register()
+    _LIVE.append(t)
     view = WT(DT_F32, rows, cols, int(buf.ctypes.data) + 4)
     assert rel_l2(wk_matvec(view, x), po.matvec(DT_F32, buf[1:].copy(), None, x, rows, cols)) < 1e-6
     t.release()

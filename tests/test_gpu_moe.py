@@ -13,6 +13,9 @@ from oracle import pyoracle as po
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
+# routing weights: softmax of logits ~N(0, 20^2) amplifies the router's f32
+# reassociation (~1e-6 relative on the logits) to ~1e-4 relative on the weights
+WTOL = dict(rtol=1e-3, atol=1e-9)
 MG = np.load(mg.os.path.join(mg.HERE, "moe.npz"))
 
 SHAPES = {
@@ -22,12 +25,26 @@ SHAPES = {
 }
 
 
+_LIVE: list = []
+
+
+@pytest.fixture(autouse=True)
+def _release_layers():
+    """Unregister every layer a test built, pass or fail (a stale region would
+    collide with a later allocation at the same host address)."""
+    yield
+    while _LIVE:
+        _LIVE.pop().release()
+
+
 def build(shape: MoEShape, seed: int, layer: int = 0):
     keys = Keys(seed)
     ex = synth.host_layer_experts(shape, keys, layer)
     w, s, b, nw = synth.host_router(shape, keys, layer)
     arrays = (ex, w, s, b, nw)
-    return keys, arrays, MoELayer.host(shape, *arrays), po.layer_struct(shape, *arrays)
+    lay = MoELayer.host(shape, *arrays)
+    _LIVE.append(lay)
+    return keys, arrays, lay, po.layer_struct(shape, *arrays)
 
 
 @pytest.mark.parametrize("name", ["tiny", "mid", "gptoss20b"])
@@ -41,7 +58,7 @@ def test_moe_decode_vs_oracle(mh, name, seed):
         xo, sel, w = moe(lay, x)
         xr, selr, wr = po.moe_decode(L, x)
         assert (sel == selr).all(), (sel, selr)
-        assert np.allclose(w, wr, rtol=1e-5, atol=1e-7)
+        assert np.allclose(w, wr, **WTOL)
         assert rel_l2(xo, xr) < TOL
     lay.release()
 
@@ -108,7 +125,7 @@ def test_prefill_vs_oracle(mh, name):
     xp, selp, wp = moe_prefill(lay, X)
     xr, selr, wr = po.moe_prefill(L, X)
     assert (selp == selr).all()
-    assert np.allclose(wp, wr, rtol=1e-5, atol=1e-7)
+    assert np.allclose(wp, wr, **WTOL)
     assert rel_l2(xp, xr) < TOL
     # device variant
     xd = DevBuf.from_array(X)
@@ -134,7 +151,7 @@ def test_topk_dev_ties_and_edges(mh):
     for t in range(n):
         s, v = po.topk(logits[t], k, decode=False)
         assert (sel[t] == s).all(), (t, sel[t], s)
-        assert np.allclose(w[t], po.router_weights(logits[t], v, 1), rtol=1e-5, atol=1e-7)
+        assert np.allclose(w[t], po.router_weights(logits[t], v, 1), rtol=1e-5, atol=1e-9)
     for d in (ld, sd, wd):
         d.free()
 
@@ -182,6 +199,7 @@ def test_stack_chain_vs_oracle(mh):
         arrays = (ex, w, s, b, nw)
         keep.append(arrays)
         layers.append(MoELayer.host(shape, *arrays))
+        _LIVE.append(layers[-1])
         structs.append(po.layer_struct(shape, *arrays))
     st = Stack(layers, max_batch=4)
     batch = 3
