@@ -133,7 +133,7 @@ def run_gpu(args, shape):
     xs.free()
 
     extra = {}
-    if args.batch == 1:
+    if args.batch == 1 and not args.no_b16:
         ms16 = timed(16, max(args.steps // 2, 5), 2, 2)
         sel = DevBuf(nl * 16 * k * 4)
         xs = inputs(1, 16, 8)
@@ -148,7 +148,7 @@ def run_gpu(args, shape):
                             "hbm_GBps": step_bytes(shape, 16, u16) / (ms16 / n16 / 1e3) / 1e9}
         log(f"batch 16: {ms16 / n16:.3f} ms/step, {u16:.1f} unique experts/layer")
 
-    # dominant kernel: per-launch HIP-event timing of the fused gate/up launch
+    # dominant kernel: per-launch HIP-event timing on the library stream
     profile_reset()
     profile_enable(True)
     xs = inputs(args.prof_steps, args.batch, 3)
@@ -156,18 +156,58 @@ def run_gpu(args, shape):
         st.decode(xs.ptr + i * args.batch * shape.hidden * 4, args.batch)
     midge_amd.sync()
     kern = {}
-    for name in ("expert_gu", "expert_down", "gemv", "topk", "rmsnorm", "combine_decode"):
+    phases = tuple("decode_step/" + n for n in (
+        "router", "barrier1", "gate_up", "gu_topk", "gu_issue", "gu_math", "gu_reduce", "gu_epilogue",
+        "barrier2_arrive_prefetch", "barrier2_wait", "down_combine", "dn_hload", "dn_math", "dn_reduce",
+        "dn_combine", "barrier3"))
+    for name in ("decode_step", "expert_gu", "expert_down", "gemv", "topk", "rmsnorm", "combine_decode") + phases:
         tot, n = profile_query(name)
-        kern[name] = {"avg_us": 1e3 * tot / max(n, 1), "launches": n}
+        if n:
+            kern[name] = {"avg_us": 1e3 * tot / n, "launches": n}
     profile_enable(False)
     xs.free()
-    gu = kern["expert_gu"]
-    gu_bytes = gu_bytes_per_launch(shape, args.batch * k)
-    achieved = gu_bytes / (gu["avg_us"] * 1e-6) / 1e9
+    if "decode_step" in kern:
+        dom = {"name": "decode_step (all 36 layers in one cooperative launch)",
+               "bytes": step_bytes(shape, args.batch, unique), "avg_us": kern["decode_step"]["avg_us"]}
+    else:
+        dom = {"name": "expert_gu (fused gate/up MXFP4 GEMV + clamped SwiGLU)",
+               "bytes": gu_bytes_per_launch(shape, args.batch * k), "avg_us": kern["expert_gu"]["avg_us"]}
+    dom["GBps"] = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
+    extra["gemv"] = gemv_probe(ev, s)
     for b in bufs:
         b.free()
     st.destroy()
-    return ms, unique, kern, achieved, gu_bytes, extra
+    return ms, unique, kern, dom, extra
+
+
+def gemv_probe(ev, s, rows: int = 262144, cols: int = 2880, reps: int = 20) -> dict:
+    """The MXFP4 GEMV engine alone: y = W x over a 262144 x 2880 matrix
+    (424 MB of nibbles + f16 scales, larger than the 256 MB Infinity Cache),
+    timed with HIP events over `reps` launches."""
+    import midge_amd
+    from midge_amd import DT_MXFP4, DevBuf, _lib, synth
+    from midge_amd.kern import WT, matvec_dev
+    data, sc = DevBuf(rows * cols // 2), DevBuf(rows * cols // 32 * 2)
+    x, y = DevBuf(cols * 4), DevBuf(rows * 4)
+    _lib.call("mh_synth_bytes_dev", data.ptr, rows * cols // 2, 11)
+    _lib.call("mh_synth_scales_dev", sc.ptr, rows * cols // 32, 12, -8, -4)
+    _lib.call("mh_synth_normal_dev", x.ptr, cols, 13, float(synth.normal_c(1.0)))
+    t = WT(DT_MXFP4, rows, cols, data.ptr, sc.ptr)
+    for _ in range(3):
+        matvec_dev(t, x, y)
+    midge_amd.sync()
+    a, b = ev.event(), ev.event()
+    ev.record(a, s)
+    for _ in range(reps):
+        matvec_dev(t, x, y)
+    ev.record(b, s)
+    ms = ev.elapsed_ms(a, b) / reps
+    nbytes = rows * cols // 2 + rows * cols // 32 * 2 + cols * 4 + rows * 4
+    for d in (data, sc, x, y):
+        d.free()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"kernel": "gemv (MXFP4)", "shape": [rows, cols], "bytes": nbytes, "avg_us": ms * 1e3,
+            "GBps": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS}
 
 
 def run_cpu(shape, seed: int, seconds: float):
@@ -220,6 +260,7 @@ def main() -> int:
     ap.add_argument("--prof-steps", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-b16", action="store_true", help="skip the extra batch-16 measurement")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the expert stack "
@@ -228,7 +269,7 @@ def main() -> int:
 
     from midge_amd.synth import MoEShape
     shape = MoEShape(hidden=2880, ffn=2880, n_experts=args.experts, top_k=4, n_layers=args.layers)
-    ms, unique, kern, achieved, gu_bytes, extra = run_gpu(args, shape)
+    ms, unique, kern, dom, extra = run_gpu(args, shape)
     ms_step = ms / args.steps
     value = args.batch * args.steps / (ms / 1e3)
     step_b = step_bytes(shape, args.batch, unique)
@@ -245,10 +286,9 @@ def main() -> int:
                                f"batch {args.batch}; attention/trunk excluded",
                    "layers": shape.n_layers, "experts": shape.n_experts, "top_k": 4, "hidden": 2880,
                    "ffn": 2880, "batch": args.batch, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "expert_gu (fused gate/up MXFP4 GEMV + clamped SwiGLU)",
-                     "bytes_per_launch": gu_bytes},
+        "roofline": {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": dom["name"], "bytes_per_launch": dom["bytes"], "avg_us": dom["avg_us"]},
         "step": {"hbm_bytes": step_b, "hbm_GBps": step_b / (ms_step / 1e3) / 1e9,
                  "hbm_frac": step_b / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS,
                  "unique_experts_per_layer": unique, "kernels": kern},

@@ -21,7 +21,7 @@ ORACLE = os.path.join(ROOT, "oracle")
 REFERENCE = os.environ.get("MIDGE_REFERENCE", "/root/reference")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["mh_runtime.hip", "mh_gemv.hip", "mh_moe.hip", "mh_prefill.hip", "mh_synth.hip"]
+SOURCES = ["mh_runtime.hip", "mh_gemv.hip", "mh_moe.hip", "mh_decode.hip", "mh_prefill.hip", "mh_synth.hip"]
 HIPFLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -73,7 +73,7 @@ def build_oracle() -> None:
     """The C oracle always; the reference shim when the reference checkout exists."""
     _run(["make", "-s", "-B", "libmidge_oracle.so"], cwd=ORACLE)
     if os.path.isfile(os.path.join(REFERENCE, "engine", "midge.c")):
-        _run(["make", "-s", "-B", "ref", f"REF={REFERENCE}"], cwd=ORACLE)
+        _run(["make", "-s", "-B", "ref", "engines", f"REF={REFERENCE}"], cwd=ORACLE)
 
 
 def main() -> int:

@@ -51,38 +51,53 @@ __device__ __forceinline__ void block_gemv(RowFn rowref, int nf, int C, int ns, 
     const int t = threadIdx.x;
     const int slot = t / C, c = t - slot * C;
     const bool active = slot < ns;
-    const int nw = blockDim.x >> 6, wave = t >> 6, lane = t & 63;
     for (int f0 = 0; f0 < nf; f0 += ns * kGemvU) {
+        // Branch-free loads: rows past nf and idle slots re-read a row the
+        // block loads anyway (a cache hit) and are masked out below. Scales
+        // stay raw f16 bits here: converting inside this loop would make
+        // every iteration wait for its load.
         mh_u4 q[kGemvU];
-        float sc[kGemvU];
+        uint32_t sb[kGemvU];
+        const int sl = active ? slot : ns - 1;
 #pragma unroll
         for (int u = 0; u < kGemvU; ++u) {
-            int f = f0 + u * ns + slot;
-            q[u] = mh_u4{0u, 0u, 0u, 0u};
-            sc[u] = 0.f;
-            if (active && f < nf) {
-                RowRef rr = rowref(f);
-                q[u] = __builtin_nontemporal_load((const mh_u4 *)(rr.data + (size_t)c * 16));
-                if constexpr (DT == MH_DT_MXFP4 || DT == MH_DT_Q4G32) sc[u] = mh_f16(rr.scale[c]);
-                else sc[u] = 1.f;
-            }
+            const int f = min(f0 + u * ns + sl, nf - 1);
+            const RowRef rr = rowref(f);
+            q[u] = mh_load16(mh_global(rr.data + (size_t)c * 16));
+            if constexpr (DT == MH_DT_MXFP4 || DT == MH_DT_Q4G32) sb[u] = mh_load_u16(mh_global(rr.scale + c));
+            else sb[u] = 0x3C00u;   // f16 1.0: int8 / f32 rows are scaled by the caller
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < kGemvU; ++u) {
-            float p = mh_dot_chunk<DT>(q[u], xr) * sc[u];
+            const bool valid = active && f0 + u * ns + slot < nf;
+            const float p = mh_dot_chunk<DT>(q[u], xr) * (valid ? mh_f16((uint16_t)sb[u]) : 0.f);
             if (active) red[(u * ns + slot) * C + c] = p;
         }
         __syncthreads();
-        const int items = kGemvU * ns;
-        for (int it = wave; it < items; it += nw) {
-            int f = f0 + it;   // it = u * ns + slot, f = f0 + u * ns + slot
-            if (f >= nf) continue;
-            float s = 0.f;
-            for (int cc = lane; cc < C; cc += 64) s += red[it * C + cc];
-            s = mh_wave_sum(s);
-            if (lane == 0) res[f] = s;
-        }
+        // row it = u * ns + slot is flat row f0 + it
+        block_reduce_rows(red, C, kGemvU * ns, res + f0, [&](int it) { return f0 + it < nf; });
         __syncthreads();
+    }
+}
+
+// Sums each row of red[nrows][C] (row-major) into out[row]. A wave takes 8
+// rows at a time: 8 lanes per row each add every 8th partial, then three
+// xor-shuffles combine them (a fixed order, so results are deterministic).
+// Rows in `skip` (out[row] untouched) are those the caller marks invalid.
+template <class Keep>
+__device__ __forceinline__ void block_reduce_rows(const float *red, int C, int nrows, float *out, Keep keep) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const int rl = lane >> 3, part = lane & 7;
+    for (int r0 = wave * 8; r0 < nrows; r0 += nw * 8) {
+        const int r = r0 + rl;
+        float s = 0.f;
+        if (r < nrows)
+            for (int cc = part; cc < C; cc += 8) s += red[r * C + cc];
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if (part == 0 && r < nrows && keep(r)) out[r] = s;
     }
 }
 

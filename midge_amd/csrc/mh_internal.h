@@ -62,6 +62,11 @@ int launch_gemv(const DevWT &w, const float *x, float *y, int batch, hipStream_t
 int launch_rmsnorm(const float *x, const float *w, float *out, int64_t n, float eps,
                    int batch, hipStream_t s);
 
+// Asynchronous failures: a kernel sets *flag (host-mapped pinned memory);
+// mh_sync() reports and clears any raised flag.
+void watch_async_error(unsigned *flag, const char *msg);
+void unwatch_async_error(unsigned *flag);
+
 // A fully resolved MoE layer (device pointers).
 struct DevLayer {
     int64_t hidden, ffn;
@@ -78,12 +83,21 @@ struct DevLayer {
 int validate_layer(const mh_moe_layer *L);
 int resolve_layer(const mh_moe_layer *L, DevLayer *out);
 
+// One-launch decode step for a whole stack at batch 1 (mh_decode.hip).
+struct StepPlan;
+int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out);
+void step_plan_destroy(StepPlan *p);
+bool step_plan_ok(const StepPlan *p);
+int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_t *sel, float *w,
+             uint32_t *usage, hipStream_t s);
+
 // Kernel timing (mh_profile_*): while enabled, every launch made through
 // MH_LAUNCH is bracketed by HIP events on its stream and accounted under its
 // name. Off by default; costs nothing when off.
 bool profiling();
 void prof_begin(const char *name, hipStream_t s);
 void prof_end(hipStream_t s);
+void prof_add(const char *name, double ms);   // account a duration measured elsewhere
 
 }  // namespace mh
 
@@ -101,6 +115,17 @@ typedef float mh_v2f __attribute__((ext_vector_type(2)));
 // 16 bytes of packed weights as four dwords (a native vector, so it can be
 // loaded with the non-temporal builtin).
 typedef uint32_t mh_u4 __attribute__((ext_vector_type(4)));
+
+// Global-address-space views: loads through them are global_load (not flat),
+// which the compiler cannot infer for pointers read from device tables.
+typedef const uint8_t __attribute__((address_space(1))) *mh_gbytes;
+__device__ __forceinline__ mh_gbytes mh_global(const void *p) { return (mh_gbytes)p; }
+__device__ __forceinline__ mh_u4 mh_load16(mh_gbytes p) {
+    return __builtin_nontemporal_load((const mh_u4 __attribute__((address_space(1))) *)p);
+}
+__device__ __forceinline__ uint32_t mh_load_u16(mh_gbytes p) {
+    return *(const uint16_t __attribute__((address_space(1))) *)p;
+}
 
 // binary16 bits -> f32 (exact for every encoding; v_cvt_f32_f16).
 __device__ __forceinline__ float mh_f16(uint16_t h) {

@@ -458,6 +458,7 @@ int resolve_layer(const mh_moe_layer *L, DevLayer *out) {
 struct mh_stack {
     std::vector<mh::DevLayer> layers;
     int max_batch;
+    mh::StepPlan *plan = nullptr;   // one-launch batch-1 path (null/ineligible -> per-layer launches)
 };
 
 using namespace mh;
@@ -598,6 +599,12 @@ int mh_stack_create(const mh_moe_layer *layers, int n_layers, int max_batch, mh_
             return fail(MH_E_ARG, "mh_stack_create: layer %d shape differs from layer 0", i);
         }
     }
+    int rc = step_plan_create(st->layers.data(), n_layers, &st->plan);
+    if (rc) {
+        step_plan_destroy(st->plan);
+        delete st;
+        return rc;
+    }
     *out = st;
     return MH_OK;
 }
@@ -614,9 +621,15 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
     if (sel) MH_TRY(resolve_dev(sel, (uint64_t)nl * batch * k * 4, "mh_stack_decode sel"));
     if (w) MH_TRY(resolve_dev(w, (uint64_t)nl * batch * k * 4, "mh_stack_decode w"));
     if (usage) MH_TRY(resolve_dev(usage, (uint64_t)nl * L0.n_experts * 4, "mh_stack_decode usage"));
+    hipStream_t s = stream();
+    const char *nf = getenv("MIDGE_HIP_NO_FUSED");   // per call, so callers can A/B the two paths
+    if (batch == 1 && !(nf && *nf && *nf != '0') && step_plan_ok(st->plan)) {
+        int rc = step_run(st->plan, st->layers.data(), nl, x, sel, w, usage, s);
+        if (rc != MH_E_UNSUPPORTED) return rc;
+        clear_error();   // shape this device cannot run in one launch: per-layer launches below
+    }
     LayerBufs b;
     MH_TRY(layer_bufs(L0, batch, &b));
-    hipStream_t s = stream();
     for (int l = 0; l < nl; l++) {
         LayerBufs bl = b;
         if (sel) bl.sel = sel + (size_t)l * batch * k;
@@ -629,6 +642,10 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
 
 int mh_stack_destroy(mh_stack *st) {
     clear_error();
+    if (st) {
+        if (st->plan) (void)hipStreamSynchronize(stream());
+        step_plan_destroy(st->plan);
+    }
     delete st;
     return MH_OK;
 }

@@ -38,6 +38,9 @@ struct State {
 
 State g;
 
+// Host-mapped error flags of asynchronous work (checked by mh_sync).
+std::vector<std::pair<unsigned *, const char *>> g_async;
+
 // Kernel timing records (mh_profile_*).
 struct ProfRec {
     const char *name;
@@ -80,6 +83,16 @@ int fail(int code, const char *fmt, ...) {
 
 void clear_error() { g_err[0] = 0; }
 
+void watch_async_error(unsigned *flag, const char *msg) { g_async.push_back({flag, msg}); }
+
+void unwatch_async_error(unsigned *flag) {
+    for (size_t i = 0; i < g_async.size(); i++)
+        if (g_async[i].first == flag) {
+            g_async.erase(g_async.begin() + (long)i);
+            return;
+        }
+}
+
 bool profiling() { return g_prof; }
 
 void prof_begin(const char *name, hipStream_t s) {
@@ -94,6 +107,12 @@ void prof_begin(const char *name, hipStream_t s) {
 
 void prof_end(hipStream_t s) {
     if (!g_prof_pending.empty() && g_prof_pending.back().stop) (void)hipEventRecord(g_prof_pending.back().stop, s);
+}
+
+void prof_add(const char *name, double ms) {
+    auto &acc = g_prof_done[name];
+    acc.first += ms;
+    acc.second += 1;
 }
 
 static int prof_collect() {
@@ -344,6 +363,11 @@ int mh_sync(void) {
     clear_error();
     MH_TRY(require_init());
     MH_HIP(hipStreamSynchronize(g.cur));
+    for (auto &a : g_async)
+        if (*(volatile unsigned *)a.first) {
+            *(volatile unsigned *)a.first = 0;
+            return fail(MH_E_HIP, "%s", a.second);
+        }
     return MH_OK;
 }
 

@@ -225,3 +225,53 @@ def test_stack_chain_vs_oracle(mh):
         d.free()
     for lay in layers:
         lay.release()
+
+
+@pytest.mark.parametrize("shape,layers", [
+    (MoEShape(hidden=256, ffn=192, n_experts=16, top_k=4), 5),
+    (MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4), 3),
+])
+def test_stack_fused_step_vs_per_layer_and_oracle(mh, shape, layers):
+    """Batch-1 stack decode runs as one cooperative launch; it must route
+    exactly as the per-layer launches and the oracle do, and agree on x."""
+    import os
+    say(f"fused step {shape.hidden}x{shape.ffn} E={shape.n_experts} layers={layers}")
+    keys = Keys(77)
+    lays, structs = [], []
+    for l in range(layers):
+        ex = synth.host_layer_experts(shape, keys, l)
+        w, s, b, nw = synth.host_router(shape, keys, l)
+        lays.append(MoELayer.host(shape, ex, w, s, b, nw))
+        _LIVE.append(lays[-1])
+        structs.append((po.layer_struct(shape, ex, w, s, b, nw), (ex, w, s, b, nw)))
+    st = Stack(lays, max_batch=1)
+    k = shape.top_k
+    for step in range(3):
+        x0 = synth.host_x(shape, keys, 1, step=step)
+        out = {}
+        for mode in ("fused", "per_layer"):
+            if mode == "per_layer":
+                os.environ["MIDGE_HIP_NO_FUSED"] = "1"
+            try:
+                xd = DevBuf.from_array(x0)
+                sd = DevBuf(layers * k * 4)
+                ud = DevBuf.from_array(np.zeros((layers, shape.n_experts), np.uint32))
+                st.decode(xd, 1, sd, None, ud)
+                mh.sync()
+                out[mode] = (xd.download(np.float32, x0.shape)[0], sd.download(np.int32, (layers, k)),
+                             ud.download(np.uint32, (layers, shape.n_experts)))
+                for d in (xd, sd, ud):
+                    d.free()
+            finally:
+                os.environ.pop("MIDGE_HIP_NO_FUSED", None)
+        xf, sf, uf = out["fused"]
+        xp, sp, up = out["per_layer"]
+        assert (sf == sp).all(), (sf, sp)
+        assert (uf == up).all()
+        assert rel_l2(xf, xp) < 1e-5
+        x = x0[0]
+        for l in range(layers):
+            x, selr, _ = po.moe_decode(structs[l][0], x)
+            assert (sf[l] == selr).all(), (l, sf[l], selr)
+        assert rel_l2(xf, x) < TOL
+    st.destroy()

@@ -32,11 +32,13 @@ def stack(mh):
         b.free()
 
 
-# Router logits here are ~N(0, 20^2); the GPU and the oracle sum them in
-# different orders (and inherit different f32 rounding from earlier layers),
-# a few 1e-4 apart. Two experts whose oracle logits are closer than this are
-# a near-tie: either order is a faithful result, and the trajectories differ
-# from there on.
+# Router logits here are ~N(0, 20^2) sums of 2880 int8 x f32 products with a
+# condition number of ~40, so the ~1e-5 relative drift that f32
+# reassociation leaves in the residual after a dozen chained layers moves
+# them by ~4e-4 relative. Two experts whose oracle logits are closer than
+# TIE (relative) are a near-tie: either order is faithful, and the chained
+# trajectories differ from there on. The teacher-forced test below removes
+# the chaining and requires identical experts at every layer.
 TIE = 1e-3
 
 
@@ -58,7 +60,7 @@ def oracle_chain(keys, x: np.ndarray, routed: np.ndarray):
             pos = [i for i in range(SHAPE.top_k) if sel[0][i] != routed[l][i]]
             involved = sorted(set(a.tolist()) | {int(sel[0][i]) for i in pos} | {int(routed[l][i]) for i in pos})
             vals = np.sort(rl[involved])
-            gap = float(np.min(np.diff(vals))) if len(vals) > 1 else 0.0
+            gap = float(np.min(np.diff(vals))) / float(np.max(np.abs(vals))) if len(vals) > 1 else 0.0
             return x, l, {"layer": l, "oracle": sel[0].tolist(), "gpu": routed[l].tolist(),
                           "logits": {int(e): float(rl[e]) for e in involved}, "gap": gap}
         need = sorted(set(sel[0].tolist()))
@@ -109,9 +111,50 @@ def test_stack_decode_vs_oracle(stack, batch, check, calls):
             say(f"oracle chain token {t} of batch {batch} call {call}")
             xr, matched, tie = oracle_chain(keys, X[t].copy(), sel[:, t])
             if tie is None:
-                assert rel_l2(got[t], xr) < 1e-4
+                assert rel_l2(got[t], xr) < 1e-3   # 36 chained layers; the bar is 1e-3
                 full += 1
             else:
                 print(f"[near-tie] token {t}: {tie}", flush=True)
                 assert tie["gap"] < TIE, f"routing differs beyond a near-tie: {tie}"
     assert full >= 1, "every checked token hit a near-tie; no full 36-layer comparison was made"
+
+
+def test_teacher_forced_every_layer(stack):
+    """Layer by layer at full size: the GPU's moe() on the oracle's own input
+    for that layer must pick the same experts (same order) and produce the
+    same residual within 1e-4 relative L2."""
+    from midge_amd.moe import moe_dev
+    st, keys, bufs = stack
+    L = SHAPE.layout
+    table = np.zeros(L.layer_stride, np.uint8)
+    lib = po.oracle()
+    bias_c = float(synth.normal_c(synth.EXPERT_BIAS_STD))
+    x = synth.host_x(SHAPE, keys, 1, step=4242)[0]
+    xd = DevBuf(SHAPE.hidden * 4)
+    sd, wd = DevBuf(SHAPE.top_k * 4), DevBuf(SHAPE.top_k * 4)
+    worst = 0.0
+    for l in range(SHAPE.n_layers):
+        say(f"teacher-forced layer {l}")
+        w, s, b, nw = synth.host_router(SHAPE, keys, l)
+        Ls = po.layer_struct(SHAPE, table, w, s, b, nw)
+        _, sel, _ = po.route_batch(Ls, x[None, :])
+
+        def gen(e):
+            dst = table[e * L.expert_stride:(e + 1) * L.expert_stride]
+            return lib.mo_synth_expert(dst.ctypes.data, SHAPE.expert_dt, SHAPE.hidden, SHAPE.ffn,
+                                       SHAPE.n_experts, l, e, keys.table, synth.EXPERT_EMIN,
+                                       synth.EXPERT_EMAX, bias_c)
+        with ThreadPoolExecutor(8) as pool:
+            assert all(rc == 0 for rc in pool.map(gen, sorted(set(sel[0].tolist()))))
+        xd.upload(x)
+        moe_dev(st.layers[l], xd, 1, sd, wd)
+        got = xd.download(np.float32, SHAPE.hidden)
+        gsel = sd.download(np.int32, SHAPE.top_k)
+        x, osel, _ = po.moe_decode(Ls, x)
+        assert (gsel == osel).all(), (l, gsel, osel)
+        err = rel_l2(got, x)
+        worst = max(worst, err)
+        assert err < 1e-4, (l, err)
+    print(f"teacher-forced worst rel L2 {worst:.2e}", flush=True)
+    for d in (xd, sd, wd):
+        d.free()
