@@ -156,10 +156,11 @@ def run_gpu(args, shape):
         st.decode(xs.ptr + i * args.batch * shape.hidden * 4, args.batch)
     midge_amd.sync()
     kern = {}
-    phases = tuple("decode_step/" + n for n in (
-        "router", "barrier1", "gate_up", "gu_topk", "gu_issue", "gu_math", "gu_reduce", "gu_epilogue",
-        "barrier2_arrive_prefetch", "barrier2_wait", "down_combine", "dn_hload", "dn_math", "dn_reduce",
-        "dn_combine", "barrier3"))
+    # per-layer phase spans of the one-launch step: mean over blocks, and the slowest block
+    spans = ("layer", "router", "barrier1", "gate_up", "gu_topk", "gu_issue", "gu_math", "gu_reduce",
+             "gu_epilogue", "barrier2_arrive_prefetch", "barrier2_wait", "down_combine", "dn_hload", "dn_math",
+             "dn_reduce", "dn_combine", "barrier3")
+    phases = tuple(f"decode_step/{n}{m}" for n in spans for m in ("", ".max"))
     for name in ("decode_step", "expert_gu", "expert_down", "gemv", "topk", "rmsnorm", "combine_decode") + phases:
         tot, n = profile_query(name)
         if n:

@@ -54,31 +54,71 @@ struct StepArgs {
     unsigned *go;            // barrier release word (written by block 0)
     unsigned seq0;           // sequence number of this launch's first barrier
     unsigned *err;
-    unsigned long long *trace;   // [L][16] phase timestamps of block 0, or null
+    unsigned long long *trace;   // [L][16][gridDim.x] per-block phase timestamps, or null
+    int res_floats;              // LDS floats of the reduced-rows area
     int red_floats;              // LDS floats of the partial-sum area
 };
 
 namespace {
 
 constexpr int kThreads = 512;   // 8 waves: 2 per SIMD, up to 256 VGPRs each
-constexpr int kUB = 12;         // gate/up row iterations in flight per thread
-constexpr int kUC = 12;         // down row iterations in flight per thread
+constexpr int kUP = 9;          // gate/up row pairs in flight per thread
+constexpr int kUC = 12;         // down rows in flight per thread
+constexpr int kNX = 8;          // x elements per thread in the router phase (H <= kNX * kThreads)
 constexpr unsigned kSpinLimit = 1u << 20;
 
+// Memory access. Every load goes through a buffer resource (32-bit offsets,
+// out-of-range reads return 0). Weights are streamed with the nontemporal
+// hint. Data that blocks exchange inside the launch (x, logits, h) is
+// written with device-scope stores and read with device-scope loads, which
+// are coherent across the XCDs' L2 caches: the barriers then need no L2
+// write-back or invalidate, and read-only weights stay cached.
+constexpr int kNT = 2;     // cache-policy bits: nontemporal
+constexpr int kDev = 16;   // cache-policy bits: device scope
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ mh_u4 ld_w16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT);
+}
+__device__ __forceinline__ uint32_t ld_w2(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kNT);
+}
+__device__ __forceinline__ float ld_f(rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ float ld_dev(rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kDev));
+}
+__device__ __forceinline__ mh_u4 ld_dev16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kDev);
+}
+__device__ __forceinline__ void st_dev(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// An opaque copy of v: values derived from it are recomputed where they are
+// used instead of being hoisted out of the layer loop and held in registers
+// (or spilled) across every phase.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// Arrive: every wave's stores have completed (device-scope stores complete
+// at the device coherence point), then thread 0 publishes `seq`.
 __device__ __forceinline__ void bar_arrive(unsigned *flags, unsigned seq) {
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's stores have landed
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __hip_atomic_store(&flags[blockIdx.x], seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (threadIdx.x == 0) __hip_atomic_store(&flags[blockIdx.x], seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Gather/broadcast wait: block 0's first wave polls every block's flag (one
-// vector load per lane per round) and then publishes `seq` in *go; every
-// other block polls that single word. A few hundred loads per round in
-// total, instead of every block sweeping every flag. Returns false (in every
-// thread) if the barrier timed out.
+// load per lane per round) and then publishes `seq` in *go; every other
+// block polls that single word. Returns false (in every thread) if the
+// barrier timed out. Loads after the wait are issued only once it has
+// returned, so device-scope loads see every store made before the arrives.
 __device__ __forceinline__ bool bar_wait(const unsigned *flags, unsigned *go, unsigned seq, unsigned *err,
                                          int *s_ok) {
     if (threadIdx.x < 64) {
@@ -99,7 +139,6 @@ __device__ __forceinline__ bool bar_wait(const unsigned *flags, unsigned *go, un
                     break;
                 }
             }
-            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent");
             if (ok && lane == 0) __hip_atomic_store(go, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else if (lane == 0) {
             while ((int)(__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - seq) < 0) {
@@ -110,7 +149,6 @@ __device__ __forceinline__ bool bar_wait(const unsigned *flags, unsigned *go, un
                 }
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         if (lane == 0) {
             *s_ok = ok ? 1 : 0;
             if (!ok) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -195,26 +233,30 @@ __device__ __forceinline__ float act_fn(float g, float u, float alpha, float lim
     return a * (u + 1.0f);
 }
 
-// Phase A's inputs that do not depend on x, loaded ahead of time: this
-// block's first router-row chunk and the first kNW norm weights per thread
-// (for layer 0 at kernel start, for layer l + 1 before layer l's last wait).
-constexpr int kNW = 4;
+// Phase A's inputs that do not depend on x, loaded ahead of time (for layer
+// 0 at kernel start, for layer l + 1 between layer l's last arrive and
+// wait): this block's first router row chunk, that row's scale and bias, and
+// the norm weights of this thread's x elements.
 struct RouterPref {
     mh_u4 rq;
-    float nw[kNW];
+    float rs, rb;
+    float nw[kNX];
 };
 
+template <int RDT>
 __device__ __forceinline__ RouterPref prefetch_router(const StepArgs &A, int l, int CR) {
     RouterPref p;
     const StepLayer Lp = A.layers[l];
     const int b = blockIdx.x, t = threadIdx.x;
-    p.rq = mh_u4{0u, 0u, 0u, 0u};
-    if (b < A.E && t < CR) p.rq = mh_load16(mh_global(Lp.router_w + (size_t)b * CR * 16 + (size_t)t * 16));
+    const int e = b < A.E ? b : 0;
+    const rsrc_t rw = make_rsrc(Lp.router_w, (uint32_t)A.E * (uint32_t)CR * 16u);
+    p.rq = ld_w16(rw, (uint32_t)(e * CR + min(t, CR - 1)) * 16u);
+    p.rs = 1.0f;
+    if constexpr (RDT == MH_DT_Q8R) p.rs = ld_f(make_rsrc(Lp.router_s, (uint32_t)A.E * 4u), (uint32_t)e * 4u);
+    p.rb = ld_f(make_rsrc(Lp.router_b, (uint32_t)A.E * 4u), (uint32_t)e * 4u);
+    const rsrc_t rn = make_rsrc(Lp.norm_w, (uint32_t)A.H * 4u);
 #pragma unroll
-    for (int k = 0; k < kNW; ++k) {
-        const int i = t + k * (int)blockDim.x;
-        p.nw[k] = i < A.H ? *(const float __attribute__((address_space(1))) *)mh_global(Lp.norm_w + i) : 0.f;
-    }
+    for (int k = 0; k < kNX; ++k) p.nw[k] = ld_f(rn, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
     return p;
 }
 
@@ -232,162 +274,178 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
     float *xs = lds;             // x at layer start
     float *xbs = xs + H;         // rmsnorm(x) * w
     float *res = xbs + H;        // reduced rows / staged logits
-    const int res_floats = max(max(E, 2 * K * F / (int)gridDim.x + 2), K * ((H + gridDim.x - 1) / gridDim.x)) + 64;
-    float *red = res + res_floats;
+    float *red = res + A.res_floats;
     float *bds = red + A.red_floats;   // [K][rows of this block's down slice]
     const int NB = gridDim.x, b = blockIdx.x, t = threadIdx.x;
-    const int nw = blockDim.x >> 6, wave = t >> 6, lane = t & 63;
+    const int wave = t >> 6;
     unsigned seq = A.seq0;
 
-    unsigned long long *tr = (A.trace && b == 0 && t == 0) ? A.trace : nullptr;
-    // Phase A's inputs that do not depend on x are loaded ahead: this
-    // block's first router row chunk and the first kNW norm weights of each
-    // thread, for layer 0 here and for layer l + 1 before layer l's last
-    // barrier wait.
-    const int CR = H / RE;                 // router chunks per row
-    RouterPref pf = prefetch_router(A, 0, CR);
+    // per-block phase timestamps (100 MHz), written by thread 0 while profiling
+    unsigned long long *tr = (A.trace && t == 0) ? A.trace + b : nullptr;
+#define MH_STAMP(ph) \
+    if (tr) tr[(size_t)(l * 16 + (ph)) * NB] = wall_clock64()
+
+    const rsrc_t rx = make_rsrc(A.x, (uint32_t)H * 4u);
+    const rsrc_t rlg = make_rsrc(A.logits, (uint32_t)E * 4u);
+    const rsrc_t rh = make_rsrc(A.h, (uint32_t)K * (uint32_t)F * 4u);
+    const uint32_t layer_bytes = (uint32_t)((uint64_t)E * A.stride - 1u) + 1u;   // < 4 GiB (plan check)
+    const int CR = H / RE;   // router chunks per row
+    RouterPref pf = prefetch_router<RDT>(A, 0, CR);
     for (int l = 0; l < A.n_layers; ++l) {
         const StepLayer Ly = A.layers[l];
-        if (tr) tr[l * 16 + 0] = wall_clock64();
+        MH_STAMP(0);
         // ------------------------------------------------ A: router
-        float ss = 0.f;
-        for (int i = t; i < H; i += blockDim.x) {
-            const float v = A.x[i];
-            xs[i] = v;
-            ss = __builtin_fmaf(v, v, ss);
-        }
-        ss = block_sum(ss, s_part);
-        const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+        {
+            float xv[kNX];
+            float ss = 0.f;
 #pragma unroll
-        for (int k = 0; k < kNW; ++k) {
-            const int i = t + k * (int)blockDim.x;
-            if (i < H) xbs[i] = xs[i] * inv * pf.nw[k];
+            for (int k = 0; k < kNX; ++k) {
+                xv[k] = ld_dev(rx, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
+                ss = __builtin_fmaf(xv[k], xv[k], ss);
+            }
+            ss = block_sum(ss, s_part);
+            const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+#pragma unroll
+            for (int k = 0; k < kNX; ++k) {
+                const int i = t + k * kThreads;
+                if (i < H) {
+                    xs[i] = xv[k];
+                    xbs[i] = xv[k] * inv * pf.nw[k];
+                }
+            }
         }
-        for (int i = t + kNW * (int)blockDim.x; i < H; i += blockDim.x) xbs[i] = xs[i] * inv * Ly.norm_w[i];
         __syncthreads();
         for (int e = b; e < E; e += NB) {
             float p = 0.f;
-            for (int c = t; c < CR; c += blockDim.x) {
-                const mh_u4 q = (e == (int)blockIdx.x && c == t) ? pf.rq
-                                                   : mh_load16(mh_global(Ly.router_w + (size_t)e * CR * 16 + (size_t)c * 16));
+            float rs = pf.rs, rb = pf.rb;
+            const rsrc_t rw = make_rsrc(Ly.router_w, (uint32_t)E * (uint32_t)CR * 16u);
+            for (int c = t; c < CR; c += kThreads) {
+                const mh_u4 q = (e == b && c == t) ? pf.rq : ld_w16(rw, (uint32_t)(e * CR + c) * 16u);
                 p += mh_dot_chunk<RDT>(q, xbs + (size_t)c * RE);
             }
             p = block_sum(p, s_part);
+            if (e != b) {
+                if constexpr (RDT == MH_DT_Q8R) rs = Ly.router_s[e];
+                rb = Ly.router_b[e];
+            }
             if (t == 0) {
-                if constexpr (RDT == MH_DT_Q8R) p *= Ly.router_s[e];
-                A.logits[e] = p + Ly.router_b[e];
+                if constexpr (RDT == MH_DT_Q8R) p *= rs;
+                st_dev(A.logits + e, p + rb);
             }
         }
-        if (tr) tr[l * 16 + 1] = wall_clock64();
+        MH_STAMP(1);
         bar_arrive(A.flags, seq);
         if (!bar_wait(A.flags, A.go, seq, A.err, &s_ok)) return;
         ++seq;
-        if (tr) tr[l * 16 + 2] = wall_clock64();
+        MH_STAMP(2);
 
         // ------------------------------------------------ B: gate/up
-        for (int e = t; e < E; e += blockDim.x) res[e] = A.logits[e];
+        for (int e = t; e < E; e += kThreads) res[e] = ld_dev(rlg, (uint32_t)e * 4u);
         __syncthreads();
         if (wave == 0) wave_topk(res, E, K, A.router_norm, s_sel, s_val, s_w);
         __syncthreads();
-        if (tr) tr[l * 16 + 8] = wall_clock64();
+        MH_STAMP(8);
         if (b == 0 && t < K) {
             if (A.sel) A.sel[(size_t)l * K + t] = s_sel[t];
             if (A.w) A.w[(size_t)l * K + t] = s_w[t];
-            if (A.usage && s_sel[t] >= 0) A.usage[(size_t)l * E + s_sel[t]] += 1u;
+            if (A.usage && s_sel[t] >= 0)
+                __hip_atomic_fetch_add(&A.usage[(size_t)l * E + s_sel[t]], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         }
+        const rsrc_t rex = make_rsrc(Ly.experts, layer_bytes);
         {
+            // Rows come in (gate, up) pairs: pair p of the k experts laid end
+            // to end is row p % F of expert p / F. The block takes pairs
+            // [p_begin, p_begin + np); they span at most two experts (np <= F,
+            // plan check): expert ia from row rb, then ia + 1.
             const int C = A.CH;
-            const int ns = blockDim.x / C;
-            const int slot = t / C, c = t - slot * C;
+            const int ns = kThreads / C;
+            const int tt = opaque(t);
+            const int slot = tt / C, c = tt - slot * C;
             const bool active = slot < ns;
-            const int TB = 2 * K * F;
-            int RB = (TB + NB - 1) / NB;
-            RB += RB & 1;
-            const int f_begin = b * RB;
-            const int nf = max(0, min(TB, f_begin + RB) - f_begin);
-            float xr[XE];
-#pragma unroll
-            for (int j = 0; j < XE; ++j) xr[j] = active ? xbs[c * XE + j] : 0.f;
-            // The block's pairs [pb, pb + nf/2) span at most two experts
-            // (nf/2 <= F, checked at plan creation): expert ia from row rb,
-            // then ia + 1.
-            const int pb = f_begin >> 1;
-            const int ia = min(pb / F, K - 1), rb = pb - ia * F;
+            const int PB = (K * F + NB - 1) / NB;
+            const int p_begin = b * PB;
+            const int np = max(0, min(K * F, p_begin + PB) - p_begin);
+            const int ia = min(p_begin / F, K - 1), rb = p_begin - ia * F;
             const int e_a = s_sel[ia], e_b = ia + 1 < K ? s_sel[ia + 1] : -1;
             const uint32_t eo_a = e_a >= 0 ? (uint32_t)e_a * (uint32_t)A.stride : 0u;
             const uint32_t eo_b = e_b >= 0 ? (uint32_t)e_b * (uint32_t)A.stride : 0u;
             const uint32_t od0 = (uint32_t)A.off[0], od1 = (uint32_t)A.off[3];
             const uint32_t os0 = (uint32_t)A.off[1], os1 = (uint32_t)A.off[4];
+            float xr[XE];
+#pragma unroll
+            for (int j = 0; j < XE; ++j) xr[j] = active ? xbs[c * XE + j] : 0.f;
+            // this thread's epilogue pair's biases, loaded with the weights
             float bg_pref = 0.f, bu_pref = 0.f;
-            for (int f0 = 0; f0 < nf; f0 += ns * kUB) {
-                // Branch-free loads (see block_gemv): a past-the-end row, an
-                // idle slot or an unfilled routing slot re-reads the block's
-                // last row and is masked out in the math; scale bits stay raw
-                // until every load is in flight.
-                mh_u4 q[kUB];
-                uint32_t sb[kUB];
+            {
+                const int pr = rb + min(t, max(np - 1, 0));
+                const bool second = pr >= F;
+                const uint32_t eo = second ? eo_b : eo_a;
+                const uint32_t r4 = (uint32_t)(second ? pr - F : pr) * 4u;
+                bg_pref = ld_f(rex, eo + (uint32_t)A.off[2] + r4);
+                bu_pref = ld_f(rex, eo + (uint32_t)A.off[5] + r4);
+            }
+            for (int p0 = 0; p0 < np; p0 += ns * kUP) {
+                // Branch-free loads: a past-the-end pair or an idle slot
+                // re-reads the block's last pair and is masked out in the
+                // math; scale bits stay raw until every load is in flight.
+                mh_u4 qg[kUP], qu[kUP];
+                uint32_t sg[kUP], su[kUP];
                 const int sl = active ? slot : ns - 1;
-                const mh_gbytes ex = mh_global(Ly.experts);
-                if (f0 == 0) {   // this thread's epilogue pair's biases, loaded with the weights
-                    const int pp = min(t, max(nf / 2 - 1, 0));
-                    const int pr = rb + pp;
+#pragma unroll
+                for (int u = 0; u < kUP; ++u) {
+                    const int pr = rb + min(p0 + u * ns + sl, np - 1);
                     const bool second = pr >= F;
                     const uint32_t eo = second ? eo_b : eo_a;
-                    const uint32_t r4 = (uint32_t)(second ? pr - F : pr) * 4u;
-                    bg_pref = *(const float __attribute__((address_space(1))) *)(ex + (eo + (uint32_t)A.off[2] + r4));
-                    bu_pref = *(const float __attribute__((address_space(1))) *)(ex + (eo + (uint32_t)A.off[5] + r4));
-                }
-#pragma unroll
-                for (int u = 0; u < kUB; ++u) {
-                    const int f = min(f0 + u * ns + sl, nf - 1);
-                    const int m = f & 1, pr = rb + (f >> 1);
-                    const bool second = pr >= F;
-                    const int r = second ? pr - F : pr;
-                    const uint32_t eo = second ? eo_b : eo_a;   // offsets fit 32 bits (plan check)
-                    const uint32_t rc = (uint32_t)(r * C + c);
-                    q[u] = mh_load16(ex + (eo + (m ? od1 : od0) + rc * 16u));
-                    sb[u] = mh_load_u16(ex + (eo + (m ? os1 : os0) + rc * 2u));
+                    const uint32_t rc = (uint32_t)((second ? pr - F : pr) * C + c);
+                    qg[u] = ld_w16(rex, eo + od0 + rc * 16u);
+                    qu[u] = ld_w16(rex, eo + od1 + rc * 16u);
+                    sg[u] = ld_w2(rex, eo + os0 + rc * 2u);
+                    su[u] = ld_w2(rex, eo + os1 + rc * 2u);
                 }
                 __builtin_amdgcn_sched_barrier(0);   // all loads issued before any math
-                if (tr && f0 == 0) tr[l * 16 + 9] = wall_clock64();
+                if (p0 == 0) MH_STAMP(9);
 #pragma unroll
-                for (int u = 0; u < kUB; ++u) {
-                    const int f = f0 + u * ns + slot;
-                    const bool valid = active && f < nf && (rb + (f >> 1) >= F ? e_b : e_a) >= 0;
-                    const float p = mh_dot_chunk<XDT>(q[u], xr) * (valid ? mh_f16((uint16_t)sb[u]) : 0.f);
-                    if (active && f < nf) red[(u * ns + slot) * C + c] = p;
-                    __builtin_amdgcn_sched_barrier(0);   // one chunk's math at a time
+                for (int u = 0; u < kUP; ++u) {
+                    const int pp = p0 + u * ns + slot;
+                    const bool inr = active && pp < np;
+                    const bool valid = inr && (rb + pp >= F ? e_b : e_a) >= 0;
+                    const float g = mh_dot_chunk<XDT>(qg[u], xr) * (valid ? mh_f16((uint16_t)sg[u]) : 0.f);
+                    const float v = mh_dot_chunk<XDT>(qu[u], xr) * (valid ? mh_f16((uint16_t)su[u]) : 0.f);
+                    if (inr) {
+                        red[(2 * (u * ns + slot)) * C + c] = g;
+                        red[(2 * (u * ns + slot) + 1) * C + c] = v;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);   // one pair's math at a time
                 }
-                if (tr && f0 == 0) tr[l * 16 + 10] = wall_clock64();
+                if (p0 == 0) MH_STAMP(10);
                 __syncthreads();
-                const int items = min(ns * kUB, nf - f0);
-                block_reduce_rows(red, C, items, res + f0, [](int) { return true; });
+                const int items = min(ns * kUP, np - p0);
+                block_reduce_rows(red, C, 2 * items, res + 2 * p0, [](int) { return true; });
                 __syncthreads();
-                if (tr && f0 == 0) tr[l * 16 + 11] = wall_clock64();
+                if (p0 == 0) MH_STAMP(11);
             }
-            // epilogue: pairs (gate, up) -> h (nf / 2 <= F < blockDim.x pairs: one per thread)
-            if (t < nf / 2) {
-                const int pp = t;
-                const int pr = rb + pp;
+            // epilogue: pair t -> h (np <= F <= kThreads pairs: one per thread)
+            if (t < np) {
+                const int pr = rb + t;
                 const bool second = pr >= F;
-                const int r = second ? pr - F : pr;
-                const int i = second ? ia + 1 : ia;
                 const int e = second ? e_b : e_a;
                 float hv = 0.f;
-                if (e >= 0) hv = act_fn(res[2 * pp] + bg_pref, res[2 * pp + 1] + bu_pref, A.alpha, A.limit, A.act_plain);
-                A.h[(size_t)i * F + r] = hv;
+                if (e >= 0) hv = act_fn(res[2 * t] + bg_pref, res[2 * t + 1] + bu_pref, A.alpha, A.limit, A.act_plain);
+                st_dev(A.h + (size_t)(second ? ia + 1 : ia) * F + (second ? pr - F : pr), hv);
             }
         }
-        if (tr) tr[l * 16 + 3] = wall_clock64();
+        MH_STAMP(3);
         bar_arrive(A.flags, seq);
 
         // ------------------------------------------------ C: down + combine
         {
-            // one pass (checked at plan creation): slot -> (expert i, row
-            // phase sub), rows j = sub + spe * u of this block's slice
+            // one pass (plan check): slot -> (expert i, row phase sub), rows
+            // j = sub + spe * u of this block's slice
             const int C = A.CF;
-            const int nsC = blockDim.x / C;
-            const int slot = t / C, c = t - slot * C;
+            const int nsC = kThreads / C;
+            const int tt = opaque(t);
+            const int slot = tt / C, c = tt - slot * C;
             const int RC = (H + NB - 1) / NB;
             const int r_begin = b * RC;
             const int nr = max(0, min(H, r_begin + RC) - r_begin);
@@ -399,37 +457,43 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             // expert's rows (cache hits) and are masked out
             const int ea = e >= 0 ? e : max(s_sel[0], 0);
             const uint32_t eo = (uint32_t)ea * (uint32_t)A.stride;
-            // branch-free prefetch (see phase B): out-of-range rows re-read
-            // the slice's first row of expert 0's slot and are masked out
             mh_u4 q[kUC];
             uint32_t sb[kUC];
-            const mh_gbytes ex = mh_global(Ly.experts);
-            const uint32_t rows_ok = nr > 0 ? (uint32_t)nr : 1u;
+            const int rows_ok = nr > 0 ? nr : 1;
+            const int r0 = min(r_begin, H - 1);
 #pragma unroll
             for (int u = 0; u < kUC; ++u) {
-                const int j = min(sub + spe * u, (int)rows_ok - 1);
-                const uint32_t rc = (uint32_t)((min(r_begin, H - 1) + j) * C + c);
-                q[u] = mh_load16(ex + (eo + (uint32_t)A.off[6] + rc * 16u));
-                sb[u] = mh_load_u16(ex + (eo + (uint32_t)A.off[7] + rc * 2u));
+                const int j = min(sub + spe * u, rows_ok - 1);
+                const uint32_t rc = (uint32_t)((r0 + j) * C + c);
+                q[u] = ld_w16(rex, eo + (uint32_t)A.off[6] + rc * 16u);
+                sb[u] = ld_w2(rex, eo + (uint32_t)A.off[7] + rc * 2u);
             }
-            // the down biases of this block's rows, (expert i, row j) -> thread i * nr + j
+            // the down biases of this block's rows, (expert ib, row jb) -> thread ib * nr + jb
             float bd_pref = 0.f;
             if (t < K * nr) {
                 const int ib = t / nr, jb = t - ib * nr;
                 const int eb = s_sel[ib];
                 if (eb >= 0)
-                    bd_pref = *(const float __attribute__((address_space(1))) *)(
-                        ex + ((uint32_t)eb * (uint32_t)A.stride + (uint32_t)A.off[8] + (uint32_t)(r_begin + jb) * 4u));
+                    bd_pref = ld_f(rex, (uint32_t)eb * (uint32_t)A.stride + (uint32_t)A.off[8] + (uint32_t)(r_begin + jb) * 4u);
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (tr) tr[l * 16 + 4] = wall_clock64();
+            MH_STAMP(4);
             if (!bar_wait(A.flags, A.go, seq, A.err, &s_ok)) return;
             ++seq;
-            if (tr) tr[l * 16 + 5] = wall_clock64();
+            MH_STAMP(5);
             float xr[XE];
+            {
+                const uint32_t hb = (uint32_t)((act ? i : 0) * F + c * XE) * 4u;
 #pragma unroll
-            for (int jj = 0; jj < XE; ++jj) xr[jj] = act ? A.h[(size_t)i * F + c * XE + jj] : 0.f;
-            if (tr) tr[l * 16 + 12] = wall_clock64();
+                for (int jj = 0; jj < XE / 4; ++jj) {
+                    const mh_u4 v = ld_dev16(rh, hb + (uint32_t)jj * 16u);
+                    xr[4 * jj + 0] = act ? __uint_as_float(v.x) : 0.f;
+                    xr[4 * jj + 1] = act ? __uint_as_float(v.y) : 0.f;
+                    xr[4 * jj + 2] = act ? __uint_as_float(v.z) : 0.f;
+                    xr[4 * jj + 3] = act ? __uint_as_float(v.w) : 0.f;
+                }
+            }
+            MH_STAMP(12);
 #pragma unroll
             for (int u = 0; u < kUC; ++u) {
                 const int j = sub + spe * u;
@@ -439,13 +503,13 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (t < K * nr) bds[t] = bd_pref;
-            if (tr) tr[l * 16 + 13] = wall_clock64();
+            MH_STAMP(13);
             __syncthreads();
             block_reduce_rows(red, C, K * RC, res, [&](int it) { return it % RC < nr; });
             __syncthreads();
-            if (tr) tr[l * 16 + 14] = wall_clock64();
+            MH_STAMP(14);
             // combine in selection order: moe = sum_i w_i (dot_i + bd_i); x += moe
-            for (int j = t; j < nr; j += blockDim.x) {
+            for (int j = t; j < nr; j += kThreads) {
 #pragma clang fp contract(off)
                 const int r = r_begin + j;
                 float moe = 0.f;
@@ -454,16 +518,17 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                     const float y = res[ii * RC + j] + bds[ii * nr + j];
                     moe = moe + s_w[ii] * y;
                 }
-                A.x[r] = xs[r] + moe;
+                st_dev(A.x + r, xs[r] + moe);
             }
         }
-        if (tr) tr[l * 16 + 6] = wall_clock64();
+        MH_STAMP(6);
         bar_arrive(A.flags, seq);
-        if (l + 1 < A.n_layers) pf = prefetch_router(A, l + 1, CR);
+        if (l + 1 < A.n_layers) pf = prefetch_router<RDT>(A, l + 1, CR);
         if (!bar_wait(A.flags, A.go, seq, A.err, &s_ok)) return;
         ++seq;
-        if (tr) tr[l * 16 + 7] = wall_clock64();
+        MH_STAMP(7);
     }
+#undef MH_STAMP
 }
 
 __global__ void k_fill_u32(unsigned *p, int n, unsigned v) {
@@ -476,7 +541,7 @@ int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
     MH_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     int per_cu = 0;
     MH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, lds));
-    if (per_cu < 1) return fail(MH_E_UNSUPPORTED, "decode step: a 1024-thread block with %zu B LDS does not fit a CU", lds);
+    if (per_cu < 1) return fail(MH_E_UNSUPPORTED, "decode step: a %d-thread block with %zu B LDS does not fit a CU", kThreads, lds);
     StepArgs a = A;
     void *args[] = {&a};
     const bool prof = profiling();
@@ -492,7 +557,7 @@ int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
 struct StepPlan {
     StepLayer *layers = nullptr;   // device [L]
     unsigned *flags = nullptr;     // device [nb + 64]: flags, then the go word on its own line
-    unsigned long long *trace = nullptr;   // device [L][8] (filled while profiling)
+    unsigned long long *trace = nullptr;   // device [L][16][nb] (filled while profiling)
     int n_layers = 0;
     unsigned *err = nullptr;       // host-mapped pinned [1]: set by a timed-out barrier
     unsigned *err_dev = nullptr;   // its device address
@@ -529,17 +594,20 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     if (L0.router.dt != MH_DT_Q8R && L0.router.dt != MH_DT_F32) return reject("router is not q8r or f32");
     const int re = L0.router.dt == MH_DT_Q8R ? 16 : 4;
     if (L0.hidden % re) return reject("router width not a chunk multiple");
-    int nb = device_cus();
-    {   // the down phase runs in one pass: every routed expert gets slots,
-        // and each slot's rows of the block's slice fit kUC iterations
-        const int nsC = kThreads / (int)(L0.ffn / 32);
-        const int spe = L0.top_k > 0 ? nsC / L0.top_k : 0;
-        const int RC = (int)((L0.hidden + nb - 1) / nb);
-        if (spe < 1 || RC > spe * kUC) return reject("down phase does not fit one pass");
-        int RB = (int)((2 * L0.top_k * L0.ffn + nb - 1) / nb);
-        RB += RB & 1;
-        if (RB / 2 > L0.ffn) return reject("a block's gate/up range would span more than two experts");
-        if ((int)(L0.hidden / 32) > kThreads || (int)(L0.hidden / 16) > kThreads) return reject("hidden too wide");
+    const int nb = device_cus();
+    {
+        const int H = (int)L0.hidden, F = (int)L0.ffn, K = L0.top_k;
+        if (H > kNX * kThreads) return reject("hidden exceeds the router phase's per-thread share");
+        // gate/up: a block's pairs span at most two experts and the epilogue
+        // has one pair per thread
+        const int PB = (K * F + nb - 1) / nb;
+        if (PB > F || PB > kThreads) return reject("a block's gate/up pairs span more than two experts");
+        // down: one pass, every routed expert gets slots, each slot's rows of
+        // the block's slice fit kUC iterations, one bias per thread
+        const int nsC = kThreads / (F / 32);
+        const int spe = K > 0 ? nsC / K : 0;
+        const int RC = (H + nb - 1) / nb;
+        if (spe < 1 || RC > spe * kUC || K * RC > kThreads) return reject("down phase does not fit one pass");
     }
     std::vector<StepLayer> host((size_t)n_layers);
     for (int l = 0; l < n_layers; l++) {
@@ -549,7 +617,7 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     MH_HIP(hipMalloc(&p->layers, sizeof(StepLayer) * (size_t)n_layers));
     MH_HIP(hipMemcpy(p->layers, host.data(), sizeof(StepLayer) * (size_t)n_layers, hipMemcpyHostToDevice));
     MH_HIP(hipMalloc(&p->flags, sizeof(unsigned) * (size_t)(nb + 64)));
-    MH_HIP(hipMalloc(&p->trace, sizeof(unsigned long long) * 16 * (size_t)n_layers));
+    MH_HIP(hipMalloc(&p->trace, sizeof(unsigned long long) * 16 * (size_t)n_layers * (size_t)nb));
     p->n_layers = n_layers;
     MH_HIP(hipHostMalloc((void **)&p->err, sizeof(unsigned), hipHostMallocMapped));
     *p->err = 0;
@@ -616,13 +684,11 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     A.seq0 = p->seq;
     p->seq += nbar;
     const int nb = p->nb;
-    const int res_floats = std::max(std::max(A.E, 2 * A.K * A.F / nb + 2), A.K * ((A.H + nb - 1) / nb)) + 64;
-    const int nsB = kThreads / A.CH, nsC = kThreads / A.CF;
-    const size_t red_floats = std::max((size_t)nsB * kUB * A.CH,
-                                       (size_t)std::min(A.K, nsC) * (size_t)((A.H + nb - 1) / nb) * A.CF);
-    A.red_floats = (int)red_floats;
-    const size_t lds = ((size_t)2 * A.H + res_floats + red_floats + (size_t)A.K * ((A.H + nb - 1) / nb)) *
-                       sizeof(float);
+    const int PB = (A.K * A.F + nb - 1) / nb, RC = (A.H + nb - 1) / nb;
+    A.res_floats = std::max(std::max(A.E, 2 * PB), A.K * RC) + 64;
+    const int nsB = kThreads / A.CH;
+    A.red_floats = std::max(2 * nsB * kUP * A.CH, A.K * RC * A.CF);
+    const size_t lds = ((size_t)2 * A.H + A.res_floats + A.red_floats + (size_t)A.K * RC) * sizeof(float);
     if (lds > 160 * 1024) return fail(MH_E_UNSUPPORTED, "decode step needs %zu B of LDS", lds);
     int rc;
     if (L0.router.dt == MH_DT_Q8R)
@@ -632,21 +698,31 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
         rc = L0.expert_dt == MH_DT_MXFP4 ? launch_t<MH_DT_F32, MH_DT_MXFP4>(A, nb, lds, s)
                                          : launch_t<MH_DT_F32, MH_DT_Q4G32>(A, nb, lds, s);
     if (rc || !A.trace) return rc;
-    // profiling: fold block 0's phase timestamps (100 MHz clock) into the profile
-    std::vector<unsigned long long> tr((size_t)16 * n_layers);
+    // profiling: fold the per-block phase timestamps (100 MHz clock) into
+    // the profile: the mean over blocks and the slowest block of each span
+    std::vector<unsigned long long> tr((size_t)16 * n_layers * nb);
     MH_HIP(hipMemcpyAsync(tr.data(), p->trace, tr.size() * 8, hipMemcpyDeviceToHost, s));
     MH_HIP(hipStreamSynchronize(s));
-    // (name, from, to) over block 0's timestamps
     static const struct { const char *name; int a, b; } spans[] = {
-        {"decode_step/router", 0, 1}, {"decode_step/barrier1", 1, 2}, {"decode_step/gate_up", 2, 3},
-        {"decode_step/gu_topk", 2, 8}, {"decode_step/gu_issue", 8, 9}, {"decode_step/gu_math", 9, 10},
-        {"decode_step/gu_reduce", 10, 11}, {"decode_step/gu_epilogue", 11, 3},
-        {"decode_step/barrier2_arrive_prefetch", 3, 4}, {"decode_step/barrier2_wait", 4, 5},
-        {"decode_step/down_combine", 5, 6}, {"decode_step/dn_hload", 5, 12}, {"decode_step/dn_math", 12, 13},
-        {"decode_step/dn_reduce", 13, 14}, {"decode_step/dn_combine", 14, 6}, {"decode_step/barrier3", 6, 7}};
+        {"router", 0, 1},         {"barrier1", 1, 2},     {"gate_up", 2, 3},       {"gu_topk", 2, 8},
+        {"gu_issue", 8, 9},       {"gu_math", 9, 10},     {"gu_reduce", 10, 11},   {"gu_epilogue", 11, 3},
+        {"barrier2_arrive_prefetch", 3, 4}, {"barrier2_wait", 4, 5}, {"down_combine", 5, 6},
+        {"dn_hload", 5, 12},      {"dn_math", 12, 13},    {"dn_reduce", 13, 14},   {"dn_combine", 14, 6},
+        {"barrier3", 6, 7},       {"layer", 0, 7}};
+    char name[96];
     for (int l = 0; l < n_layers; l++)
-        for (const auto &sp : spans)
-            prof_add(sp.name, (double)(tr[(size_t)l * 16 + sp.b] - tr[(size_t)l * 16 + sp.a]) * 1e-5);
+        for (const auto &sp : spans) {
+            double sum = 0, mx = 0;
+            for (int b = 0; b < nb; b++) {
+                const double d = (double)(tr[((size_t)l * 16 + sp.b) * nb + b] - tr[((size_t)l * 16 + sp.a) * nb + b]);
+                sum += d;
+                mx = std::max(mx, d);
+            }
+            snprintf(name, sizeof(name), "decode_step/%s", sp.name);
+            prof_add(name, sum / nb * 1e-5);
+            snprintf(name, sizeof(name), "decode_step/%s.max", sp.name);
+            prof_add(name, mx * 1e-5);
+        }
     return MH_OK;
 }
 
