@@ -157,10 +157,12 @@ def run_gpu(args, shape):
     midge_amd.sync()
     kern = {}
     # per-layer phase spans of the one-launch step: mean over blocks, and the slowest block
-    spans = ("layer", "router", "barrier1", "gate_up", "gu_topk", "gu_issue", "gu_math", "gu_reduce",
-             "gu_epilogue", "barrier2_arrive_prefetch", "barrier2_wait", "down_combine", "dn_hload", "dn_math",
-             "dn_reduce", "dn_combine", "barrier3")
-    phases = tuple(f"decode_step/{n}{m}" for n in spans for m in ("", ".max"))
+    spans = ("layer", "x_wait", "router", "route", "route0_gather", "route0_rank", "route0_weights",
+             "route0_publish", "gate_up", "gu_issue", "gu_math", "gu_reduce", "gu_epilogue",
+             "barrier_arrive_prefetch", "barrier_wait", "down_combine", "dn_hload", "dn_math", "dn_reduce",
+             "dn_combine", "tail")
+    phases = tuple(f"decode_step/{n}{m}" for n in spans for m in ("", ".max")) + tuple(
+        f"decode_step/crit_{n}" for n in ("logits", "routed", "h", "x"))
     for name in ("decode_step", "expert_gu", "expert_down", "gemv", "topk", "rmsnorm", "combine_decode") + phases:
         tot, n = profile_query(name)
         if n:

@@ -2,23 +2,30 @@
 // in one cooperative launch: the MoE half of forward()'s layer loop
 // (engine/midge.c:557-560) with moe() (engine/midge.c:469-549) per layer.
 //
-// One block per CU, 512 threads. Per layer, three phases separated by
-// grid barriers:
-//   A  router     every block loads x, forms xb = rmsnorm(x) in LDS; the
-//                 router's rows are spread over the blocks -> logits.
-//   B  gate/up    every block runs the same stable top-k on the logits, then
-//                 its share of the routed experts' gate/up rows (the pairs of
-//                 all k experts laid end to end and cut evenly), with the
-//                 bias + clamped SwiGLU epilogue -> h[k][ffn].
+// One block per CU, 512 threads. Per layer:
+//   A  router     every block reads x (the previous layer's output, as
+//                 sequence-tagged words), forms xb = rmsnorm(x) * w in LDS;
+//                 the router's rows are spread over the blocks and each
+//                 logit is published as a tagged word.
+//   route         block 0 gathers the tagged logits, ranks them (stable
+//                 top-k, ties to the lower index) and publishes the routing
+//                 record (expert, weight per slot) as tagged words, which
+//                 every other block polls.
+//   B  gate/up    each block takes an even share of the routed experts'
+//                 (gate, up) row pairs, with the bias + clamped SwiGLU
+//                 epilogue -> h[k][ffn]; then a grid barrier.
 //   C  down       each block owns a slice of output rows for all k experts;
 //                 their weights are loaded into registers between the
-//                 barrier's arrive and wait, so the load overlaps the wait.
-//                 Epilogue: y = Wd h + bd, moe = sum_i w_i y_i in selection
-//                 order, x += moe.
-// Barriers are contention-free: each block publishes a monotonically
-// increasing sequence number in its own flag; one wave per block polls all
-// flags with a single vector load per lane. Waits are bounded: a barrier that
-// does not complete within ~1 s raises an error flag and every block exits.
+//                 barrier's arrive and wait. Epilogue: y = Wd h + bd,
+//                 moe = sum_i w_i y_i in selection order, x += moe, written
+//                 as tagged words for the next layer (plain floats after the
+//                 last layer).
+// Tagged words carry the producer's sequence number next to the value in one
+// 64-bit store, so a consumer needs no separate barrier: it polls the words
+// it needs until every tag matches. The one full barrier per layer (before
+// the down phase, which needs all of h) is a gather/broadcast over per-block
+// flags. Every wait is bounded: one that does not complete within ~1 s raises
+// an error flag and every block exits.
 #include <stdio.h>
 
 #include <algorithm>
@@ -48,13 +55,15 @@ struct StepArgs {
     int32_t *sel;            // [L][K] or null
     float *w;                // [L][K] or null
     uint32_t *usage;         // [L][E] or null
-    float *logits;           // [E] scratch
+    uint64_t *lw;            // [E] tagged logits
+    uint64_t *rec;           // [K] tagged routing record (block 0 -> all)
+    uint64_t *xw;            // [H] tagged x between layers
     float *h;                // [K][F] scratch
     unsigned *flags;         // [gridDim.x] barrier flags
     unsigned *go;            // barrier release word (written by block 0)
-    unsigned seq0;           // sequence number of this launch's first barrier
+    unsigned seq0;           // first sequence number of this launch (3 per layer)
     unsigned *err;
-    unsigned long long *trace;   // [L][16][gridDim.x] per-block phase timestamps, or null
+    unsigned long long *trace;   // [L][kStamps][gridDim.x] per-block phase timestamps, or null
     int res_floats;              // LDS floats of the reduced-rows area
     int red_floats;              // LDS floats of the partial-sum area
 };
@@ -66,6 +75,8 @@ constexpr int kUP = 9;          // gate/up row pairs in flight per thread
 constexpr int kUC = 12;         // down rows in flight per thread
 constexpr int kNX = 8;          // x elements per thread in the router phase (H <= kNX * kThreads)
 constexpr unsigned kSpinLimit = 1u << 20;
+constexpr int kStamps = 24;     // phase timestamps per layer and block while profiling
+constexpr int kEL = 2;          // logits per lane in the routing wave (E <= 64 * kEL)
 
 // Memory access. Every load goes through a buffer resource (32-bit offsets,
 // out-of-range reads return 0). Weights are streamed with the nontemporal
@@ -76,8 +87,16 @@ constexpr unsigned kSpinLimit = 1u << 20;
 constexpr int kNT = 2;     // cache-policy bits: nontemporal
 constexpr int kDev = 16;   // cache-policy bits: device scope
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Every resource here is uniform across the block; the pointer fields read
+// from the layer table are made scalar explicitly (readfirstlane), otherwise
+// the compiler keeps them in vector registers and wraps every buffer access
+// in a loop over the distinct values.
 __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    void *u = (void *)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 __device__ __forceinline__ mh_u4 ld_w16(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT);
@@ -169,36 +188,76 @@ __device__ __forceinline__ float block_sum(float v, float *part) {
     return s;
 }
 
-// Stable top-k by one wave over LDS logits v[E] (ties to the lower index;
-// only values > -1e30 qualify; unfilled slots get -1, engine/midge.c:476-486)
-// and the routing weights (engine/midge.c:502-512). Results in LDS.
-__device__ void wave_topk(const float *v, int E, int k, int router_norm, int *s_sel, float *s_val, float *s_w) {
+// Tagged words: (tag << 32) | value bits in one device-scope 64-bit store.
+__device__ __forceinline__ void st_tag(uint64_t *p, unsigned tag, float v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_tag(uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Routing record word for slot i: 22 tag bits, 10 expert bits (0x3FF = an
+// unfilled slot), the weight's 32 bits.
+constexpr unsigned kRecTagMask = 0x3FFFFFu;
+__device__ __forceinline__ uint64_t rec_word(unsigned tag, int sel, float w) {
+    const uint64_t code = sel < 0 ? 0x3FFu : (uint64_t)sel;
+    return ((uint64_t)(tag & kRecTagMask) << 42) | (code << 32) | __float_as_uint(w);
+}
+
+// Maximum over the wave (every lane gets it): DPP within rows of 16, then
+// row broadcasts; lanes a DPP step does not write keep their value.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    const int o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xF, false);
+    return fmaxf(v, __int_as_float(o));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = dpp_max_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x141, 0xF>(v);   // row_half_mirror
+    v = dpp_max_step<0x140, 0xF>(v);   // row_mirror
+    v = dpp_max_step<0x142, 0xA>(v);   // row_bcast:15
+    v = dpp_max_step<0x143, 0xC>(v);   // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Stable top-k over the wave's E <= 64 * kEL logits (lane holds element
+// lane + 64 j in v[j]; absent elements are -inf): k rounds of "largest
+// remaining value, lowest index among equals"; only values > -1e30
+// qualify, unfilled slots get -1 (engine/midge.c:476-486). Lane 0 writes
+// s_sel / s_val.
+__device__ __forceinline__ void wave_topk(float *v, int k, int *s_sel, float *s_val) {
     const int lane = threadIdx.x & 63;
-    unsigned long long taken = 0;   // bit j: element lane + 64 j is taken
     for (int i = 0; i < k; ++i) {
-        float bv = -1e30f;
-        int bi = INT32_MAX;
-        for (int j = 0; lane + 64 * j < E; ++j) {
-            const int e = lane + 64 * j;
-            if (!((taken >> j) & 1ull) && v[e] > bv) {
-                bv = v[e];
-                bi = e;
+        float lm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kEL; ++j) lm = fmaxf(lm, v[j]);
+        const float m = wave_max(lm);
+        int idx = -1;
+        if (m > -1e30f) {
+#pragma unroll
+            for (int j = kEL - 1; j >= 0; --j) {
+                const unsigned long long hit = __ballot(v[j] == m);
+                if (hit) idx = 64 * j + (__ffsll((long long)hit) - 1);
             }
         }
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
+        if (idx >= 0 && (idx & 63) == lane) {
+#pragma unroll
+            for (int j = 0; j < kEL; ++j)
+                if (j == (idx >> 6)) v[j] = -INFINITY;   // taken
         }
-        if (bi != INT32_MAX && (bi & 63) == lane) taken |= 1ull << (bi >> 6);
         if (lane == 0) {
-            s_sel[i] = bi == INT32_MAX ? -1 : bi;
-            s_val[i] = bi == INT32_MAX ? -1e30f : bv;
+            s_sel[i] = idx;
+            s_val[i] = idx >= 0 ? m : -1e30f;
         }
     }
+}
+
+// Routing weights for the selected slots (engine/midge.c:502-512), by one
+// wave: softmax over the k selected logits (router_norm) or the k entries of
+// the softmax over all E logits v[]. Lane 0 writes s_w.
+__device__ void wave_weights(const float *v, int E, int k, int router_norm, const float *s_val, float *s_w) {
+    const int lane = threadIdx.x & 63;
     float fmx = 0.f, fden = 0.f;
     if (!router_norm) {
         float m = -INFINITY;
@@ -271,38 +330,77 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
     __shared__ float s_val[16];
     __shared__ int s_ok;
     const int H = A.H, F = A.F, E = A.E, K = A.K;
-    float *xs = lds;             // x at layer start
-    float *xbs = xs + H;         // rmsnorm(x) * w
-    float *res = xbs + H;        // reduced rows / staged logits
+    // xb = rmsnorm(x) * w is kept in 32-element groups padded to 33 floats:
+    // thread c reads group c element by element, and the padding puts the
+    // 64 lanes of a wave in 64 distinct LDS banks.
+    float *xs = lds;                   // x at layer start
+    float *xbs = xs + H;               // xb, padded: element i at (i / 32) * 33 + i % 32
+    float *res = xbs + (H / 32) * 33;  // reduced rows / staged logits
     float *red = res + A.res_floats;
     float *bds = red + A.red_floats;   // [K][rows of this block's down slice]
     const int NB = gridDim.x, b = blockIdx.x, t = threadIdx.x;
     const int wave = t >> 6;
-    unsigned seq = A.seq0;
 
     // per-block phase timestamps (100 MHz), written by thread 0 while profiling
     unsigned long long *tr = (A.trace && t == 0) ? A.trace + b : nullptr;
 #define MH_STAMP(ph) \
-    if (tr) tr[(size_t)(l * 16 + (ph)) * NB] = wall_clock64()
+    if (tr) tr[(size_t)(l * kStamps + (ph)) * NB] = wall_clock64()
 
     const rsrc_t rx = make_rsrc(A.x, (uint32_t)H * 4u);
-    const rsrc_t rlg = make_rsrc(A.logits, (uint32_t)E * 4u);
     const rsrc_t rh = make_rsrc(A.h, (uint32_t)K * (uint32_t)F * 4u);
     const uint32_t layer_bytes = (uint32_t)((uint64_t)E * A.stride - 1u) + 1u;   // < 4 GiB (plan check)
     const int CR = H / RE;   // router chunks per row
     RouterPref pf = prefetch_router<RDT>(A, 0, CR);
     for (int l = 0; l < A.n_layers; ++l) {
         const StepLayer Ly = A.layers[l];
+        // sequence numbers of this layer: logits and routing record, the
+        // barrier before the down phase, x for the next layer
+        const unsigned tagA = A.seq0 + 3u * (unsigned)l, tagB = tagA + 1u, tagC = tagA + 2u;
         MH_STAMP(0);
         // ------------------------------------------------ A: router
         {
             float xv[kNX];
+            if (l == 0) {
+#pragma unroll
+                for (int k = 0; k < kNX; ++k) xv[k] = ld_dev(rx, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
+            } else {
+                // the previous layer's x, tagged tagA - 1: load all, re-poll the late ones
+                uint64_t wv[kNX];
+                const unsigned want = tagA - 1u;
+                const int tt = opaque(t);
+#pragma unroll
+                for (int k = 0; k < kNX; ++k) {
+                    const int i = tt + k * kThreads;
+                    wv[k] = i < H ? ld_tag(A.xw + i) : (uint64_t)want << 32;
+                }
+                bool late = false;
+                for (unsigned spins = 0;; ++spins) {
+                    bool ready = true;
+#pragma unroll
+                    for (int k = 0; k < kNX; ++k) ready = ready && (unsigned)(wv[k] >> 32) == want;
+                    if (ready) break;
+                    if (spins > kSpinLimit) {
+                        late = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                    for (int k = 0; k < kNX; ++k) {
+                        const int i = tt + k * kThreads;
+                        if (i < H && (unsigned)(wv[k] >> 32) != want) wv[k] = ld_tag(A.xw + i);
+                    }
+                }
+                if (__syncthreads_or(late)) {
+                    if (t == 0) __hip_atomic_store(A.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    return;
+                }
+#pragma unroll
+                for (int k = 0; k < kNX; ++k) xv[k] = __uint_as_float((uint32_t)wv[k]);
+            }
+            MH_STAMP(15);
             float ss = 0.f;
 #pragma unroll
-            for (int k = 0; k < kNX; ++k) {
-                xv[k] = ld_dev(rx, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
-                ss = __builtin_fmaf(xv[k], xv[k], ss);
-            }
+            for (int k = 0; k < kNX; ++k) ss = __builtin_fmaf(xv[k], xv[k], ss);
             ss = block_sum(ss, s_part);
             const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
 #pragma unroll
@@ -310,7 +408,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 const int i = t + k * kThreads;
                 if (i < H) {
                     xs[i] = xv[k];
-                    xbs[i] = xv[k] * inv * pf.nw[k];
+                    xbs[(i >> 5) * 33 + (i & 31)] = xv[k] * inv * pf.nw[k];
                 }
             }
         }
@@ -321,7 +419,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             const rsrc_t rw = make_rsrc(Ly.router_w, (uint32_t)E * (uint32_t)CR * 16u);
             for (int c = t; c < CR; c += kThreads) {
                 const mh_u4 q = (e == b && c == t) ? pf.rq : ld_w16(rw, (uint32_t)(e * CR + c) * 16u);
-                p += mh_dot_chunk<RDT>(q, xbs + (size_t)c * RE);
+                const int i0 = c * RE;   // a router chunk lies inside one 32-element group
+                p += mh_dot_chunk<RDT>(q, xbs + (i0 >> 5) * 33 + (i0 & 31));
             }
             p = block_sum(p, s_part);
             if (e != b) {
@@ -330,28 +429,92 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             }
             if (t == 0) {
                 if constexpr (RDT == MH_DT_Q8R) p *= rs;
-                st_dev(A.logits + e, p + rb);
+                st_tag(A.lw + e, tagA, p + rb);
             }
         }
         MH_STAMP(1);
-        bar_arrive(A.flags, seq);
-        if (!bar_wait(A.flags, A.go, seq, A.err, &s_ok)) return;
-        ++seq;
+
+        // ------------------------------------------------ route
+        if (b == 0) {
+            // one wave gathers the logits (kEL per lane: element lane + 64 j),
+            // selects the stable top-k and publishes the routing record; the
+            // block's other waves wait at the barrier below
+            bool late = false;
+            if (wave == 0) {
+                const int lane = t;
+                const int tt = opaque(t);
+                uint64_t wv[kEL];
+#pragma unroll
+                for (int j = 0; j < kEL; ++j) {
+                    const int e = tt + 64 * j;
+                    wv[j] = e < E ? ld_tag(A.lw + e) : (uint64_t)tagA << 32;
+                }
+                for (unsigned spins = 0;; ++spins) {
+                    bool ready = true;
+#pragma unroll
+                    for (int j = 0; j < kEL; ++j) ready = ready && (unsigned)(wv[j] >> 32) == tagA;
+                    if (__all(ready)) break;
+                    if (spins > kSpinLimit) {
+                        late = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                    for (int j = 0; j < kEL; ++j) {
+                        const int e = tt + 64 * j;
+                        if (e < E && (unsigned)(wv[j] >> 32) != tagA) wv[j] = ld_tag(A.lw + e);
+                    }
+                }
+                MH_STAMP(16);
+                float v[kEL];
+#pragma unroll
+                for (int j = 0; j < kEL; ++j) {
+                    v[j] = lane + 64 * j < E ? __uint_as_float((uint32_t)wv[j]) : -INFINITY;
+                    res[lane + 64 * j] = v[j];   // all logits, for the softmax over all of them
+                }
+                wave_topk(v, K, s_sel, s_val);
+                MH_STAMP(17);
+                wave_weights(res, E, K, A.router_norm, s_val, s_w);
+                MH_STAMP(18);
+                if (lane < K) {
+                    __hip_atomic_store(A.rec + lane, rec_word(tagA, s_sel[lane], s_w[lane]), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    if (A.sel) A.sel[(size_t)l * K + lane] = s_sel[lane];
+                    if (A.w) A.w[(size_t)l * K + lane] = s_w[lane];
+                    if (A.usage && s_sel[lane] >= 0)
+                        __hip_atomic_fetch_add(&A.usage[(size_t)l * E + s_sel[lane]], 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            if (__syncthreads_or(late)) {
+                if (t == 0) __hip_atomic_store(A.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                return;
+            }
+        } else {
+            bool late = false;
+            const int tt = opaque(t);
+            if (tt < K) {
+                uint64_t w = ld_tag(A.rec + tt);
+                for (unsigned spins = 0; (unsigned)(w >> 42) != (tagA & kRecTagMask); ++spins) {
+                    if (spins > kSpinLimit) {
+                        late = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    w = ld_tag(A.rec + tt);
+                }
+                const int code = (int)((w >> 32) & 0x3FFu);
+                s_sel[tt] = code == 0x3FF ? -1 : code;
+                s_w[tt] = __uint_as_float((uint32_t)w);
+            }
+            if (__syncthreads_or(late)) {
+                if (t == 0) __hip_atomic_store(A.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                return;
+            }
+        }
         MH_STAMP(2);
 
         // ------------------------------------------------ B: gate/up
-        for (int e = t; e < E; e += kThreads) res[e] = ld_dev(rlg, (uint32_t)e * 4u);
-        __syncthreads();
-        if (wave == 0) wave_topk(res, E, K, A.router_norm, s_sel, s_val, s_w);
-        __syncthreads();
-        MH_STAMP(8);
-        if (b == 0 && t < K) {
-            if (A.sel) A.sel[(size_t)l * K + t] = s_sel[t];
-            if (A.w) A.w[(size_t)l * K + t] = s_w[t];
-            if (A.usage && s_sel[t] >= 0)
-                __hip_atomic_fetch_add(&A.usage[(size_t)l * E + s_sel[t]], 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-        }
         const rsrc_t rex = make_rsrc(Ly.experts, layer_bytes);
         {
             // Rows come in (gate, up) pairs: pair p of the k experts laid end
@@ -374,57 +537,56 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             const uint32_t os0 = (uint32_t)A.off[1], os1 = (uint32_t)A.off[4];
             float xr[XE];
 #pragma unroll
-            for (int j = 0; j < XE; ++j) xr[j] = active ? xbs[c * XE + j] : 0.f;
-            // this thread's epilogue pair's biases, loaded with the weights
-            float bg_pref = 0.f, bu_pref = 0.f;
+            for (int j = 0; j < XE; ++j) xr[j] = active ? xbs[c * 33 + j] : 0.f;
+            // One pass (plan check: np <= ns * kUP). Branch-free loads: a
+            // past-the-end pair or an idle slot re-reads the block's last pair
+            // and is masked out in the math; scale bits stay raw until every
+            // load is in flight.
+            mh_u4 qg[kUP], qu[kUP];
+            uint32_t sg[kUP], su[kUP];
+            const int sl = active ? slot : ns - 1;
+            const int plast = max(np - 1, 0);
+#pragma unroll
+            for (int u = 0; u < kUP; ++u) {
+                const int pr = rb + min(u * ns + sl, plast);
+                const bool second = pr >= F;
+                const uint32_t eo = second ? eo_b : eo_a;
+                const uint32_t rc = (uint32_t)((second ? pr - F : pr) * C + c);
+                qg[u] = ld_w16(rex, eo + od0 + rc * 16u);
+                qu[u] = ld_w16(rex, eo + od1 + rc * 16u);
+                sg[u] = ld_w2(rex, eo + os0 + rc * 2u);
+                su[u] = ld_w2(rex, eo + os1 + rc * 2u);
+            }
+            // this thread's epilogue pair's biases, behind the weights
+            float bg_pref, bu_pref;
             {
-                const int pr = rb + min(t, max(np - 1, 0));
+                const int pr = rb + min(t, plast);
                 const bool second = pr >= F;
                 const uint32_t eo = second ? eo_b : eo_a;
                 const uint32_t r4 = (uint32_t)(second ? pr - F : pr) * 4u;
                 bg_pref = ld_f(rex, eo + (uint32_t)A.off[2] + r4);
                 bu_pref = ld_f(rex, eo + (uint32_t)A.off[5] + r4);
             }
-            for (int p0 = 0; p0 < np; p0 += ns * kUP) {
-                // Branch-free loads: a past-the-end pair or an idle slot
-                // re-reads the block's last pair and is masked out in the
-                // math; scale bits stay raw until every load is in flight.
-                mh_u4 qg[kUP], qu[kUP];
-                uint32_t sg[kUP], su[kUP];
-                const int sl = active ? slot : ns - 1;
+            __builtin_amdgcn_sched_barrier(0);   // all loads issued before any math
+            MH_STAMP(9);
 #pragma unroll
-                for (int u = 0; u < kUP; ++u) {
-                    const int pr = rb + min(p0 + u * ns + sl, np - 1);
-                    const bool second = pr >= F;
-                    const uint32_t eo = second ? eo_b : eo_a;
-                    const uint32_t rc = (uint32_t)((second ? pr - F : pr) * C + c);
-                    qg[u] = ld_w16(rex, eo + od0 + rc * 16u);
-                    qu[u] = ld_w16(rex, eo + od1 + rc * 16u);
-                    sg[u] = ld_w2(rex, eo + os0 + rc * 2u);
-                    su[u] = ld_w2(rex, eo + os1 + rc * 2u);
+            for (int u = 0; u < kUP; ++u) {
+                const int pp = u * ns + slot;
+                const bool inr = active && pp < np;
+                const bool valid = inr && (rb + pp >= F ? e_b : e_a) >= 0;
+                const float g = mh_dot_chunk<XDT>(qg[u], xr) * (valid ? mh_f16((uint16_t)sg[u]) : 0.f);
+                const float v = mh_dot_chunk<XDT>(qu[u], xr) * (valid ? mh_f16((uint16_t)su[u]) : 0.f);
+                if (inr) {
+                    red[(2 * pp) * C + c] = g;
+                    red[(2 * pp + 1) * C + c] = v;
                 }
-                __builtin_amdgcn_sched_barrier(0);   // all loads issued before any math
-                if (p0 == 0) MH_STAMP(9);
-#pragma unroll
-                for (int u = 0; u < kUP; ++u) {
-                    const int pp = p0 + u * ns + slot;
-                    const bool inr = active && pp < np;
-                    const bool valid = inr && (rb + pp >= F ? e_b : e_a) >= 0;
-                    const float g = mh_dot_chunk<XDT>(qg[u], xr) * (valid ? mh_f16((uint16_t)sg[u]) : 0.f);
-                    const float v = mh_dot_chunk<XDT>(qu[u], xr) * (valid ? mh_f16((uint16_t)su[u]) : 0.f);
-                    if (inr) {
-                        red[(2 * (u * ns + slot)) * C + c] = g;
-                        red[(2 * (u * ns + slot) + 1) * C + c] = v;
-                    }
-                    __builtin_amdgcn_sched_barrier(0);   // one pair's math at a time
-                }
-                if (p0 == 0) MH_STAMP(10);
-                __syncthreads();
-                const int items = min(ns * kUP, np - p0);
-                block_reduce_rows(red, C, 2 * items, res + 2 * p0, [](int) { return true; });
-                __syncthreads();
-                if (p0 == 0) MH_STAMP(11);
+                __builtin_amdgcn_sched_barrier(0);   // one pair's math at a time
             }
+            MH_STAMP(10);
+            __syncthreads();
+            block_reduce_rows(red, C, 2 * np, res, [](int) { return true; });
+            __syncthreads();
+            MH_STAMP(11);
             // epilogue: pair t -> h (np <= F <= kThreads pairs: one per thread)
             if (t < np) {
                 const int pr = rb + t;
@@ -436,7 +598,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             }
         }
         MH_STAMP(3);
-        bar_arrive(A.flags, seq);
+        bar_arrive(A.flags, tagB);
 
         // ------------------------------------------------ C: down + combine
         {
@@ -478,8 +640,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             }
             __builtin_amdgcn_sched_barrier(0);
             MH_STAMP(4);
-            if (!bar_wait(A.flags, A.go, seq, A.err, &s_ok)) return;
-            ++seq;
+            if (!bar_wait(A.flags, A.go, tagB, A.err, &s_ok)) return;
             MH_STAMP(5);
             float xr[XE];
             {
@@ -518,14 +679,12 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                     const float y = res[ii * RC + j] + bds[ii * nr + j];
                     moe = moe + s_w[ii] * y;
                 }
-                st_dev(A.x + r, xs[r] + moe);
+                if (l + 1 < A.n_layers) st_tag(A.xw + r, tagC, xs[r] + moe);
+                else st_dev(A.x + r, xs[r] + moe);
             }
         }
         MH_STAMP(6);
-        bar_arrive(A.flags, seq);
         if (l + 1 < A.n_layers) pf = prefetch_router<RDT>(A, l + 1, CR);
-        if (!bar_wait(A.flags, A.go, seq, A.err, &s_ok)) return;
-        ++seq;
         MH_STAMP(7);
     }
 #undef MH_STAMP
@@ -557,11 +716,12 @@ int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
 struct StepPlan {
     StepLayer *layers = nullptr;   // device [L]
     unsigned *flags = nullptr;     // device [nb + 64]: flags, then the go word on its own line
+    uint64_t *tagged = nullptr;    // device: logits [E] | record [16] | x [H], tagged words
+    size_t tagged_words = 0;
     unsigned long long *trace = nullptr;   // device [L][16][nb] (filled while profiling)
     int n_layers = 0;
     unsigned *err = nullptr;       // host-mapped pinned [1]: set by a timed-out barrier
     unsigned *err_dev = nullptr;   // its device address
-    float *logits = nullptr;       // device [E]
     float *h = nullptr;            // device [K][F]
     unsigned seq = 0;              // next barrier sequence number
     int nb = 0;
@@ -581,7 +741,7 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     if (L0.expert_dt != MH_DT_MXFP4 && L0.expert_dt != MH_DT_Q4G32) return reject("experts are not 4-bit g32");
     if (L0.hidden % 32 || L0.ffn % 32 || L0.hidden / 32 > kThreads || L0.ffn / 32 > kThreads)
         return reject("hidden/ffn not multiples of 32 or too wide");
-    if (L0.n_experts > 1024 || L0.top_k > 16) return reject("too many experts");
+    if (L0.n_experts > 64 * kEL || L0.top_k > 16) return reject("too many experts");
     if (L0.expert_stride * (uint64_t)L0.n_experts >= (1ull << 32)) return reject("a layer's experts exceed 4 GiB");
     for (int l = 0; l < n_layers; l++) {
         const DevLayer &L = layers[l];
@@ -602,6 +762,7 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
         // has one pair per thread
         const int PB = (K * F + nb - 1) / nb;
         if (PB > F || PB > kThreads) return reject("a block's gate/up pairs span more than two experts");
+        if (PB > (kThreads / (H / 32)) * kUP) return reject("gate/up does not fit one pass");
         // down: one pass, every routed expert gets slots, each slot's rows of
         // the block's slice fit kUC iterations, one bias per thread
         const int nsC = kThreads / (F / 32);
@@ -617,13 +778,15 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     MH_HIP(hipMalloc(&p->layers, sizeof(StepLayer) * (size_t)n_layers));
     MH_HIP(hipMemcpy(p->layers, host.data(), sizeof(StepLayer) * (size_t)n_layers, hipMemcpyHostToDevice));
     MH_HIP(hipMalloc(&p->flags, sizeof(unsigned) * (size_t)(nb + 64)));
-    MH_HIP(hipMalloc(&p->trace, sizeof(unsigned long long) * 16 * (size_t)n_layers * (size_t)nb));
+    MH_HIP(hipMalloc(&p->trace, sizeof(unsigned long long) * kStamps * (size_t)n_layers * (size_t)nb));
     p->n_layers = n_layers;
     MH_HIP(hipHostMalloc((void **)&p->err, sizeof(unsigned), hipHostMallocMapped));
     *p->err = 0;
     MH_HIP(hipHostGetDevicePointer((void **)&p->err_dev, p->err, 0));
     watch_async_error(p->err, "decode step: a grid barrier timed out (blocks not co-resident)");
-    MH_HIP(hipMalloc(&p->logits, sizeof(float) * (size_t)L0.n_experts));
+    p->tagged_words = (size_t)L0.n_experts + 16 + (size_t)L0.hidden;
+    MH_HIP(hipMalloc(&p->tagged, sizeof(uint64_t) * p->tagged_words));
+    MH_HIP(hipMemset(p->tagged, 0, sizeof(uint64_t) * p->tagged_words));
     MH_HIP(hipMalloc(&p->h, sizeof(float) * (size_t)L0.top_k * (size_t)L0.ffn));
     MH_HIP(hipMemset(p->flags, 0, sizeof(unsigned) * (size_t)(nb + 64)));
     MH_HIP(hipDeviceSynchronize());
@@ -640,7 +803,7 @@ void step_plan_destroy(StepPlan *p) {
     (void)hipFree(p->trace);
     unwatch_async_error(p->err);
     (void)hipHostFree(p->err);
-    (void)hipFree(p->logits);
+    (void)hipFree(p->tagged);
     (void)hipFree(p->h);
     delete p;
 }
@@ -670,7 +833,9 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     A.sel = sel;
     A.w = w;
     A.usage = usage;
-    A.logits = p->logits;
+    A.lw = p->tagged;
+    A.rec = p->tagged + A.E;
+    A.xw = p->tagged + A.E + 16;
     A.h = p->h;
     A.flags = p->flags;
     A.go = p->flags + ((p->nb + 63) / 32) * 32;   // a separate 128-byte line
@@ -679,16 +844,18 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     const unsigned nbar = 3u * (unsigned)n_layers;
     if (p->seq > 0xF0000000u) {   // wrap: restart the sequence from a clean slate
         MH_LAUNCH("fill", k_fill_u32, dim3(1), dim3(256), 0, s, p->flags, p->nb + 64, 0u);
+        MH_LAUNCH("fill", k_fill_u32, dim3(8), dim3(256), 0, s, (unsigned *)p->tagged, (int)(2 * p->tagged_words), 0u);
         p->seq = 1;
     }
     A.seq0 = p->seq;
     p->seq += nbar;
     const int nb = p->nb;
     const int PB = (A.K * A.F + nb - 1) / nb, RC = (A.H + nb - 1) / nb;
-    A.res_floats = std::max(std::max(A.E, 2 * PB), A.K * RC) + 64;
+    A.res_floats = std::max(64 * kEL, std::max(2 * PB, A.K * RC)) + 64;
     const int nsB = kThreads / A.CH;
     A.red_floats = std::max(2 * nsB * kUP * A.CH, A.K * RC * A.CF);
-    const size_t lds = ((size_t)2 * A.H + A.res_floats + A.red_floats + (size_t)A.K * RC) * sizeof(float);
+    const size_t lds = ((size_t)A.H + (size_t)(A.H / 32) * 33 + A.res_floats + A.red_floats + (size_t)A.K * RC) *
+                       sizeof(float);
     if (lds > 160 * 1024) return fail(MH_E_UNSUPPORTED, "decode step needs %zu B of LDS", lds);
     int rc;
     if (L0.router.dt == MH_DT_Q8R)
@@ -700,29 +867,49 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     if (rc || !A.trace) return rc;
     // profiling: fold the per-block phase timestamps (100 MHz clock) into
     // the profile: the mean over blocks and the slowest block of each span
-    std::vector<unsigned long long> tr((size_t)16 * n_layers * nb);
+    std::vector<unsigned long long> tr((size_t)kStamps * n_layers * nb);
     MH_HIP(hipMemcpyAsync(tr.data(), p->trace, tr.size() * 8, hipMemcpyDeviceToHost, s));
     MH_HIP(hipStreamSynchronize(s));
-    static const struct { const char *name; int a, b; } spans[] = {
-        {"router", 0, 1},         {"barrier1", 1, 2},     {"gate_up", 2, 3},       {"gu_topk", 2, 8},
-        {"gu_issue", 8, 9},       {"gu_math", 9, 10},     {"gu_reduce", 10, 11},   {"gu_epilogue", 11, 3},
-        {"barrier2_arrive_prefetch", 3, 4}, {"barrier2_wait", 4, 5}, {"down_combine", 5, 6},
-        {"dn_hload", 5, 12},      {"dn_math", 12, 13},    {"dn_reduce", 13, 14},   {"dn_combine", 14, 6},
-        {"barrier3", 6, 7},       {"layer", 0, 7}};
+    // (name, from, to, only block 0)
+    static const struct { const char *name; int a, b; bool b0; } spans[] = {
+        {"x_wait", 0, 15, false},   {"router", 15, 1, false},     {"route", 1, 2, false},
+        {"route0_gather", 1, 16, true}, {"route0_rank", 16, 17, true}, {"route0_weights", 17, 18, true},
+        {"route0_publish", 18, 2, true}, {"gate_up", 2, 3, false}, {"gu_issue", 2, 9, false},
+        {"gu_math", 9, 10, false},  {"gu_reduce", 10, 11, false}, {"gu_epilogue", 11, 3, false},
+        {"barrier_arrive_prefetch", 3, 4, false}, {"barrier_wait", 4, 5, false}, {"down_combine", 5, 6, false},
+        {"dn_hload", 5, 12, false}, {"dn_math", 12, 13, false},  {"dn_reduce", 13, 14, false},
+        {"dn_combine", 14, 6, false}, {"tail", 6, 7, false},     {"layer", 0, 7, false}};
     char name[96];
-    for (int l = 0; l < n_layers; l++)
+    auto at = [&](int l, int st, int b) { return (double)tr[((size_t)l * kStamps + st) * nb + b]; };
+    for (int l = 0; l < n_layers; l++) {
         for (const auto &sp : spans) {
+            const int nbk = sp.b0 ? 1 : nb;
             double sum = 0, mx = 0;
-            for (int b = 0; b < nb; b++) {
-                const double d = (double)(tr[((size_t)l * 16 + sp.b) * nb + b] - tr[((size_t)l * 16 + sp.a) * nb + b]);
+            for (int b = 0; b < nbk; b++) {
+                const double d = at(l, sp.b, b) - at(l, sp.a, b);
                 sum += d;
                 mx = std::max(mx, d);
             }
             snprintf(name, sizeof(name), "decode_step/%s", sp.name);
-            prof_add(name, sum / nb * 1e-5);
+            prof_add(name, sum / nbk * 1e-5);
             snprintf(name, sizeof(name), "decode_step/%s.max", sp.name);
             prof_add(name, mx * 1e-5);
         }
+        // the critical path: from the first block's layer start to the last
+        // block's logit, the last block's routing record and the last arrival
+        double t0 = 1e300, lastA = 0, lastR = 0, lastB = 0, lastC = 0;
+        for (int b = 0; b < nb; b++) {
+            t0 = std::min(t0, at(l, 0, b));
+            lastA = std::max(lastA, at(l, 1, b));
+            lastR = std::max(lastR, at(l, 2, b));
+            lastB = std::max(lastB, at(l, 3, b));
+            lastC = std::max(lastC, at(l, 6, b));
+        }
+        prof_add("decode_step/crit_logits", (lastA - t0) * 1e-5);
+        prof_add("decode_step/crit_routed", (lastR - t0) * 1e-5);
+        prof_add("decode_step/crit_h", (lastB - t0) * 1e-5);
+        prof_add("decode_step/crit_x", (lastC - t0) * 1e-5);
+    }
     return MH_OK;
 }
 

@@ -275,3 +275,77 @@ def test_stack_fused_step_vs_per_layer_and_oracle(mh, shape, layers):
             assert (sf[l] == selr).all(), (l, sf[l], selr)
         assert rel_l2(xf, x) < TOL
     st.destroy()
+
+
+def test_stack_fused_step_ties_and_unfilled_slots(mh):
+    """Routing edge cases through the one-launch step, against the per-layer
+    launches and the oracle: 128 experts whose router rows repeat every 8
+    (exact ties in groups of 16: the top 4 are the lowest indices of the best
+    group, with equal weights), and a layer where only two experts' logits
+    exceed -1e30 (slots 2 and 3 unfilled: expert -1, weight 0)."""
+    import os
+    shape = MoEShape(hidden=256, ffn=192, n_experts=128, top_k=4)
+    keys = Keys(91)
+    lays, structs, host = [], [], []
+    for l in range(3):
+        ex = synth.host_layer_experts(shape, keys, l)
+        w, s, b, nw = synth.host_router(shape, keys, l)
+        if l == 1:
+            w = np.ascontiguousarray(w.reshape(shape.n_experts, -1)[np.arange(shape.n_experts) % 8]).reshape(w.shape)
+            s, b = s[np.arange(shape.n_experts) % 8].copy(), b[np.arange(shape.n_experts) % 8].copy()
+        if l == 2:
+            b = np.full_like(b, -1e31)
+            b[[3, 77]] = 0.0
+        lays.append(MoELayer.host(shape, ex, w, s, b, nw))
+        _LIVE.append(lays[-1])
+        structs.append(po.layer_struct(shape, ex, w, s, b, nw))
+        host.append((ex, w, s, b, nw))
+    st = Stack(lays, max_batch=1)
+    k = shape.top_k
+    x0 = synth.host_x(shape, keys, 1, step=5)
+    out = {}
+    for mode in ("fused", "per_layer"):
+        if mode == "per_layer":
+            os.environ["MIDGE_HIP_NO_FUSED"] = "1"
+        try:
+            xd = DevBuf.from_array(x0)
+            sd, wd = DevBuf(3 * k * 4), DevBuf(3 * k * 4)
+            st.decode(xd, 1, sd, wd)
+            mh.sync()
+            out[mode] = (xd.download(np.float32, x0.shape)[0], sd.download(np.int32, (3, k)),
+                         wd.download(np.float32, (3, k)))
+            for d in (xd, sd, wd):
+                d.free()
+        finally:
+            os.environ.pop("MIDGE_HIP_NO_FUSED", None)
+    st.destroy()
+    xf, sf, wf = out["fused"]
+    xp, sp, wp = out["per_layer"]
+    x = x0[0]
+    for l in range(2):
+        x, selr, wr = po.moe_decode(structs[l], x)
+        say(f"layer {l}: fused {sf[l].tolist()} oracle {np.asarray(selr).tolist()}")
+        assert (sf[l] == selr).all() and (sp[l] == selr).all(), (l, sf[l], sp[l], selr)
+        np.testing.assert_allclose(wf[l], wr, rtol=1e-5, atol=1e-7)
+    # layer 2: the reference would index expert -1 for an unfilled slot
+    # (engine/midge.c:515-517), so its moe() is undefined here and the oracle
+    # refuses; this library skips unfilled slots. Composed from the oracle's
+    # pieces: router, stable top-k, weights, and the filled experts' FFNs.
+    ex, w, s, b, nw = host[2]
+    xb = po.rmsnorm(x, nw, shape.norm_eps)
+    rl = po.matvec(shape.router_dt, w, s, xb, shape.n_experts, shape.hidden) + b
+    selr, val = po.topk(rl, k, decode=True)
+    wr = po.router_weights(rl, val, 1)
+    assert (sf[2] == selr).all() and (sp[2] == selr).all(), (sf[2], sp[2], selr)
+    np.testing.assert_allclose(wf[2], wr, rtol=1e-5, atol=1e-7)
+    moe = np.zeros_like(x)
+    for i in range(k):
+        if selr[i] >= 0:
+            moe = (moe + np.float32(wr[i]) * po.expert_ffn(structs[2], int(selr[i]), xb)).astype(np.float32)
+    x = (x + moe).astype(np.float32)
+    g = sf[1][0] % 8
+    assert sf[1].tolist() == [g, g + 8, g + 16, g + 24]      # ties go to the lower index
+    assert np.allclose(wf[1], 0.25)
+    assert sf[2][2:].tolist() == [-1, -1] and (wf[2][2:] == 0).all()
+    assert sorted(sf[2][:2].tolist()) == [3, 77]
+    assert rel_l2(xf, xp) < 1e-5 and rel_l2(xf, x) < TOL
