@@ -8,11 +8,13 @@ Attention and the dense trunk are excluded. Every step starts from a fresh
 seeded hidden state, so routing - and the experts read - differ per step.
 
 Prints ONE JSON line. `value` is decode tokens per second. `roofline` is the
-dominant kernel (the fused expert gate/up + SwiGLU launch) timed with HIP
-events on the library stream: algorithmic bytes per launch / average launch
-duration, against 8 TB/s. `cpu_baseline` is the reference engine (built from
-its own sources into oracle/_ref) running moe() on the host cores over one
-resident 128-expert layer, scaled to 36 layers.
+dominant kernel: at batch 1 the whole step is one launch (k_decode_step),
+timed with HIP events on the library stream over the timed region;
+algorithmic bytes per launch (every weight, scale, bias and router byte the
+step must read, once) / launch duration, against 8 TB/s. `traffic` is the
+HBM bytes per launch measured by rocprofv3 (profiles/). `cpu_baseline` is the
+reference engine (built from its own sources into oracle/_ref) running moe()
+on the host cores over one resident 128-expert layer, scaled to 36 layers.
 
     python bench.py [--steps K] [--warmup W] [--batch B] [--no-cpu]
 """
@@ -49,6 +51,8 @@ class HipEvents:
         self.hip.hipEventSynchronize.argtypes = [C.c_void_p]
         self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
         self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+        self.hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        self.hip.hipDeviceSynchronize.argtypes = []
 
     def event(self):
         e = C.c_void_p()
@@ -96,6 +100,17 @@ def run_gpu(args, shape):
         f"({shape.layout.layer_stride * shape.n_layers / 2**30:.2f} GiB) generated in {time.time() - t0:.1f}s")
     ev = HipEvents()
     s = stream()
+    if args.copy_calib_mib:
+        # a plain device-to-device copy of known size (the runtime's copy
+        # kernel), for scaling the HBM byte counters of a --pmc run
+        n = args.copy_calib_mib << 20
+        src, dst = DevBuf(n), DevBuf(n)
+        for _ in range(2):
+            assert ev.hip.hipMemcpy(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), n, 3) == 0   # device to device
+        assert ev.hip.hipDeviceSynchronize() == 0
+        src.free()
+        dst.free()
+        log(f"copy calibration: 2 x {args.copy_calib_mib} MiB device-to-device")
 
     def inputs(n_steps: int, batch: int, salt: int) -> DevBuf:
         xs = DevBuf(n_steps * batch * shape.hidden * 4)
@@ -170,8 +185,17 @@ def run_gpu(args, shape):
     profile_enable(False)
     xs.free()
     if "decode_step" in kern:
-        dom = {"name": "decode_step (all 36 layers in one cooperative launch)",
-               "bytes": step_bytes(shape, args.batch, unique), "avg_us": kern["decode_step"]["avg_us"]}
+        # one launch per step: the timed region's event time per step is the
+        # launch's average duration (the profiled launches also write phase
+        # stamps and run a few percent slower)
+        dom = {"name": "k_decode_step (all layers of a step in one cooperative launch)",
+               "bytes": step_bytes(shape, args.batch, unique), "avg_us": ms / args.steps * 1e3,
+               "profiled_avg_us": kern["decode_step"]["avg_us"]}
+        tpath = os.path.join(ROOT, "profiles", "decode_step_120b_b1_traffic.json")
+        if args.batch == 1 and shape.n_layers == 36 and shape.n_experts == 128 and os.path.exists(tpath):
+            with open(tpath) as f:
+                dom["traffic"] = json.load(f)["traffic_bytes"]
+            dom["traffic_source"] = "profiles/decode_step_120b_b1_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE)"
     else:
         dom = {"name": "expert_gu (fused gate/up MXFP4 GEMV + clamped SwiGLU)",
                "bytes": gu_bytes_per_launch(shape, args.batch * k), "avg_us": kern["expert_gu"]["avg_us"]}
@@ -264,6 +288,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b16", action="store_true", help="skip the extra batch-16 measurement")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="first copy this many MiB device-to-device twice (byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the expert stack "
@@ -290,8 +316,10 @@ def main() -> int:
                    "layers": shape.n_layers, "experts": shape.n_experts, "top_k": 4, "hidden": 2880,
                    "ffn": 2880, "batch": args.batch, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": dom["name"], "bytes_per_launch": dom["bytes"], "avg_us": dom["avg_us"]},
+                     "frac": dom["GBps"] / HBM_PEAK_GBS, "traffic": dom.get("traffic"),
+                     "kernel": dom["name"], "bytes_per_launch": dom["bytes"], "avg_us": dom["avg_us"],
+                     **({"traffic_source": dom["traffic_source"]} if "traffic_source" in dom else {}),
+                     **({"profiled_avg_us": dom["profiled_avg_us"]} if "profiled_avg_us" in dom else {})},
         "step": {"hbm_bytes": step_b, "hbm_GBps": step_b / (ms_step / 1e3) / 1e9,
                  "hbm_frac": step_b / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS,
                  "unique_experts_per_layer": unique, "kernels": kern},
@@ -299,6 +327,8 @@ def main() -> int:
     }
     out.update(extra)
     print(json.dumps(out), flush=True)
+    import midge_amd
+    midge_amd.shutdown()
     return 0
 
 

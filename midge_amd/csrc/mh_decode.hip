@@ -27,6 +27,7 @@
 // flags. Every wait is bounded: one that does not complete within ~1 s raises
 // an error flag and every block exits.
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <vector>
@@ -705,7 +706,18 @@ int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
     void *args[] = {&a};
     const bool prof = profiling();
     if (prof) prof_begin("decode_step", s);
-    hipError_t e = hipLaunchCooperativeKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s);
+    // One block per CU with the occupancy checked above: every block is
+    // resident at once. The cooperative launch makes the runtime verify that
+    // too; MIDGE_HIP_COOP=0 selects a plain launch of the same grid (for
+    // tools that do not handle cooperative dispatches). A block that were
+    // not resident would make the grid's bounded waits time out and report
+    // an error through mh_sync, never hang.
+    const char *coop = getenv("MIDGE_HIP_COOP");
+    hipError_t e;
+    if (coop && coop[0] == '0')
+        e = hipLaunchKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s);
+    else
+        e = hipLaunchCooperativeKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s);
     if (prof) prof_end(s);
     return hip_check(e, "decode step cooperative launch");
 }
