@@ -42,7 +42,7 @@ int resolve_dev(const void *p, uint64_t bytes, const char *what);
 
 // Library-owned device scratch that grows on demand (slot = purpose id).
 // Contents are not preserved across growth.
-enum Scratch { S_X = 0, S_Y, S_XB, S_H, S_YE, S_RL, S_SEL, S_W, S_PLAN, S_MISC, S_COUNT };
+enum Scratch { S_X = 0, S_Y, S_XB, S_H, S_YE, S_RL, S_SEL, S_W, S_PLAN, S_MISC, S_LIST, S_Q, S_COUNT };
 int scratch(Scratch slot, uint64_t bytes, void **p);
 
 // Bytes per element class for a tensor view.
@@ -82,6 +82,13 @@ struct DevLayer {
 // Shape/layout checks of a layer description (no pointer access, no HIP).
 int validate_layer(const mh_moe_layer *L);
 int resolve_layer(const mh_moe_layer *L, DevLayer *out);
+
+// Expert-major prefill with scaled MFMA (mh_prefill.hip): the routed
+// experts of n tokens into ye[n * k][hidden] (slot order); the caller adds
+// them to x with the prefill combine.
+bool prefill_mfma_ok(const DevLayer &L);
+int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32_t *sel, float *ye,
+                          hipStream_t s);
 
 // One-launch decode step for a whole stack at batch 1 (mh_decode.hip).
 struct StepPlan;

@@ -377,7 +377,8 @@ int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uin
 
 int run_expert_major(const DevLayer &L, int n, const float *xb, const int32_t *sel, const float *w, float *x,
                      const LayerBufs &b, hipStream_t s) {
-    MH_TRY(launch_experts(L, n * L.top_k, sel, xb, b.h, b.ye, s));
+    if (prefill_mfma_ok(L)) MH_TRY(run_expert_major_mfma(L, n, xb, sel, b.ye, s));
+    else MH_TRY(launch_experts(L, n * L.top_k, sel, xb, b.h, b.ye, s));
     MH_LAUNCH("combine_prefill", k_combine_prefill, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s,
                        x, b.ye, sel, w, L.hidden, L.top_k);
     return hip_check(hipGetLastError(), "prefill combine launch");

@@ -28,6 +28,18 @@ SHAPES = {
 _LIVE: list = []
 
 
+@pytest.fixture(params=["mfma", "gemv"])
+def prefill_path(request, monkeypatch):
+    """The expert-major prefill runs the scaled-MFMA grouped GEMM for MXFP4
+    experts; MIDGE_HIP_NO_MFMA=1 selects the per-assignment GEMV kernels.
+    Both must match the oracle."""
+    if request.param == "gemv":
+        monkeypatch.setenv("MIDGE_HIP_NO_MFMA", "1")
+    else:
+        monkeypatch.delenv("MIDGE_HIP_NO_MFMA", raising=False)
+    return request.param
+
+
 @pytest.fixture(autouse=True)
 def _release_layers():
     """Unregister every layer a test built, pass or fail (a stale region would
@@ -117,9 +129,9 @@ def test_moe_dev_batch(mh, batch):
 
 
 @pytest.mark.parametrize("name", ["tiny", "mid"])
-def test_prefill_vs_oracle(mh, name):
+def test_prefill_vs_oracle(mh, name, prefill_path):
     shape = SHAPES[name]
-    say(f"prefill {name} 40 tokens")
+    say(f"prefill {name} 40 tokens, {prefill_path}")
     keys, arrays, lay, L = build(shape, 4)
     X = synth.host_x(shape, keys, 40, step=3)
     xp, selp, wp = moe_prefill(lay, X)
@@ -156,13 +168,13 @@ def test_topk_dev_ties_and_edges(mh):
         d.free()
 
 
-def test_cfg3_prefill_512_tokens_sampled(mh):
+def test_cfg3_prefill_512_tokens_sampled(mh, prefill_path):
     # expert-major prefill at gpt-oss-20b shape: 512 tokens, 32 experts, top-4,
     # router logits ~N(0,1) given directly; every token on the GPU, a sample of
     # tokens on the oracle (tokens are independent), plus usage counts
     shape = SHAPES["gptoss20b"]
     n = 512
-    say("cfg3 prefill 512 tokens")
+    say(f"cfg3 prefill 512 tokens, {prefill_path}")
     keys, arrays, lay, L = build(shape, 31)
     X = synth.host_x(shape, keys, n, step=7)
     logits = synth.synth_normal(synth.hash64_int(keys.seed, 99), n * shape.n_experts,
