@@ -201,6 +201,8 @@ def run_gpu(args, shape):
                "bytes": gu_bytes_per_launch(shape, args.batch * k), "avg_us": kern["expert_gu"]["avg_us"]}
     dom["GBps"] = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
     extra["gemv"] = gemv_probe(ev, s)
+    if not args.no_prefill:
+        extra["prefill"] = prefill_probe(ev, s, args.seed)
     for b in bufs:
         b.free()
     st.destroy()
@@ -235,6 +237,79 @@ def gemv_probe(ev, s, rows: int = 262144, cols: int = 2880, reps: int = 20) -> d
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"kernel": "gemv (MXFP4)", "shape": [rows, cols], "bytes": nbytes, "avg_us": ms * 1e3,
             "GBps": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS}
+
+
+MFMA_FP8_PEAK_TFLOPS = 5000.0   # dense fp8 MFMA (the rate of fp4 x fp8 operands)
+
+
+def prefill_probe(ev, s, seed: int, n: int = 512, reps: int = 10) -> dict:
+    """Expert-major prefill of one gpt-oss-20b MoE layer (32 MXFP4 experts
+    2880x2880, top-4) for 512 tokens routed by N(0,1) logits: the grouped
+    scaled-MFMA GEMM path and, for comparison, the per-assignment GEMV path.
+    Timed with HIP events over `reps` calls of mh_expert_major_dev."""
+    import midge_amd
+    from midge_amd import DevBuf, _lib, synth
+    from midge_amd.device import profile_enable, profile_query, profile_reset
+    from midge_amd.moe import Stack, expert_major_dev, topk_dev
+    from midge_amd.synth import MoEShape
+    shape = MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4, n_layers=1)
+    st, bufs, keys = Stack.synthetic(shape, seed + 3, 1)
+    lay = st.layers[0]
+    H, E, k = shape.hidden, shape.n_experts, shape.top_k
+    logits, xb, x = DevBuf(n * E * 4), DevBuf(n * H * 4), DevBuf(n * H * 4)
+    _lib.call("mh_synth_normal_dev", logits.ptr, n * E, synth.hash64_int(keys.x, 77), float(synth.normal_c(1.0)))
+    _lib.call("mh_synth_normal_dev", xb.ptr, n * H, synth.hash64_int(keys.x, 78), float(synth.normal_c(1.0)))
+    _lib.call("mh_synth_normal_dev", x.ptr, n * H, synth.hash64_int(keys.x, 79), float(synth.normal_c(1.0)))
+    sel, w = DevBuf(n * k * 4), DevBuf(n * k * 4)
+    topk_dev(logits, n, E, k, 1, sel, w)
+    counts = np.bincount(sel.download(np.int32, (n, k)).ravel(), minlength=E)
+    out = {"workload": f"one gpt-oss-20b MoE layer, {n} tokens, {E} MXFP4 experts 2880x2880, top-{k}",
+           "tokens_per_expert": {"min": int(counts.min()), "max": int(counts.max()), "mean": float(counts.mean())}}
+    weights = E * shape.layout.expert_stride
+    useful_flops = 2.0 * n * k * 3 * shape.hidden * shape.ffn
+    for path in ("mfma", "gemv"):
+        if path == "gemv":
+            os.environ["MIDGE_HIP_NO_MFMA"] = "1"
+        try:
+            r = reps if path == "mfma" else 2
+            expert_major_dev(lay, n, xb, sel, w, x)
+            midge_amd.sync()
+            a, b = ev.event(), ev.event()
+            ev.record(a, s)
+            for _ in range(r):
+                expert_major_dev(lay, n, xb, sel, w, x)
+            ev.record(b, s)
+            ms = ev.elapsed_ms(a, b) / r
+            res = {"ms": ms, "tok_per_s": n / (ms * 1e-3), "weight_GBps": weights / (ms * 1e-3) / 1e9}
+            if path == "mfma":
+                profile_reset()
+                profile_enable(True)
+                expert_major_dev(lay, n, xb, sel, w, x)
+                midge_amd.sync()
+                kern = {}
+                for name in ("plist", "quant_x", "moe_gu_mfma", "quant_h", "moe_down_mfma", "combine_prefill"):
+                    tot, cnt = profile_query(name)
+                    if cnt:
+                        kern[name] = {"us": 1e3 * tot, "launches": cnt}
+                profile_enable(False)
+                gemm_us = sum(kern[n_]["us"] for n_ in ("moe_gu_mfma", "moe_down_mfma") if n_ in kern)
+                tiles = int(sum(-(-int(c) // 32) for c in counts))          # 32-token tiles over experts
+                issued = 2.0 * tiles * 32 * 3 * shape.hidden * shape.ffn * 3   # 3 matrices x 3 activation terms
+                res.update({"kernels": kern, "useful_TFLOPs": useful_flops / (ms * 1e-3) / 1e12,
+                            "gemm_issued_TFLOPs": issued / (gemm_us * 1e-6) / 1e12 if gemm_us else None,
+                            "mfma_util_of_fp8_peak": issued / (gemm_us * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFLOPS
+                            if gemm_us else None})
+            out[path] = res
+        finally:
+            os.environ.pop("MIDGE_HIP_NO_MFMA", None)
+    out["speedup_mfma_vs_gemv"] = out["gemv"]["ms"] / out["mfma"]["ms"]
+    for d in (logits, xb, x, sel, w):
+        d.free()
+    st.destroy()
+    for d in bufs:
+        d.free()
+    log(f"prefill cfg3: mfma {out['mfma']['ms']:.3f} ms, gemv {out['gemv']['ms']:.3f} ms")
+    return out
 
 
 def run_cpu(shape, seed: int, seconds: float):
@@ -288,6 +363,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b16", action="store_true", help="skip the extra batch-16 measurement")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the expert-major prefill measurement")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device twice (byte-counter calibration)")
     args = ap.parse_args()

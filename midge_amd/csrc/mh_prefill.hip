@@ -45,7 +45,7 @@ namespace mh {
 namespace {
 
 constexpr int kTerms = 3;      // fp8 terms per activation
-constexpr int kNT = 2;         // 32-token tiles per pass (weights loaded once per pass)
+constexpr int kNT = 4;         // 32-token tiles per pass (weights loaded once per pass)
 constexpr int kWaves = 4;      // 32-row tiles per block (one per wave)
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -164,38 +164,76 @@ __device__ __forceinline__ int e8m0_of_f16(uint32_t h, unsigned *bad) {
     return (int)((f >> 23) & 0xFFu);  // a zero scale (an e8m0 below f16's range) becomes 2^-127
 }
 
+// LDS of the GEMM block: two buffers of one K step's B operands for every
+// (term, token tile, half, lane) as 16-byte pieces, their scales, and one
+// 32 x 33 transpose tile per wave.
+constexpr int kBPieces = kTerms * kNT * 2 * 64;              // 16-byte pieces per K step
+constexpr int kBScales = kTerms * kNT * 64;                  // scale bytes per K step
+constexpr int kPiecesPerThread = kBPieces / (64 * kWaves);   // 6
+constexpr int kScalesPerThread = (kBScales + 64 * kWaves - 1) / (64 * kWaves);
+constexpr size_t kGemmLds = 2 * (size_t)kBPieces * 16 + 2 * (size_t)kBScales + sizeof(float) * kWaves * 32 * 33;
+static_assert(kBPieces % (64 * kWaves) == 0, "B pieces must split evenly over the block");
+
 // MODE 0: gate/up (K = H, rows = F, B rows = tokens through list_tok);
 // MODE 1: down (K = F, rows = H, B rows = list positions).
+// Block = (expert, 4 row tiles of 32), one wave per row tile; the expert's
+// tokens in passes of up to kNT 32-token tiles. Per K step the block stages
+// B (all terms and tiles) in LDS, double-buffered: step s+1 is loaded from
+// memory while step s's MFMAs run; each wave keeps its A (weight) chunks two
+// steps ahead in registers.
 template <int MODE>
 __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
-    __shared__ float tile[kWaves][32][33];
+    extern __shared__ __attribute__((aligned(16))) uint8_t glds[];
+    mh_u4 *bbuf = (mh_u4 *)glds;                                    // [2][kBPieces]
+    uint8_t *sbuf = glds + 2 * (size_t)kBPieces * 16;                // [2][kBScales]
+    float(*tiles)[32][33] = (float(*)[32][33])(sbuf + 2 * kBScales);
     const int K = MODE == 0 ? A.H : A.F;
     const int R = MODE == 0 ? A.F : A.H;
     const int RT = R / 32;
     const int groups = (RT + kWaves - 1) / kWaves;
     const int e = blockIdx.x / groups, rgrp = blockIdx.x - e * groups;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int rt = rgrp * kWaves + wave;
-    if (rt >= RT) return;   // no block-wide synchronisation below
+    const bool wact = rt < RT;                 // inactive waves still stage B
     const int base = A.offs[e], T = A.offs[e + 1] - base;
-    if (T == 0) return;
+    if (T == 0) return;                        // block-uniform
     const int m = l & 31, g = l >> 5;
-    const int row = rt * 32 + m;
+    const int row = (wact ? rt : 0) * 32 + m;
     const uint8_t *ex = A.experts + (uint64_t)e * A.stride;
     const int rowbytes = K / 2, nsc = K / 32, steps = K / 64;
     const uint8_t *a0 = ex + A.off[MODE == 0 ? 0 : 6] + (size_t)row * rowbytes;
     const uint16_t *s0 = (const uint16_t *)(ex + A.off[MODE == 0 ? 1 : 7]) + (size_t)row * nsc;
-    const uint8_t *a1 = ex + A.off[3] + (size_t)row * rowbytes;              // up (MODE 0)
+    const uint8_t *a1 = ex + A.off[3] + (size_t)row * rowbytes;
     const uint16_t *s1 = (const uint16_t *)(ex + A.off[4]) + (size_t)row * nsc;
     unsigned bad = 0;
-    float(*tl)[33] = tile[wave];
+    float(*tl)[33] = tiles[wave];
     for (int p0 = 0; p0 < T; p0 += 32 * kNT) {
         const int nt = min(kNT, (T - p0 + 31) / 32);
-        int brow[kNT];
+        // this thread's B pieces: q = tid + 256 i -> (term, tile, half, lane)
+        const uint8_t *bsrc[kPiecesPerThread];
 #pragma unroll
-        for (int j = 0; j < kNT; ++j) {
-            const int p = p0 + 32 * j + m;
-            brow[j] = (j < nt && p < T) ? (MODE == 0 ? A.list_tok[base + p] : base + p) : -1;
+        for (int i = 0; i < kPiecesPerThread; ++i) {
+            const int q = tid + 64 * kWaves * i;
+            const int lane = q & 63, half = (q >> 6) & 1, j = (q >> 7) % kNT, t = q / (128 * kNT);
+            const int p = p0 + 32 * j + (lane & 31);
+            int br = -1;
+            if (j < nt && p < T) br = MODE == 0 ? A.list_tok[base + p] : base + p;
+            bsrc[i] = br < 0 ? nullptr
+                             : A.bq + ((size_t)t * A.b_rows + br) * K + 16 * (lane >> 5) + 32 * half;
+        }
+        const uint8_t *ssrc[kScalesPerThread];
+#pragma unroll
+        for (int i = 0; i < kScalesPerThread; ++i) {
+            const int q = tid + 64 * kWaves * i;
+            ssrc[i] = nullptr;
+            if (q < kBScales) {
+                const int lane = q & 63, j = (q >> 6) % kNT, t = q / (64 * kNT);
+                const int p = p0 + 32 * j + (lane & 31);
+                if (j < nt && p < T) {
+                    const int br = MODE == 0 ? A.list_tok[base + p] : base + p;
+                    ssrc[i] = A.bs + ((size_t)t * A.b_rows + br) * nsc + (lane >> 5);
+                }
+            }
         }
         v16f acc0[kNT], acc1[kNT];
 #pragma unroll
@@ -203,75 +241,133 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
             acc0[j] = v16f{};
             acc1[j] = v16f{};
         }
-        for (int s = 0; s < steps; ++s) {
-            const int c = 2 * s + g;
-            v8i qa0 = {}, qa1 = {};
-            const mh_u4 w0 = mh_load16(mh_global(a0 + c * 16));
-            qa0[0] = (int)w0.x; qa0[1] = (int)w0.y; qa0[2] = (int)w0.z; qa0[3] = (int)w0.w;
-            const int sa0 = e8m0_of_f16(mh_load_u16(mh_global(s0 + c)), &bad);
-            int sa1 = 127;
+        // stage step 0
+        {
+            mh_u4 rb[kPiecesPerThread];
+            uint32_t rs[kScalesPerThread];
+#pragma unroll
+            for (int i = 0; i < kPiecesPerThread; ++i)
+                rb[i] = bsrc[i] ? *(const mh_u4 *)bsrc[i] : mh_u4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < kScalesPerThread; ++i) rs[i] = ssrc[i] ? *ssrc[i] : 0u;
+#pragma unroll
+            for (int i = 0; i < kPiecesPerThread; ++i) bbuf[tid + 64 * kWaves * i] = rb[i];
+#pragma unroll
+            for (int i = 0; i < kScalesPerThread; ++i)
+                if (tid + 64 * kWaves * i < kBScales) sbuf[tid + 64 * kWaves * i] = (uint8_t)rs[i];
+        }
+        // A for steps 0 and 1
+        mh_u4 wa0[3], wa1[3];
+        uint32_t ws0[3], ws1[3];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int c = 2 * min(u, steps - 1) + g;
+            wa0[u] = mh_load16(mh_global(a0 + c * 16));
+            ws0[u] = mh_load_u16(mh_global(s0 + c));
             if constexpr (MODE == 0) {
-                const mh_u4 w1 = mh_load16(mh_global(a1 + c * 16));
-                qa1[0] = (int)w1.x; qa1[1] = (int)w1.y; qa1[2] = (int)w1.z; qa1[3] = (int)w1.w;
-                sa1 = e8m0_of_f16(mh_load_u16(mh_global(s1 + c)), &bad);
-            }
-#pragma unroll
-            for (int t = 0; t < kTerms; ++t) {
-#pragma unroll
-                for (int j = 0; j < kNT; ++j) {
-                    if (j >= nt) break;
-                    v8i qb = {};
-                    int sb = 0;
-                    if (brow[j] >= 0) {
-                        const uint8_t *bp = A.bq + ((size_t)t * A.b_rows + brow[j]) * K + 64 * s + 16 * g;
-                        const uint4 lo = *(const uint4 *)bp, hi = *(const uint4 *)(bp + 32);
-                        qb[0] = (int)lo.x; qb[1] = (int)lo.y; qb[2] = (int)lo.z; qb[3] = (int)lo.w;
-                        qb[4] = (int)hi.x; qb[5] = (int)hi.y; qb[6] = (int)hi.z; qb[7] = (int)hi.w;
-                        sb = A.bs[((size_t)t * A.b_rows + brow[j]) * nsc + c];
-                    }
-                    acc0[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa0, qb, acc0[j], 4, 0, 0, sa0, 0, sb);
-                    if constexpr (MODE == 0)
-                        acc1[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa1, qb, acc1[j], 4, 0, 0, sa1, 0, sb);
-                }
+                wa1[u] = mh_load16(mh_global(a1 + c * 16));
+                ws1[u] = mh_load_u16(mh_global(s1 + c));
             }
         }
-        // epilogue through the wave's LDS tile: lane (m, g) owns column m
-        // (token p0 + 32 j + m) and rows 8 (i / 4) + 4 g + i % 4; after the
-        // transpose lane l writes rows 32 rt + (l & 31) of tokens (l >> 5) + 2 q
+        __syncthreads();
+        for (int s = 0; s < steps; ++s) {
+            const int cur = s & 1;
+            // memory for step s+1 (B pieces, into registers) and step s+2 (A)
+            mh_u4 rb[kPiecesPerThread];
+            uint32_t rs[kScalesPerThread];
+            const bool more = s + 1 < steps;
 #pragma unroll
-        for (int j = 0; j < kNT; ++j) {
-            if (j >= nt) break;
+            for (int i = 0; i < kPiecesPerThread; ++i)
+                rb[i] = (more && bsrc[i]) ? *(const mh_u4 *)(bsrc[i] + 64 * (s + 1)) : mh_u4{0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int rr = 8 * (i / 4) + 4 * g + (i % 4);
-                const size_t grow4 = (size_t)(rt * 32 + rr) * 4;
-                float v;
+            for (int i = 0; i < kScalesPerThread; ++i) rs[i] = (more && ssrc[i]) ? ssrc[i][2 * (s + 1)] : 0u;
+            {
+                const int c = 2 * min(s + 2, steps - 1) + g;
+                wa0[(s + 2) % 3] = mh_load16(mh_global(a0 + c * 16));
+                ws0[(s + 2) % 3] = mh_load_u16(mh_global(s0 + c));
                 if constexpr (MODE == 0) {
-                    float gg = acc0[j][i] + *(const float *)(ex + A.off[2] + grow4);
-                    float uu = acc1[j][i] + *(const float *)(ex + A.off[5] + grow4);
-                    if (A.act_plain) {
-                        v = gg / (1.0f + expf(-gg)) * uu;
-                    } else {
-                        if (gg > A.limit) gg = A.limit;
-                        if (uu > A.limit) uu = A.limit;
-                        if (uu < -A.limit) uu = -A.limit;
-                        v = gg / (1.0f + expf(-A.alpha * gg)) * (uu + 1.0f);
+                    wa1[(s + 2) % 3] = mh_load16(mh_global(a1 + c * 16));
+                    ws1[(s + 2) % 3] = mh_load_u16(mh_global(s1 + c));
+                }
+            }
+            if (wact) {
+                const int u = s % 3;
+                v8i qa0 = {}, qa1 = {};
+                qa0[0] = (int)wa0[u].x; qa0[1] = (int)wa0[u].y; qa0[2] = (int)wa0[u].z; qa0[3] = (int)wa0[u].w;
+                const int sa0 = e8m0_of_f16(ws0[u], &bad);
+                int sa1 = 127;
+                if constexpr (MODE == 0) {
+                    qa1[0] = (int)wa1[u].x; qa1[1] = (int)wa1[u].y; qa1[2] = (int)wa1[u].z; qa1[3] = (int)wa1[u].w;
+                    sa1 = e8m0_of_f16(ws1[u], &bad);
+                }
+                const mh_u4 *bb = bbuf + (size_t)cur * kBPieces;
+                const uint8_t *sb8 = sbuf + (size_t)cur * kBScales;
+#pragma unroll
+                for (int t = 0; t < kTerms; ++t) {
+#pragma unroll
+                    for (int j = 0; j < kNT; ++j) {
+                        if (j >= nt) break;
+                        const mh_u4 lo = bb[((t * kNT + j) * 2 + 0) * 64 + l];
+                        const mh_u4 hi = bb[((t * kNT + j) * 2 + 1) * 64 + l];
+                        const v8i qb = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+                        const int sbv = sb8[(t * kNT + j) * 64 + l];
+                        acc0[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa0, qb, acc0[j], 4, 0, 0, sa0, 0, sbv);
+                        if constexpr (MODE == 0)
+                            acc1[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa1, qb, acc1[j], 4, 0, 0, sa1, 0, sbv);
                     }
-                } else {
-                    v = acc0[j][i] + *(const float *)(ex + A.off[8] + grow4);
-                }
-                tl[m][rr] = v;   // [token][row]
-            }
-            __builtin_amdgcn_wave_barrier();
-            for (int q = 0; q < 16; ++q) {
-                const int tok = 2 * q + g, p = p0 + 32 * j + tok;
-                if (p < T) {
-                    const float v = tl[tok][m];
-                    if constexpr (MODE == 0) A.hbuf[(size_t)(base + p) * A.F + rt * 32 + m] = v;
-                    else A.ye[(size_t)A.slot_of[base + p] * A.H + rt * 32 + m] = v;
                 }
             }
-            __builtin_amdgcn_wave_barrier();
+            if (more) {
+                mh_u4 *nb = bbuf + (size_t)(cur ^ 1) * kBPieces;
+#pragma unroll
+                for (int i = 0; i < kPiecesPerThread; ++i) nb[tid + 64 * kWaves * i] = rb[i];
+                uint8_t *ns = sbuf + (size_t)(cur ^ 1) * kBScales;
+#pragma unroll
+                for (int i = 0; i < kScalesPerThread; ++i)
+                    if (tid + 64 * kWaves * i < kBScales) ns[tid + 64 * kWaves * i] = (uint8_t)rs[i];
+            }
+            __syncthreads();
+        }
+        if (wact) {
+            // epilogue through the wave's LDS tile: lane (m, g) owns column m
+            // (token p0 + 32 j + m) and rows 8 (i / 4) + 4 g + i % 4; after the
+            // transpose lane l writes row 32 rt + m of tokens 2 q + g
+#pragma unroll
+            for (int j = 0; j < kNT; ++j) {
+                if (j >= nt) break;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int rr = 8 * (i / 4) + 4 * g + (i % 4);
+                    const size_t grow4 = (size_t)(rt * 32 + rr) * 4;
+                    float v;
+                    if constexpr (MODE == 0) {
+                        float gg = acc0[j][i] + *(const float *)(ex + A.off[2] + grow4);
+                        float uu = acc1[j][i] + *(const float *)(ex + A.off[5] + grow4);
+                        if (A.act_plain) {
+                            v = gg / (1.0f + expf(-gg)) * uu;
+                        } else {
+                            if (gg > A.limit) gg = A.limit;
+                            if (uu > A.limit) uu = A.limit;
+                            if (uu < -A.limit) uu = -A.limit;
+                            v = gg / (1.0f + expf(-A.alpha * gg)) * (uu + 1.0f);
+                        }
+                    } else {
+                        v = acc0[j][i] + *(const float *)(ex + A.off[8] + grow4);
+                    }
+                    tl[m][rr] = v;   // [token][row]
+                }
+                __builtin_amdgcn_wave_barrier();
+                for (int q = 0; q < 16; ++q) {
+                    const int tok = 2 * q + g, p = p0 + 32 * j + tok;
+                    if (p < T) {
+                        const float v = tl[tok][m];
+                        if constexpr (MODE == 0) A.hbuf[(size_t)(base + p) * A.F + rt * 32 + m] = v;
+                        else A.ye[(size_t)A.slot_of[base + p] * A.H + rt * 32 + m] = v;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
         }
     }
     if (bad) atomicOr(A.err, 1u);
@@ -298,6 +394,12 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
                           hipStream_t s) {
     const int k = L.top_k, E = L.n_experts, N = n * k;
     const int H = (int)L.hidden, F = (int)L.ffn;
+    static bool lds_set = false;
+    if (!lds_set) {
+        MH_HIP(hipFuncSetAttribute((const void *)k_moe_gemm<0>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds));
+        MH_HIP(hipFuncSetAttribute((const void *)k_moe_gemm<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds));
+        lds_set = true;
+    }
     if (!g_scale_err) {
         MH_HIP(hipHostMalloc((void **)&g_scale_err, sizeof(unsigned), hipHostMallocMapped));
         *g_scale_err = 0;
@@ -351,7 +453,7 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
         MH_LAUNCH("quant_x", k_quant_terms, dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, xb, nullptr, n, H,
                   q, q + (size_t)kTerms * n * H);
         const int groups = (F / 32 + kWaves - 1) / kWaves;
-        MH_LAUNCH("moe_gu_mfma", k_moe_gemm<0>, dim3((unsigned)(E * groups)), dim3(64 * kWaves), 0, s, A);
+        MH_LAUNCH("moe_gu_mfma", k_moe_gemm<0>, dim3((unsigned)(E * groups)), dim3(64 * kWaves), kGemmLds, s, A);
     }
     // down over the quantized h (list order)
     {
@@ -362,7 +464,7 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
         MH_LAUNCH("quant_h", k_quant_terms, dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, hbuf, nullptr, N,
                   F, q, q + (size_t)kTerms * N * F);
         const int groups = (H / 32 + kWaves - 1) / kWaves;
-        MH_LAUNCH("moe_down_mfma", k_moe_gemm<1>, dim3((unsigned)(E * groups)), dim3(64 * kWaves), 0, s, A);
+        MH_LAUNCH("moe_down_mfma", k_moe_gemm<1>, dim3((unsigned)(E * groups)), dim3(64 * kWaves), kGemmLds, s, A);
     }
     return hip_check(hipGetLastError(), "prefill MFMA launches");
 }
