@@ -17,7 +17,7 @@
 namespace mh {
 
 constexpr int kGemvU = 4;          // row iterations in flight per thread
-constexpr int kGemvThreads = 1024;
+constexpr int kGemvThreads = 512;
 
 // Slots per block for C chunks per row and the thread count that covers them.
 inline void gemv_shape(int C, int *ns, int *nt) {
@@ -28,8 +28,8 @@ inline void gemv_shape(int C, int *ns, int *nt) {
     *nt = t;
 }
 
-// LDS floats needed by block_gemv for ns slots of C chunks.
-inline size_t gemv_lds_floats(int ns, int C) { return (size_t)kGemvU * ns * C; }
+// LDS floats needed by block_gemv for ns slots of C chunks (two buffers).
+inline size_t gemv_lds_floats(int ns, int C) { return (size_t)2 * kGemvU * ns * C; }
 
 // Row source for block_gemv: flat row f -> (data pointer, scale pointer).
 // `scale` is the f16 group scales for 4-bit types, unused otherwise.
@@ -37,49 +37,6 @@ struct RowRef {
     const uint8_t *data;
     const uint16_t *scale;
 };
-
-// Computes res[f] = sum over chunks of dot(row f, x) for f in [0, nf).
-// For 4-bit types the f16 group scale is applied per chunk (exact: powers of
-// two commute with rounding; non-power-of-two scales multiply the group's
-// partial sum once, as the reference does). For int8 the per-row scale is the
-// caller's. `xr` holds this thread's E elements of x; `red` is LDS of
-// gemv_lds_floats(ns, C); `res` is LDS of at least nf floats.
-// Must be called by every thread of the block.
-template <int DT, class RowFn>
-__device__ __forceinline__ void block_gemv(RowFn rowref, int nf, int C, int ns, const float *xr,
-                                           float *red, float *res) {
-    const int t = threadIdx.x;
-    const int slot = t / C, c = t - slot * C;
-    const bool active = slot < ns;
-    for (int f0 = 0; f0 < nf; f0 += ns * kGemvU) {
-        // Branch-free loads: rows past nf and idle slots re-read a row the
-        // block loads anyway (a cache hit) and are masked out below. Scales
-        // stay raw f16 bits here: converting inside this loop would make
-        // every iteration wait for its load.
-        mh_u4 q[kGemvU];
-        uint32_t sb[kGemvU];
-        const int sl = active ? slot : ns - 1;
-#pragma unroll
-        for (int u = 0; u < kGemvU; ++u) {
-            const int f = min(f0 + u * ns + sl, nf - 1);
-            const RowRef rr = rowref(f);
-            q[u] = mh_load16(mh_global(rr.data + (size_t)c * 16));
-            if constexpr (DT == MH_DT_MXFP4 || DT == MH_DT_Q4G32) sb[u] = mh_load_u16(mh_global(rr.scale + c));
-            else sb[u] = 0x3C00u;   // f16 1.0: int8 / f32 rows are scaled by the caller
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < kGemvU; ++u) {
-            const bool valid = active && f0 + u * ns + slot < nf;
-            const float p = mh_dot_chunk<DT>(q[u], xr) * (valid ? mh_f16((uint16_t)sb[u]) : 0.f);
-            if (active) red[(u * ns + slot) * C + c] = p;
-        }
-        __syncthreads();
-        // row it = u * ns + slot is flat row f0 + it
-        block_reduce_rows(red, C, kGemvU * ns, res + f0, [&](int it) { return f0 + it < nf; });
-        __syncthreads();
-    }
-}
 
 // Sums each row of red[nrows][C] (row-major) into out[row]. A wave takes 8
 // rows at a time: 8 lanes per row each add every 8th partial, then three
@@ -99,6 +56,75 @@ __device__ __forceinline__ void block_reduce_rows(const float *red, int C, int n
         s += __shfl_xor(s, 4, 64);
         if (part == 0 && r < nrows && keep(r)) out[r] = s;
     }
+}
+
+// One step's loads: U row iterations of this thread's chunk (branch-free:
+// rows past nf and idle slots re-read the block's last row, a cache hit,
+// and are masked out in the math). Scale bits stay raw f16 here: converting
+// inside the load loop would make every iteration wait for its load.
+template <int DT, int U, class RowFn>
+__device__ __forceinline__ void gemv_load(RowFn rowref, int f0, int nf, int c, int sl, int ns, mh_u4 *q,
+                                          uint32_t *sb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int f = min(f0 + u * ns + sl, nf - 1);
+        const RowRef rr = rowref(f);
+        q[u] = mh_load16(mh_global(rr.data + (size_t)c * 16));
+        if constexpr (DT == MH_DT_MXFP4 || DT == MH_DT_Q4G32) sb[u] = mh_load_u16(mh_global(rr.scale + c));
+        else sb[u] = 0x3C00u;   // f16 1.0: int8 / f32 rows are scaled by the caller
+    }
+}
+
+// One step's math: partial dot products of this thread's chunk into red.
+template <int DT, int U>
+__device__ __forceinline__ void gemv_math(const mh_u4 *q, const uint32_t *sb, const float *xr, int f0, int nf,
+                                          int slot, int c, int C, int ns, bool active, float *red) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const bool valid = active && f0 + u * ns + slot < nf;
+        const float p = mh_dot_chunk<DT>(q[u], xr) * (valid ? mh_f16((uint16_t)sb[u]) : 0.f);
+        if (active) red[(u * ns + slot) * C + c] = p;
+    }
+}
+
+// Computes res[f] = sum over chunks of dot(row f, x) for f in [0, nf).
+// For 4-bit types the f16 group scale is applied per chunk (exact: powers of
+// two commute with rounding; non-power-of-two scales multiply the group's
+// partial sum once, as the reference does). For int8 the per-row scale is the
+// caller's. `xr` holds this thread's E elements of x; `red` is LDS of
+// gemv_lds_floats(ns, C) (two buffers); `res` is LDS of at least nf floats.
+// Software-pipelined two deep: while step i (U rows per slot) is computed,
+// synchronised and reduced, the loads of step i + 1 are in flight. Must be
+// called by every thread.
+template <int DT, int U = kGemvU, class RowFn>
+__device__ __forceinline__ void block_gemv(RowFn rowref, int nf, int C, int ns, const float *xr,
+                                           float *red, float *res) {
+    const int t = threadIdx.x;
+    const int slot = t / C, c = t - slot * C;
+    const bool active = slot < ns;
+    const int sl = active ? slot : ns - 1;
+    const int step = ns * U;
+    const int per = U * ns * C;   // floats of one red buffer
+    mh_u4 qa[U], qb[U];
+    uint32_t sa[U], sbb[U];
+    if (nf <= 0) return;
+    gemv_load<DT, U>(rowref, 0, nf, c, sl, ns, qa, sa);
+    for (int f0 = 0; f0 < nf; f0 += 2 * step) {
+        // even step f0 from qa; odd step f0 + step from qb
+        const bool odd = f0 + step < nf;
+        if (odd) gemv_load<DT, U>(rowref, f0 + step, nf, c, sl, ns, qb, sbb);
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_math<DT, U>(qa, sa, xr, f0, nf, slot, c, C, ns, active, red);
+        __syncthreads();
+        block_reduce_rows(red, C, step, res + f0, [&](int it) { return f0 + it < nf; });
+        if (!odd) break;
+        if (f0 + 2 * step < nf) gemv_load<DT, U>(rowref, f0 + 2 * step, nf, c, sl, ns, qa, sa);
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_math<DT, U>(qb, sbb, xr, f0 + step, nf, slot, c, C, ns, active, red + per);
+        __syncthreads();
+        block_reduce_rows(red + per, C, step, res + f0 + step, [&](int it) { return f0 + step + it < nf; });
+    }
+    __syncthreads();
 }
 
 // Load this thread's E elements of x (zeros for idle threads).
