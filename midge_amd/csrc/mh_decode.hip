@@ -10,13 +10,17 @@
 //   route         block 0 gathers the tagged logits, ranks them (stable
 //                 top-k, ties to the lower index) and publishes the routing
 //                 record (expert, weight per slot) as tagged words, which
-//                 every other block polls.
+//                 every other block polls (one poller per word: polling by
+//                 every block congests the lines it polls).
 //   B  gate/up    each block takes an even share of the routed experts'
 //                 (gate, up) row pairs, with the bias + clamped SwiGLU
 //                 epilogue -> h[k][ffn]; then a grid barrier.
-//   C  down       each block owns a slice of output rows for all k experts;
-//                 their weights are loaded into registers between the
-//                 barrier's arrive and wait. Epilogue: y = Wd h + bd,
+//   C  down       each block owns a slice of output rows for all k experts.
+//                 MXFP4 stacks: the rows are loaded during the barrier,
+//                 staged in LDS and multiplied on the matrix cores (f16 MFMA
+//                 over h split into two f16 terms); otherwise they are
+//                 loaded into registers between the barrier's arrive and wait
+//                 and multiplied on the vector ALUs. Epilogue: y = Wd h + bd,
 //                 moe = sum_i w_i y_i in selection order, x += moe, written
 //                 as tagged words for the next layer (plain floats after the
 //                 last layer).
@@ -24,8 +28,9 @@
 // 64-bit store, so a consumer needs no separate barrier: it polls the words
 // it needs until every tag matches. The one full barrier per layer (before
 // the down phase, which needs all of h) is a gather/broadcast over per-block
-// flags. Every wait is bounded: one that does not complete within ~1 s raises
-// an error flag and every block exits.
+// flags (measured faster than every block polling every flag). Every wait is
+// bounded: one that does not complete within ~1 s raises an error flag and
+// every block exits.
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -59,7 +64,9 @@ struct StepArgs {
     uint64_t *lw;            // [E] tagged logits
     uint64_t *rec;           // [K] tagged routing record (block 0 -> all)
     uint64_t *xw;            // [H] tagged x between layers
-    float *h;                // [K][F] scratch
+    float *h;                // [K][F] scratch (VALU path)
+    uint16_t *h16;           // [2][K][Fpad] f16 planes of h (MFMA path)
+    int Fpad;                // ffn rounded up to 128
     unsigned *flags;         // [gridDim.x] barrier flags
     unsigned *go;            // barrier release word (written by block 0)
     unsigned seq0;           // first sequence number of this launch (3 per layer)
@@ -78,6 +85,11 @@ constexpr int kNX = 8;          // x elements per thread in the router phase (H 
 constexpr unsigned kSpinLimit = 1u << 20;
 constexpr int kStamps = 24;     // phase timestamps per layer and block while profiling
 constexpr int kEL = 2;          // logits per lane in the routing wave (E <= 64 * kEL)
+// static LDS capacities of the one-launch step (plan creation checks a
+// stack against them)
+constexpr int kHMax = 3072;         // hidden size
+constexpr int kResMax = 1024;       // floats of reduced rows
+constexpr int kRedMax = 8192;       // floats of partial sums
 
 // Memory access. Every load goes through a buffer resource (32-bit offsets,
 // out-of-range reads return 0). Weights are streamed with the nontemporal
@@ -320,25 +332,77 @@ __device__ __forceinline__ RouterPref prefetch_router(const StepArgs &A, int l, 
     return p;
 }
 
-template <int RDT, int XDT>
+// ---------------------------------------------------------------- MFMA
+// The down projection of an MXFP4 stack runs on V_MFMA_F32_16X16X32_F16
+// (measured layout on gfx950: lane l holds A row l % 16 and B column l % 16,
+// 8 consecutive K values 8 (l / 16) .. +7 each; output lane l holds column
+// l % 16 of rows 4 (l / 16) + i).
+//   A  16 of the block's down rows (rows of different routed experts may
+//      share a tile), e2m1 converted to f16 with the chunk's power-of-two
+//      scale, which is exact (the plan scans every scale)
+//   B  h split into two f16 terms (hi = h rounded, lo = h - hi rounded:
+//      within 2^-22 |h|), written by the producing block as two planes;
+//      column 2 i + term holds routed slot i's term, so a B operand is one
+//      16-byte load and row rho's dot product is columns 2 i + 0, 2 i + 1 of
+//      its slot i summed
+// A K step of 128 = 4 lane groups x 32 takes one 16-byte MXFP4 chunk per
+// lane group: lane (m, g) converts dword j of its chunk for the step's j-th
+// MFMA, and B lane (n, g) supplies elements 8 j .. 8 j + 7 of the same chunk.
+// The weights cannot be loaded in this lane layout directly (16 rows x 64 B
+// per instruction streams from HBM ~25% slower than whole rows), so they are
+// loaded as whole rows and staged through LDS.
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kQ = 3;                  // 128-column K steps per wave (ffn <= 8 * kQ * 128)
+constexpr int kKPad = 8 * kQ * 128;    // largest padded ffn
+constexpr int kRTC = 3;                // down row tiles (k * rows per block <= 48)
+constexpr int kSD = kKPad / 32 + 1;    // LDS row stride (chunks) of the staged down rows
+
+__device__ __forceinline__ v8h fp4x8_f16(uint32_t w, float s) {
+    const v2h a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0);
+    const v2h b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1);
+    const v2h c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2);
+    const v2h d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3);
+    return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ uint32_t dword_of(const mh_u4 &q, int j) {
+    return j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+}
+// v of lane + K within the lane's row of 16 (0 past the row's end)
+template <int K>
+__device__ __forceinline__ float dpp_shl(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + K, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void st_dev16(rsrc_t r, uint32_t off, uint16_t v) {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kDev);
+}
+
+template <int RDT, int XDT, bool MF>
 __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
     constexpr int XE = mh_chunk<XDT>::E;   // elements per expert chunk (32)
     constexpr int RE = mh_chunk<RDT>::E;   // elements per router chunk (16 int8 / 4 f32)
-    extern __shared__ float lds[];
+    // LDS is static (capacities are checked at plan creation).
     __shared__ float s_part[16];
     __shared__ int s_sel[16];
     __shared__ float s_w[16];
     __shared__ float s_val[16];
     __shared__ int s_ok;
+    __shared__ __attribute__((aligned(16))) float s_xs[kHMax];       // x at layer start
+    // xb = rmsnorm(x) * w in 32-element groups padded to 33 floats: thread c
+    // reads group c element by element, and the padding puts the 64 lanes of
+    // a wave in 64 distinct LDS banks
+    __shared__ __attribute__((aligned(16))) float s_xbs[kHMax / 32 * 33];
+    __shared__ __attribute__((aligned(16))) float s_res[kResMax];    // reduced rows / staged logits
+    __shared__ __attribute__((aligned(16))) float s_red[kRedMax];    // partial sums
+    __shared__ __attribute__((aligned(16))) float s_bds[kThreads];   // [K][rows of this block's down slice]
+    // MFMA path: the block's down rows ([16 kRTC rows][kSD chunks]) and scales
+    __shared__ __attribute__((aligned(16))) uint8_t s_dw[MF ? 16 * kRTC * kSD * 16 : 16];
+    __shared__ uint16_t s_ds[MF ? 16 * kRTC * kSD : 2];
     const int H = A.H, F = A.F, E = A.E, K = A.K;
-    // xb = rmsnorm(x) * w is kept in 32-element groups padded to 33 floats:
-    // thread c reads group c element by element, and the padding puts the
-    // 64 lanes of a wave in 64 distinct LDS banks.
-    float *xs = lds;                   // x at layer start
-    float *xbs = xs + H;               // xb, padded: element i at (i / 32) * 33 + i % 32
-    float *res = xbs + (H / 32) * 33;  // reduced rows / staged logits
-    float *red = res + A.res_floats;
-    float *bds = red + A.red_floats;   // [K][rows of this block's down slice]
+    float *xs = s_xs, *xbs = s_xbs, *res = s_res, *red = s_red, *bds = s_bds;
     const int NB = gridDim.x, b = blockIdx.x, t = threadIdx.x;
     const int wave = t >> 6;
 
@@ -352,6 +416,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
     const uint32_t layer_bytes = (uint32_t)((uint64_t)E * A.stride - 1u) + 1u;   // < 4 GiB (plan check)
     const int CR = H / RE;   // router chunks per row
     RouterPref pf = prefetch_router<RDT>(A, 0, CR);
+    const rsrc_t rh16 = make_rsrc(A.h16, (uint32_t)(2 * K * A.Fpad) * 2u);
     for (int l = 0; l < A.n_layers; ++l) {
         const StepLayer Ly = A.layers[l];
         // sequence numbers of this layer: logits and routing record, the
@@ -517,6 +582,9 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
 
         // ------------------------------------------------ B: gate/up
         const rsrc_t rex = make_rsrc(Ly.experts, layer_bytes);
+        mh_u4 qd[kUC];       // this thread's down rows (loaded in phase B, used in phase C)
+        uint32_t sd[kUC];
+        float bd_pref = 0.f;
         {
             // Rows come in (gate, up) pairs: pair p of the k experts laid end
             // to end is row p % F of expert p / F. The block takes pairs
@@ -584,25 +652,208 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 __builtin_amdgcn_sched_barrier(0);   // one pair's math at a time
             }
             MH_STAMP(10);
+            if constexpr (!MF) {
+                // the gate/up weight registers are free: start the down slice
+                // now, so it streams in during the reduction, the epilogue and
+                // the barrier (branch-free: out-of-range rows re-read row 0 of
+                // the slice, idle slots and unfilled routing slots the first
+                // routed expert; all are masked out in the math)
+                const int CD = A.CF, nsC = kThreads / CD, spe = nsC / K;
+                const int td = opaque(t);
+                const int dslot = td / CD, dc = td - dslot * CD;
+                const int di = dslot / spe, dsub = dslot - di * spe;
+                const int de = di < K ? s_sel[di] : -1;
+                const int ea = de >= 0 ? de : max(s_sel[0], 0);
+                const uint32_t eo = (uint32_t)ea * (uint32_t)A.stride;
+                const int RC = (H + NB - 1) / NB, r_begin = b * RC;
+                const int nr = max(0, min(H, r_begin + RC) - r_begin);
+                const int rows_ok = nr > 0 ? nr : 1, r0 = min(r_begin, H - 1);
+#pragma unroll
+                for (int u = 0; u < kUC; ++u) {
+                    const int j = min(dsub + spe * u, rows_ok - 1);
+                    const uint32_t rc = (uint32_t)((r0 + j) * CD + dc);
+                    qd[u] = ld_w16(rex, eo + (uint32_t)A.off[6] + rc * 16u);
+                    sd[u] = ld_w2(rex, eo + (uint32_t)A.off[7] + rc * 2u);
+                }
+                if (t < K * nr) {   // the down biases: (expert ib, row jb) -> thread ib * nr + jb
+                    const int ib = t / nr, jb = t - ib * nr;
+                    const int eb = s_sel[ib];
+                    if (eb >= 0)
+                        bd_pref = ld_f(rex, (uint32_t)eb * (uint32_t)A.stride + (uint32_t)A.off[8] +
+                                                (uint32_t)(r_begin + jb) * 4u);
+                }
+            }
             __syncthreads();
             block_reduce_rows(red, C, 2 * np, res, [](int) { return true; });
             __syncthreads();
             MH_STAMP(11);
-            // epilogue: pair t -> h (np <= F <= kThreads pairs: one per thread)
-            if (t < np) {
-                const int pr = rb + t;
-                const bool second = pr >= F;
-                const int e = second ? e_b : e_a;
-                float hv = 0.f;
-                if (e >= 0) hv = act_fn(res[2 * t] + bg_pref, res[2 * t + 1] + bu_pref, A.alpha, A.limit, A.act_plain);
-                st_dev(A.h + (size_t)(second ? ia + 1 : ia) * F + (second ? pr - F : pr), hv);
+            if constexpr (MF) {
+                if (wave == 0) {
+                    // epilogue (np <= 64: one pair per lane): h as two f16
+                    // planes, hi = h rounded, lo = (h - hi) rounded; then
+                    // arrive as soon as this wave's stores are complete
+                    if (t < np) {
+#pragma clang fp contract(off)
+                        const int pr = rb + t;
+                        const bool second = pr >= F;
+                        const int e = second ? e_b : e_a;
+                        float hv = 0.f;
+                        if (e >= 0)
+                            hv = act_fn(res[2 * t] + bg_pref, res[2 * t + 1] + bu_pref, A.alpha, A.limit, A.act_plain);
+                        const _Float16 hi = (_Float16)hv;
+                        const _Float16 lo = (_Float16)(hv - (float)hi);
+                        const uint32_t o = (uint32_t)((second ? ia + 1 : ia) * A.Fpad + (second ? pr - F : pr));
+                        st_dev16(rh16, o * 2u, __builtin_bit_cast(uint16_t, hi));
+                        st_dev16(rh16, ((uint32_t)(K * A.Fpad) + o) * 2u, __builtin_bit_cast(uint16_t, lo));
+                    }
+                    __builtin_amdgcn_s_waitcnt(0);
+                    if (t == 0)
+                        __hip_atomic_store(&A.flags[b], tagB, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    // waves 1.. load the block's down rows (whole rows per
+                    // instruction: thread (slot, chunk)) while the barrier
+                    // completes, then stage them in LDS as row rho = i * RC + j
+                    // at a stride of SD chunks (odd: the MFMA lanes' 16 rows
+                    // fall in distinct banks)
+                    const int CD = A.CF, SD = CD | 1, nsC = (kThreads - 64) / CD, spe = nsC / K;
+                    const int RC = (H + NB - 1) / NB, r_begin = b * RC;
+                    const int nr = max(0, min(H, r_begin + RC) - r_begin);
+                    if (nr > 0) {
+                        const int td = opaque(t) - 64;
+                        const int dslot = td / CD, dc = td - dslot * CD;
+                        const int di = dslot / spe, dsub = dslot - di * spe;
+                        const int de = di < K ? s_sel[di] : -1;
+                        const int ea = de >= 0 ? de : max(s_sel[0], 0);
+                        const uint32_t eo = (uint32_t)ea * (uint32_t)A.stride;
+#pragma unroll
+                        for (int u = 0; u < kUC; ++u) {
+                            const uint32_t rc = (uint32_t)((r_begin + min(dsub + spe * u, nr - 1)) * CD + dc);
+                            qd[u] = ld_w16(rex, eo + (uint32_t)A.off[6] + rc * 16u);
+                            sd[u] = ld_w2(rex, eo + (uint32_t)A.off[7] + rc * 2u);
+                        }
+                        // the down biases: (expert ib, row jb) -> thread 64 + ib * nr + jb
+                        const int tb = min(td, K * nr - 1);
+                        const int ib = tb / nr, jb = tb - ib * nr;
+                        const int eb = s_sel[ib];
+                        const float bdv = ld_f(rex, (uint32_t)max(eb, 0) * (uint32_t)A.stride + (uint32_t)A.off[8] +
+                                                        (uint32_t)(r_begin + jb) * 4u);
+                        if (di < K) {
+#pragma unroll
+                            for (int u = 0; u < kUC; ++u) {
+                                const int j = dsub + spe * u;
+                                if (j < nr) {
+                                    const int o = (di * RC + j) * SD + dc;
+                                    *(mh_u4 *)(s_dw + (size_t)o * 16) = qd[u];
+                                    s_ds[o] = (uint16_t)sd[u];
+                                }
+                            }
+                        }
+                        if (td < K * nr) bds[td] = eb >= 0 ? bdv : 0.f;
+                    }
+                }
+            } else {
+                // epilogue: pair t -> h (np <= F <= kThreads pairs: one per thread)
+                if (t < np) {
+                    const int pr = rb + t;
+                    const bool second = pr >= F;
+                    const int e = second ? e_b : e_a;
+                    float hv = 0.f;
+                    if (e >= 0) hv = act_fn(res[2 * t] + bg_pref, res[2 * t + 1] + bu_pref, A.alpha, A.limit, A.act_plain);
+                    st_dev(A.h + (size_t)(second ? ia + 1 : ia) * F + (second ? pr - F : pr), hv);
+                }
             }
         }
         MH_STAMP(3);
-        bar_arrive(A.flags, tagB);
+        if constexpr (!MF) bar_arrive(A.flags, tagB);
 
         // ------------------------------------------------ C: down + combine
-        {
+        if constexpr (MF) {
+            const int CF = A.CF, NQC = (CF + 3) >> 2;
+            const int RC = (H + NB - 1) / NB, r_begin = b * RC;
+            const int nr = max(0, min(H, r_begin + RC) - r_begin);
+            const int rowsC = K * RC;
+            // a block without output rows reads no h (the next layer's
+            // producers may overwrite it as soon as every x row is in)
+            if (nr > 0 || b == 0) {
+                MH_STAMP(4);
+                if (!bar_wait(A.flags, A.go, tagB, A.err, &s_ok)) return;
+                MH_STAMP(5);
+                const int tt = opaque(t);
+                const int lane = tt & 63, m = lane & 15, g = lane >> 4;
+                const int wv = __builtin_amdgcn_readfirstlane(tt >> 6);
+                // B: column m = 2 i + term reads 8 values of plane (m & 1),
+                // slot i = m / 2
+                // (lanes of unused columns and K steps past the end read
+                // past the buffer, which returns zeros: no branch)
+                v8h hb[kQ][4];
+#pragma unroll
+                for (int u = 0; u < kQ; ++u) {
+                    const int q = kQ * wv + u;
+                    const bool use = q < NQC && m < 2 * K;
+                    const uint32_t e16 = (uint32_t)(((m & 1) * K + (m >> 1)) * A.Fpad + 128 * q + 32 * g);
+                    const uint32_t o = use ? e16 * 2u : 0x80000000u;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) hb[u][j] = __builtin_bit_cast(v8h, ld_dev16(rh16, o + 16u * j));
+                }
+                MH_STAMP(12);
+                v4f acc[kRTC];
+#pragma unroll
+                for (int rt = 0; rt < kRTC; ++rt) acc[rt] = v4f{0.f, 0.f, 0.f, 0.f};
+                const int SD = CF | 1;
+#pragma unroll
+                for (int u = 0; u < kQ; ++u) {
+                    const int q = kQ * wv + u;
+                    if (q >= NQC) break;
+                    const int c = min(4 * q + g, CF - 1);   // past F: B is zero
+#pragma unroll
+                    for (int rt = 0; rt < kRTC; ++rt) {
+                        if (16 * rt >= rowsC) break;
+                        const int o = min(16 * rt + m, rowsC - 1) * SD + c;
+                        const mh_u4 qa = *(const mh_u4 *)(s_dw + (size_t)o * 16);
+                        const float sc = mh_f16(s_ds[o]);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp4x8_f16(dword_of(qa, j), sc), hb[u][j],
+                                                                             acc[rt], 0, 0, 0);
+                    }
+                }
+                // row rho belongs to slot i = rho / RC: its columns 2 i, 2 i + 1
+                float *redw = red + wv * 48;
+#pragma unroll
+                for (int rt = 0; rt < kRTC; ++rt) {
+                    if (16 * rt >= rowsC) break;
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii) {
+                        const float v = acc[rt][ii];
+                        const float v1 = dpp_shl<1>(v);
+                        const int rho = 16 * rt + 4 * g + ii;
+                        if (rho < rowsC && m == 2 * (rho / RC)) redw[rho] = v + v1;
+                    }
+                }
+                MH_STAMP(13);
+                __syncthreads();
+                if (t < rowsC) {
+                    float sum = 0.f;
+#pragma unroll
+                    for (int w = 0; w < kThreads / 64; ++w) sum += red[w * 48 + t];
+                    res[t] = sum;
+                }
+                __syncthreads();
+                MH_STAMP(14);
+                for (int j = t; j < nr; j += kThreads) {
+#pragma clang fp contract(off)
+                    const int r = r_begin + j;
+                    float moe = 0.f;
+                    for (int ii = 0; ii < K; ++ii) {
+                        if (s_sel[ii] < 0) continue;
+                        const float y = res[ii * RC + j] + bds[ii * nr + j];
+                        moe = moe + s_w[ii] * y;
+                    }
+                    if (l + 1 < A.n_layers) st_tag(A.xw + r, tagC, xs[r] + moe);
+                    else st_dev(A.x + r, xs[r] + moe);
+                }
+            }
+        } else {
             // one pass (plan check): slot -> (expert i, row phase sub), rows
             // j = sub + spe * u of this block's slice
             const int C = A.CF;
@@ -616,29 +867,6 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             const int i = slot / spe, sub = slot - i * spe;
             const bool act = i < K;
             const int e = act ? s_sel[i] : -1;
-            // idle slots and unfilled routing slots read the first routed
-            // expert's rows (cache hits) and are masked out
-            const int ea = e >= 0 ? e : max(s_sel[0], 0);
-            const uint32_t eo = (uint32_t)ea * (uint32_t)A.stride;
-            mh_u4 q[kUC];
-            uint32_t sb[kUC];
-            const int rows_ok = nr > 0 ? nr : 1;
-            const int r0 = min(r_begin, H - 1);
-#pragma unroll
-            for (int u = 0; u < kUC; ++u) {
-                const int j = min(sub + spe * u, rows_ok - 1);
-                const uint32_t rc = (uint32_t)((r0 + j) * C + c);
-                q[u] = ld_w16(rex, eo + (uint32_t)A.off[6] + rc * 16u);
-                sb[u] = ld_w2(rex, eo + (uint32_t)A.off[7] + rc * 2u);
-            }
-            // the down biases of this block's rows, (expert ib, row jb) -> thread ib * nr + jb
-            float bd_pref = 0.f;
-            if (t < K * nr) {
-                const int ib = t / nr, jb = t - ib * nr;
-                const int eb = s_sel[ib];
-                if (eb >= 0)
-                    bd_pref = ld_f(rex, (uint32_t)eb * (uint32_t)A.stride + (uint32_t)A.off[8] + (uint32_t)(r_begin + jb) * 4u);
-            }
             __builtin_amdgcn_sched_barrier(0);
             MH_STAMP(4);
             if (!bar_wait(A.flags, A.go, tagB, A.err, &s_ok)) return;
@@ -660,7 +888,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             for (int u = 0; u < kUC; ++u) {
                 const int j = sub + spe * u;
                 const bool valid = e >= 0 && j < nr;
-                const float p = mh_dot_chunk<XDT>(q[u], xr) * (valid ? mh_f16((uint16_t)sb[u]) : 0.f);
+                const float p = mh_dot_chunk<XDT>(qd[u], xr) * (valid ? mh_f16((uint16_t)sd[u]) : 0.f);
                 if (act && j < nr) red[(i * RC + j) * C + c] = p;
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -695,9 +923,22 @@ __global__ void k_fill_u32(unsigned *p, int n, unsigned v) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
 }
 
-template <int RDT, int XDT>
+// Flags a down-projection MXFP4 scale that the MFMA path cannot apply
+// exactly in f16: it must be zero or a power of two in [2^-23, 2^13], so that
+// every e2m1 value times it is an f16.
+__global__ void k_scan_scales(const uint8_t *experts, uint64_t stride, uint64_t od, int n, unsigned *bad) {
+    const uint16_t *d = (const uint16_t *)(experts + (uint64_t)blockIdx.y * stride + od);
+    bool ok = true;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const unsigned v = d[i], e = (v >> 10) & 31u, mn = v & 1023u;
+        ok = ok && ((v & 0x7FFFu) == 0 || (e == 0 && mn >= 2 && (mn & (mn - 1)) == 0) || (e != 0 && e <= 28 && mn == 0));
+    }
+    if (!ok) atomicOr(bad, 1u);
+}
+
+template <int RDT, int XDT, bool MF>
 int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
-    auto k = k_decode_step<RDT, XDT>;
+    auto k = k_decode_step<RDT, XDT, MF>;
     MH_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     int per_cu = 0;
     MH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, lds));
@@ -735,6 +976,9 @@ struct StepPlan {
     unsigned *err = nullptr;       // host-mapped pinned [1]: set by a timed-out barrier
     unsigned *err_dev = nullptr;   // its device address
     float *h = nullptr;            // device [K][F]
+    uint16_t *h16 = nullptr;       // device [2][K][Fpad]
+    int Fpad = 0;
+    int mf = 0;                    // 1 = the MFMA path may run the expert GEMVs
     unsigned seq = 0;              // next barrier sequence number
     int nb = 0;
     int ok = 0;                    // 1 = eligible, 0 = not (reason recorded)
@@ -782,6 +1026,17 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
         const int RC = (H + nb - 1) / nb;
         if (spe < 1 || RC > spe * kUC || K * RC > kThreads) return reject("down phase does not fit one pass");
     }
+    // MFMA down path: MXFP4 experts, the clamped SwiGLU (|h| <= limit (limit +
+    // 1) fits f16), shapes within the tiles, exact f16 scales (scanned below)
+    {
+        const int H = (int)L0.hidden, F = (int)L0.ffn, K = L0.top_k;
+        const int RC = (H + nb - 1) / nb, PB = (K * F + nb - 1) / nb;
+        const int spe = K > 0 ? (kThreads - 64) / (F / 32) / K : 0;   // down rows in flight: waves 1..
+        const float lim = L0.limit;
+        p->mf = L0.expert_dt == MH_DT_MXFP4 && !L0.act_plain && lim >= 0.f && lim * (lim + 1.f) < 60000.f &&
+                F <= kKPad && K * RC <= 16 * kRTC && 2 * K <= 16 && PB <= 64 && spe >= 1 && RC <= spe * kUC &&
+                K * RC <= kThreads - 64;
+    }
     std::vector<StepLayer> host((size_t)n_layers);
     for (int l = 0; l < n_layers; l++) {
         const DevLayer &L = layers[l];
@@ -800,6 +1055,25 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     MH_HIP(hipMalloc(&p->tagged, sizeof(uint64_t) * p->tagged_words));
     MH_HIP(hipMemset(p->tagged, 0, sizeof(uint64_t) * p->tagged_words));
     MH_HIP(hipMalloc(&p->h, sizeof(float) * (size_t)L0.top_k * (size_t)L0.ffn));
+    p->Fpad = (int)((L0.ffn + 127) / 128 * 128);
+    MH_HIP(hipMalloc(&p->h16, sizeof(uint16_t) * 2 * (size_t)L0.top_k * (size_t)p->Fpad));
+    MH_HIP(hipMemset(p->h16, 0, sizeof(uint16_t) * 2 * (size_t)L0.top_k * (size_t)p->Fpad));   // the padding stays 0
+    if (p->mf) {
+        unsigned *bad = nullptr;
+        MH_HIP(hipMalloc(&bad, sizeof(unsigned)));
+        MH_HIP(hipMemset(bad, 0, sizeof(unsigned)));
+        const int n_dn = (int)(L0.hidden * (L0.ffn / 32));
+        for (int l = 0; l < n_layers; l++) {
+            const DevLayer &L = layers[l];
+            hipLaunchKernelGGL(k_scan_scales, dim3(16, (unsigned)L.n_experts), dim3(256), 0, 0, L.experts,
+                               L.expert_stride, L.off[7], n_dn, bad);
+        }
+        unsigned hb = 0;
+        MH_HIP(hipGetLastError());
+        MH_HIP(hipMemcpy(&hb, bad, sizeof(unsigned), hipMemcpyDeviceToHost));
+        (void)hipFree(bad);
+        if (hb) p->mf = 0;   // the VALU path handles any f16 scale
+    }
     MH_HIP(hipMemset(p->flags, 0, sizeof(unsigned) * (size_t)(nb + 64)));
     MH_HIP(hipDeviceSynchronize());
     p->seq = 1;
@@ -817,6 +1091,7 @@ void step_plan_destroy(StepPlan *p) {
     (void)hipHostFree(p->err);
     (void)hipFree(p->tagged);
     (void)hipFree(p->h);
+    (void)hipFree(p->h16);
     delete p;
 }
 
@@ -848,9 +1123,11 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     A.lw = p->tagged;
     A.rec = p->tagged + A.E;
     A.xw = p->tagged + A.E + 16;
-    A.h = p->h;
-    A.flags = p->flags;
     A.go = p->flags + ((p->nb + 63) / 32) * 32;   // a separate 128-byte line
+    A.h = p->h;
+    A.h16 = p->h16;
+    A.Fpad = p->Fpad;
+    A.flags = p->flags;
     A.trace = profiling() ? p->trace : nullptr;
     A.err = p->err_dev;
     const unsigned nbar = 3u * (unsigned)n_layers;
@@ -866,16 +1143,25 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     A.res_floats = std::max(64 * kEL, std::max(2 * PB, A.K * RC)) + 64;
     const int nsB = kThreads / A.CH;
     A.red_floats = std::max(2 * nsB * kUP * A.CH, A.K * RC * A.CF);
-    const size_t lds = ((size_t)A.H + (size_t)(A.H / 32) * 33 + A.res_floats + A.red_floats + (size_t)A.K * RC) *
-                       sizeof(float);
-    if (lds > 160 * 1024) return fail(MH_E_UNSUPPORTED, "decode step needs %zu B of LDS", lds);
+    if (A.H > kHMax || A.res_floats > kResMax || A.red_floats > kRedMax)
+        return fail(MH_E_UNSUPPORTED, "decode step: shape exceeds the kernel's LDS capacities");
+    const size_t lds = 0;
+    const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two paths
+    const bool mf = p->mf && !(nm && nm[0] && nm[0] != '0');
     int rc;
-    if (L0.router.dt == MH_DT_Q8R)
-        rc = L0.expert_dt == MH_DT_MXFP4 ? launch_t<MH_DT_Q8R, MH_DT_MXFP4>(A, nb, lds, s)
-                                         : launch_t<MH_DT_Q8R, MH_DT_Q4G32>(A, nb, lds, s);
-    else
-        rc = L0.expert_dt == MH_DT_MXFP4 ? launch_t<MH_DT_F32, MH_DT_MXFP4>(A, nb, lds, s)
-                                         : launch_t<MH_DT_F32, MH_DT_Q4G32>(A, nb, lds, s);
+    if (L0.router.dt == MH_DT_Q8R) {
+        if (L0.expert_dt == MH_DT_MXFP4)
+            rc = mf ? launch_t<MH_DT_Q8R, MH_DT_MXFP4, true>(A, nb, lds, s)
+                    : launch_t<MH_DT_Q8R, MH_DT_MXFP4, false>(A, nb, lds, s);
+        else
+            rc = launch_t<MH_DT_Q8R, MH_DT_Q4G32, false>(A, nb, lds, s);
+    } else {
+        if (L0.expert_dt == MH_DT_MXFP4)
+            rc = mf ? launch_t<MH_DT_F32, MH_DT_MXFP4, true>(A, nb, lds, s)
+                    : launch_t<MH_DT_F32, MH_DT_MXFP4, false>(A, nb, lds, s);
+        else
+            rc = launch_t<MH_DT_F32, MH_DT_Q4G32, false>(A, nb, lds, s);
+    }
     if (rc || !A.trace) return rc;
     // profiling: fold the per-block phase timestamps (100 MHz clock) into
     // the profile: the mean over blocks and the slowest block of each span
@@ -916,6 +1202,21 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
             lastR = std::max(lastR, at(l, 2, b));
             lastB = std::max(lastB, at(l, 3, b));
             lastC = std::max(lastC, at(l, 6, b));
+        }
+        // every stamp's earliest and latest block, from the layer's first start
+        static const int order[] = {0, 15, 1, 16, 17, 18, 2, 9, 10, 11, 3, 4, 5, 12, 13, 14, 6, 7};
+        for (int st : order) {
+            double lo = 1e300, hi = 0;
+            for (int b = 0; b < nb; b++) {
+                if (st >= 16 && b > 0) break;   // block 0 only
+                const double v = at(l, st, b) - t0;
+                lo = std::min(lo, v);
+                hi = std::max(hi, v);
+            }
+            snprintf(name, sizeof(name), "decode_step/t%02d.first", st);
+            prof_add(name, lo * 1e-5);
+            snprintf(name, sizeof(name), "decode_step/t%02d.last", st);
+            prof_add(name, hi * 1e-5);
         }
         prof_add("decode_step/crit_logits", (lastA - t0) * 1e-5);
         prof_add("decode_step/crit_routed", (lastR - t0) * 1e-5);
