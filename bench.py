@@ -177,7 +177,9 @@ def run_gpu(args, shape):
              "barrier_arrive_prefetch", "barrier_wait", "down_combine", "dn_hload", "dn_math", "dn_reduce",
              "dn_combine", "tail")
     phases = tuple(f"decode_step/{n}{m}" for n in spans for m in ("", ".max")) + tuple(
-        f"decode_step/crit_{n}" for n in ("logits", "routed", "h", "x"))
+        f"decode_step/crit_{n}" for n in ("logits", "routed", "h", "x")) + tuple(
+        f"decode_step/t{st:02d}.{w}" for st in (0, 15, 1, 16, 17, 18, 2, 9, 10, 11, 3, 4, 5, 12, 13, 14, 6, 7)
+        for w in ("first", "last"))
     for name in ("decode_step", "expert_gu", "expert_down", "gemv", "topk", "rmsnorm", "combine_decode") + phases:
         tot, n = profile_query(name)
         if n:

@@ -1146,6 +1146,9 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     if (A.H > kHMax || A.res_floats > kResMax || A.red_floats > kRedMax)
         return fail(MH_E_UNSUPPORTED, "decode step: shape exceeds the kernel's LDS capacities");
     const size_t lds = 0;
+    if (A.trace)   // stamps a block does not reach (a skipped phase) stay 0
+        MH_LAUNCH("fill", k_fill_u32, dim3(64), dim3(256), 0, s, (unsigned *)p->trace,
+                  (int)(2 * (size_t)kStamps * n_layers * p->nb), 0u);
     const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two paths
     const bool mf = p->mf && !(nm && nm[0] && nm[0] != '0');
     int rc;
@@ -1183,13 +1186,16 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
         for (const auto &sp : spans) {
             const int nbk = sp.b0 ? 1 : nb;
             double sum = 0, mx = 0;
+            int cnt = 0;
             for (int b = 0; b < nbk; b++) {
+                if (at(l, sp.b, b) == 0 || at(l, sp.a, b) == 0) continue;
                 const double d = at(l, sp.b, b) - at(l, sp.a, b);
                 sum += d;
                 mx = std::max(mx, d);
+                ++cnt;
             }
             snprintf(name, sizeof(name), "decode_step/%s", sp.name);
-            prof_add(name, sum / nbk * 1e-5);
+            prof_add(name, cnt ? sum / cnt * 1e-5 : 0.0);
             snprintf(name, sizeof(name), "decode_step/%s.max", sp.name);
             prof_add(name, mx * 1e-5);
         }
@@ -1209,6 +1215,7 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
             double lo = 1e300, hi = 0;
             for (int b = 0; b < nb; b++) {
                 if (st >= 16 && b > 0) break;   // block 0 only
+                if (at(l, st, b) == 0) continue;
                 const double v = at(l, st, b) - t0;
                 lo = std::min(lo, v);
                 hi = std::max(hi, v);
