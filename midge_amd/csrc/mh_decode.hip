@@ -306,30 +306,76 @@ __device__ __forceinline__ float act_fn(float g, float u, float alpha, float lim
 }
 
 // Phase A's inputs that do not depend on x, loaded ahead of time (for layer
-// 0 at kernel start, for layer l + 1 between layer l's last arrive and
-// wait): this block's first router row chunk, that row's scale and bias, and
-// the norm weights of this thread's x elements.
+// 0 at kernel start, for layer l + 1 after layer l's output): the elements
+// of this block's router row that this thread's x elements meet (as raw
+// bits: int8 or f32), that row's scale and bias, and the norm weights of
+// this thread's x elements.
 struct RouterPref {
-    mh_u4 rq;
+    uint32_t rw[kNX];
     float rs, rb;
     float nw[kNX];
 };
 
 template <int RDT>
-__device__ __forceinline__ RouterPref prefetch_router(const StepArgs &A, int l, int CR) {
+__device__ __forceinline__ RouterPref prefetch_router(const StepArgs &A, int l) {
     RouterPref p;
     const StepLayer Lp = A.layers[l];
-    const int b = blockIdx.x, t = threadIdx.x;
+    const int b = blockIdx.x, t = threadIdx.x, H = A.H;
     const int e = b < A.E ? b : 0;
-    const rsrc_t rw = make_rsrc(Lp.router_w, (uint32_t)A.E * (uint32_t)CR * 16u);
-    p.rq = ld_w16(rw, (uint32_t)(e * CR + min(t, CR - 1)) * 16u);
+    constexpr uint32_t wb = RDT == MH_DT_Q8R ? 1u : 4u;   // bytes per router weight
+    const rsrc_t rw = make_rsrc(Lp.router_w, (uint32_t)A.E * (uint32_t)H * wb);
+#pragma unroll
+    for (int k = 0; k < kNX; ++k) {   // past H: the next row's weights (or 0), met by x = 0
+        const uint32_t o = ((uint32_t)e * (uint32_t)H + (uint32_t)(t + k * kThreads)) * wb;
+        if constexpr (RDT == MH_DT_Q8R) p.rw[k] = __builtin_amdgcn_raw_buffer_load_b8(rw, o, 0, 0);
+        else p.rw[k] = __builtin_amdgcn_raw_buffer_load_b32(rw, o, 0, 0);
+    }
     p.rs = 1.0f;
     if constexpr (RDT == MH_DT_Q8R) p.rs = ld_f(make_rsrc(Lp.router_s, (uint32_t)A.E * 4u), (uint32_t)e * 4u);
     p.rb = ld_f(make_rsrc(Lp.router_b, (uint32_t)A.E * 4u), (uint32_t)e * 4u);
-    const rsrc_t rn = make_rsrc(Lp.norm_w, (uint32_t)A.H * 4u);
+    const rsrc_t rn = make_rsrc(Lp.norm_w, (uint32_t)H * 4u);
 #pragma unroll
     for (int k = 0; k < kNX; ++k) p.nw[k] = ld_f(rn, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
     return p;
+}
+
+template <int RDT>
+__device__ __forceinline__ float router_weight(uint32_t bits) {
+    if constexpr (RDT == MH_DT_Q8R) return (float)(int8_t)(uint8_t)bits;
+    else return __uint_as_float(bits);
+}
+
+// Sum over the wave with DPP (the result is valid in lane 63): within rows
+// of 16, then the row broadcasts; rows a step does not write add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add_step(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = dpp_add_step<0x141, 0xF>(v);   // row_half_mirror
+    v = dpp_add_step<0x140, 0xF>(v);   // row_mirror
+    v = dpp_add_step<0x142, 0xA>(v);   // row_bcast:15
+    v = dpp_add_step<0x143, 0xC>(v);   // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// Two sums over the block at once (all threads get them). `part` is LDS [16].
+__device__ __forceinline__ float2 block_sum2(float a, float c, float *part) {
+    a = wave_sum_dpp(a);
+    c = wave_sum_dpp(c);
+    if ((threadIdx.x & 63) == 0) {
+        part[2 * (threadIdx.x >> 6)] = a;
+        part[2 * (threadIdx.x >> 6) + 1] = c;
+    }
+    __syncthreads();
+    float sa = 0.f, sc = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
+        sa += part[2 * i];
+        sc += part[2 * i + 1];
+    }
+    __syncthreads();
+    return make_float2(sa, sc);
 }
 
 // ---------------------------------------------------------------- MFMA
@@ -415,7 +461,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
     const rsrc_t rh = make_rsrc(A.h, (uint32_t)K * (uint32_t)F * 4u);
     const uint32_t layer_bytes = (uint32_t)((uint64_t)E * A.stride - 1u) + 1u;   // < 4 GiB (plan check)
     const int CR = H / RE;   // router chunks per row
-    RouterPref pf = prefetch_router<RDT>(A, 0, CR);
+    RouterPref pf = prefetch_router<RDT>(A, 0);
     const rsrc_t rh16 = make_rsrc(A.h16, (uint32_t)(2 * K * A.Fpad) * 2u);
     for (int l = 0; l < A.n_layers; ++l) {
         const StepLayer Ly = A.layers[l];
@@ -464,11 +510,21 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 for (int k = 0; k < kNX; ++k) xv[k] = __uint_as_float((uint32_t)wv[k]);
             }
             MH_STAMP(15);
-            float ss = 0.f;
+            // the sum of squares and this block's logit in one pass: the
+            // row's dot with xb = x * inv * w is inv * (row . (x * w))
+            float ss = 0.f, dp = 0.f;
 #pragma unroll
-            for (int k = 0; k < kNX; ++k) ss = __builtin_fmaf(xv[k], xv[k], ss);
-            ss = block_sum(ss, s_part);
-            const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+            for (int k = 0; k < kNX; ++k) {
+                ss = __builtin_fmaf(xv[k], xv[k], ss);
+                dp = __builtin_fmaf(router_weight<RDT>(pf.rw[k]), xv[k] * pf.nw[k], dp);
+            }
+            const float2 sums = block_sum2(ss, dp, s_part);
+            const float inv = 1.0f / sqrtf(sums.x / (float)H + A.eps);
+            if (b < E && t == 0) {
+                float p = sums.y * inv;
+                if constexpr (RDT == MH_DT_Q8R) p *= pf.rs;
+                st_tag(A.lw + b, tagA, p + pf.rb);
+            }
 #pragma unroll
             for (int k = 0; k < kNX; ++k) {
                 const int i = t + k * kThreads;
@@ -479,23 +535,19 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             }
         }
         __syncthreads();
-        for (int e = b; e < E; e += NB) {
+        // router rows beyond the grid (more experts than blocks): over xb
+        for (int e = b + NB; e < E; e += NB) {
             float p = 0.f;
-            float rs = pf.rs, rb = pf.rb;
             const rsrc_t rw = make_rsrc(Ly.router_w, (uint32_t)E * (uint32_t)CR * 16u);
             for (int c = t; c < CR; c += kThreads) {
-                const mh_u4 q = (e == b && c == t) ? pf.rq : ld_w16(rw, (uint32_t)(e * CR + c) * 16u);
+                const mh_u4 q = ld_w16(rw, (uint32_t)(e * CR + c) * 16u);
                 const int i0 = c * RE;   // a router chunk lies inside one 32-element group
                 p += mh_dot_chunk<RDT>(q, xbs + (i0 >> 5) * 33 + (i0 & 31));
             }
             p = block_sum(p, s_part);
-            if (e != b) {
-                if constexpr (RDT == MH_DT_Q8R) rs = Ly.router_s[e];
-                rb = Ly.router_b[e];
-            }
             if (t == 0) {
-                if constexpr (RDT == MH_DT_Q8R) p *= rs;
-                st_tag(A.lw + e, tagA, p + rb);
+                if constexpr (RDT == MH_DT_Q8R) p *= Ly.router_s[e];
+                st_tag(A.lw + e, tagA, p + Ly.router_b[e]);
             }
         }
         MH_STAMP(1);
@@ -913,7 +965,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             }
         }
         MH_STAMP(6);
-        if (l + 1 < A.n_layers) pf = prefetch_router<RDT>(A, l + 1, CR);
+        if (l + 1 < A.n_layers) pf = prefetch_router<RDT>(A, l + 1);
         MH_STAMP(7);
     }
 #undef MH_STAMP
