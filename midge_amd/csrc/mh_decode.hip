@@ -196,7 +196,8 @@ __device__ __forceinline__ float block_sum(float v, float *part) {
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
     __syncthreads();
     float s = 0.f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s += part[i];
+#pragma unroll
+    for (int i = 0; i < kThreads / 64; ++i) s += part[i];
     __syncthreads();
     return s;
 }
@@ -234,13 +235,30 @@ __device__ __forceinline__ float wave_max(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Sum over the wave with DPP (the result is valid in lane 63): within rows
+// of 16, then the row broadcasts; rows a step does not write add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add_step(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = dpp_add_step<0x141, 0xF>(v);   // row_half_mirror
+    v = dpp_add_step<0x140, 0xF>(v);   // row_mirror
+    v = dpp_add_step<0x142, 0xA>(v);   // row_bcast:15
+    v = dpp_add_step<0x143, 0xC>(v);   // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 // Stable top-k over the wave's E <= 64 * kEL logits (lane holds element
 // lane + 64 j in v[j]; absent elements are -inf): k rounds of "largest
 // remaining value, lowest index among equals"; only values > -1e30
-// qualify, unfilled slots get -1 (engine/midge.c:476-486). Lane 0 writes
-// s_sel / s_val.
-__device__ __forceinline__ void wave_topk(float *v, int k, int *s_sel, float *s_val) {
+// qualify, unfilled slots get -1 (engine/midge.c:476-486). Lane i < k ends
+// with slot i's expert in *sel and its logit in *val (-1e30 if unfilled).
+__device__ __forceinline__ void wave_topk(float *v, int k, int *sel, float *val) {
     const int lane = threadIdx.x & 63;
+    *sel = -1;
+    *val = -1e30f;
     for (int i = 0; i < k; ++i) {
         float lm = -INFINITY;
 #pragma unroll
@@ -259,41 +277,33 @@ __device__ __forceinline__ void wave_topk(float *v, int k, int *s_sel, float *s_
             for (int j = 0; j < kEL; ++j)
                 if (j == (idx >> 6)) v[j] = -INFINITY;   // taken
         }
-        if (lane == 0) {
-            s_sel[i] = idx;
-            s_val[i] = idx >= 0 ? m : -1e30f;
+        if (lane == i) {
+            *sel = idx;
+            *val = idx >= 0 ? m : -1e30f;
         }
     }
 }
 
-// Routing weights for the selected slots (engine/midge.c:502-512), by one
-// wave: softmax over the k selected logits (router_norm) or the k entries of
-// the softmax over all E logits v[]. Lane 0 writes s_w.
-__device__ void wave_weights(const float *v, int E, int k, int router_norm, const float *s_val, float *s_w) {
-    const int lane = threadIdx.x & 63;
-    float fmx = 0.f, fden = 0.f;
-    if (!router_norm) {
-        float m = -INFINITY;
-        for (int e = lane; e < E; e += 64) m = fmaxf(m, v[e]);
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        float s = 0.f;
-        for (int e = lane; e < E; e += 64) s += expf(v[e] - m);
-        fden = mh_wave_sum(s);
-        fmx = m;
+// Routing weight of slot `lane` (engine/midge.c:502-512), by one wave from
+// wave_topk's per-lane results: softmax over the k selected logits
+// (router_norm; the denominator summed in slot order) or the slot's entry of
+// the softmax over all E logits (v: kEL per lane, -inf past E).
+__device__ __forceinline__ float wave_weight(const float *v, int k, int router_norm, float val) {
+    if (router_norm) {
+        const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(val), 0));
+        const float ex = expf(val - mx);
+        float den = 0.f;
+        for (int i = 0; i < k; ++i) den += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), i));
+        return ex / den;
     }
-    if (lane == 0) {
-        if (router_norm) {
-            const float mx = s_val[0];
-            float den = 0.f;
-            for (int i = 0; i < k; ++i) {
-                s_w[i] = expf(s_val[i] - mx);
-                den += s_w[i];
-            }
-            for (int i = 0; i < k; ++i) s_w[i] /= den;
-        } else {
-            for (int i = 0; i < k; ++i) s_w[i] = expf(s_val[i] - fmx) / fden;
-        }
-    }
+    float lm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kEL; ++j) lm = fmaxf(lm, v[j]);
+    const float m = wave_max(lm);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < kEL; ++j) sum += v[j] > -INFINITY ? expf(v[j] - m) : 0.f;
+    return expf(val - m) / wave_sum_dpp(sum);
 }
 
 __device__ __forceinline__ float act_fn(float g, float u, float alpha, float limit, int plain) {
@@ -345,21 +355,6 @@ __device__ __forceinline__ float router_weight(uint32_t bits) {
     else return __uint_as_float(bits);
 }
 
-// Sum over the wave with DPP (the result is valid in lane 63): within rows
-// of 16, then the row broadcasts; rows a step does not write add 0.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add_step(float v) {
-    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
-}
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v = dpp_add_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
-    v = dpp_add_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
-    v = dpp_add_step<0x141, 0xF>(v);   // row_half_mirror
-    v = dpp_add_step<0x140, 0xF>(v);   // row_mirror
-    v = dpp_add_step<0x142, 0xA>(v);   // row_bcast:15
-    v = dpp_add_step<0x143, 0xC>(v);   // row_bcast:31
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
 // Two sums over the block at once (all threads get them). `part` is LDS [16].
 __device__ __forceinline__ float2 block_sum2(float a, float c, float *part) {
     a = wave_sum_dpp(a);
@@ -370,7 +365,8 @@ __device__ __forceinline__ float2 block_sum2(float a, float c, float *part) {
     }
     __syncthreads();
     float sa = 0.f, sc = 0.f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
+#pragma unroll
+    for (int i = 0; i < kThreads / 64; ++i) {
         sa += part[2 * i];
         sc += part[2 * i + 1];
     }
@@ -434,7 +430,6 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
     __shared__ float s_part[16];
     __shared__ int s_sel[16];
     __shared__ float s_w[16];
-    __shared__ float s_val[16];
     __shared__ int s_ok;
     __shared__ __attribute__((aligned(16))) float s_xs[kHMax];       // x at layer start
     // xb = rmsnorm(x) * w in 32-element groups padded to 33 floats: thread c
@@ -584,23 +579,27 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                     }
                 }
                 MH_STAMP(16);
-                float v[kEL];
+                float v[kEL], v0[kEL];
 #pragma unroll
                 for (int j = 0; j < kEL; ++j) {
                     v[j] = lane + 64 * j < E ? __uint_as_float((uint32_t)wv[j]) : -INFINITY;
-                    res[lane + 64 * j] = v[j];   // all logits, for the softmax over all of them
+                    v0[j] = v[j];
                 }
-                wave_topk(v, K, s_sel, s_val);
+                int my_sel;
+                float my_val;
+                wave_topk(v, K, &my_sel, &my_val);
                 MH_STAMP(17);
-                wave_weights(res, E, K, A.router_norm, s_val, s_w);
+                const float my_w = wave_weight(v0, K, A.router_norm, my_val);
                 MH_STAMP(18);
                 if (lane < K) {
-                    __hip_atomic_store(A.rec + lane, rec_word(tagA, s_sel[lane], s_w[lane]), __ATOMIC_RELAXED,
+                    s_sel[lane] = my_sel;
+                    s_w[lane] = my_w;
+                    __hip_atomic_store(A.rec + lane, rec_word(tagA, my_sel, my_w), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
-                    if (A.sel) A.sel[(size_t)l * K + lane] = s_sel[lane];
-                    if (A.w) A.w[(size_t)l * K + lane] = s_w[lane];
-                    if (A.usage && s_sel[lane] >= 0)
-                        __hip_atomic_fetch_add(&A.usage[(size_t)l * E + s_sel[lane]], 1u, __ATOMIC_RELAXED,
+                    if (A.sel) A.sel[(size_t)l * K + lane] = my_sel;
+                    if (A.w) A.w[(size_t)l * K + lane] = my_w;
+                    if (A.usage && my_sel >= 0)
+                        __hip_atomic_fetch_add(&A.usage[(size_t)l * E + my_sel], 1u, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
                 }
             }

@@ -289,6 +289,62 @@ def test_stack_fused_step_vs_per_layer_and_oracle(mh, shape, layers):
     st.destroy()
 
 
+FUSED_VARIANTS = {
+    "softmax_all_logits": dict(router_norm=0),
+    "plain_silu": dict(act_plain=1),
+    "q4g32_experts": dict(expert_dt=_lib.DT_Q4G32),
+    "f32_router": dict(router_dt=_lib.DT_F32),
+}
+
+
+@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("variant", list(FUSED_VARIANTS))
+def test_stack_fused_step_variants(mh, variant, path):
+    """The one-launch step for the layer variants the reference supports
+    beside gpt-oss's (softmax over all logits, plain SiLU, q4 g32 experts, an
+    f32 router), on the matrix-core and the vector-ALU down path where the
+    variant allows the former: exact selection and x against the oracle."""
+    import dataclasses
+    import os
+    shape = dataclasses.replace(MoEShape(hidden=256, ffn=192, n_experts=16, top_k=4), **FUSED_VARIANTS[variant])
+    layers = 3
+    say(f"fused step variant {variant} path {path}")
+    keys = Keys(314)
+    lays, structs, keep = [], [], []
+    for l in range(layers):
+        ex = synth.host_layer_experts(shape, keys, l)
+        w, s, b, nw = synth.host_router(shape, keys, l)
+        if shape.router_dt == _lib.DT_F32:
+            w, s = (w.astype(np.float32) * s[:, None]).astype(np.float32), None
+        keep.append((ex, w, s, b, nw))
+        lays.append(MoELayer.host(shape, ex, w, s, b, nw))
+        _LIVE.append(lays[-1])
+        structs.append(po.layer_struct(shape, ex, w, s, b, nw))
+    if path == "valu":
+        os.environ["MIDGE_HIP_NO_MFMA"] = "1"
+    try:
+        st = Stack(lays, max_batch=1)
+        k = shape.top_k
+        for step in range(3):
+            x0 = synth.host_x(shape, keys, 1, step=step)
+            xd = DevBuf.from_array(x0)
+            sd = DevBuf(layers * k * 4)
+            st.decode(xd, 1, sd, None, None)
+            mh.sync()
+            xf = xd.download(np.float32, x0.shape)[0]
+            sf = sd.download(np.int32, (layers, k))
+            for d in (xd, sd):
+                d.free()
+            x = x0[0]
+            for l in range(layers):
+                x, selr, _ = po.moe_decode(structs[l], x)
+                assert (sf[l] == selr).all(), (step, l, sf[l], selr)
+            assert rel_l2(xf, x) < TOL, (step, rel_l2(xf, x))
+        st.destroy()
+    finally:
+        os.environ.pop("MIDGE_HIP_NO_MFMA", None)
+
+
 def test_stack_fused_step_ties_and_unfilled_slots(mh):
     """Routing edge cases through the one-launch step, against the per-layer
     launches and the oracle: 128 experts whose router rows repeat every 8
