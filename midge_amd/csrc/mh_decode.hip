@@ -422,6 +422,53 @@ __device__ __forceinline__ void st_dev16(rsrc_t r, uint32_t off, uint16_t v) {
     __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kDev);
 }
 
+// The down rows [0, rows) of the block's slice (row rho = i * RC + j: slot i,
+// row j), staged in LDS at a stride of SD chunks, times h's two f16 planes
+// (hb: this lane's B operands, loaded by the caller), NT = ceil(rows / 16)
+// row tiles; row rho's partial (columns 2 i, 2 i + 1 summed) goes to
+// red[w * 48 + rho].
+template <int NT>
+__device__ __forceinline__ void dn_mfma_t(const uint8_t *sw, const uint16_t *ss, const v8h (*hb)[4], int SD, int CF,
+                                          int rows, int RC, float *red) {
+    const int tt = opaque(threadIdx.x);
+    const int lane = tt & 63, m = lane & 15, g = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tt >> 6);
+    const int NQC = (CF + 3) >> 2;
+    v4f acc[NT];
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) acc[rt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kQ; ++u) {
+        const int q = kQ * wv + u;
+        if (q >= NQC) break;
+        const int c = min(4 * q + g, CF - 1);   // past F: B is zero
+        mh_u4 qa[NT];
+        float sc[NT];
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt) {
+            const int o = min(16 * rt + m, rows - 1) * SD + c;
+            qa[rt] = *(const mh_u4 *)(sw + (size_t)o * 16);
+            sc[rt] = mh_f16(ss[o]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp4x8_f16(dword_of(qa[rt], j), sc[rt]), hb[u][j], acc[rt],
+                                                                 0, 0, 0);
+    }
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const float v = acc[rt][ii];
+            const float v1 = dpp_shl<1>(v);
+            const int rho = 16 * rt + 4 * g + ii;
+            if (rho < rows && m == 2 * (rho / RC)) red[wv * 48 + rho] = v + v1;
+        }
+    }
+}
+
 template <int RDT, int XDT, bool MF>
 __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
     constexpr int XE = mh_chunk<XDT>::E;   // elements per expert chunk (32)
@@ -592,12 +639,15 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 const float my_w = wave_weight(v0, K, A.router_norm, my_val);
                 MH_STAMP(18);
                 if (lane < K) {
-                    s_sel[lane] = my_sel;
-                    s_w[lane] = my_w;
-                    __hip_atomic_store(A.rec + lane, rec_word(tagA, my_sel, my_w), __ATOMIC_RELAXED,
+                    // (addresses from an opaque lane: recomputed here, not
+                    // hoisted out of the layer loop and spilled)
+                    const int ln = opaque(lane);
+                    s_sel[ln] = my_sel;
+                    s_w[ln] = my_w;
+                    __hip_atomic_store(A.rec + ln, rec_word(tagA, my_sel, my_w), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
-                    if (A.sel) A.sel[(size_t)l * K + lane] = my_sel;
-                    if (A.w) A.w[(size_t)l * K + lane] = my_w;
+                    if (A.sel) A.sel[(size_t)l * K + ln] = my_sel;
+                    if (A.w) A.w[(size_t)l * K + ln] = my_w;
                     if (A.usage && my_sel >= 0)
                         __hip_atomic_fetch_add(&A.usage[(size_t)l * E + my_sel], 1u, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
@@ -847,39 +897,11 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                     for (int j = 0; j < 4; ++j) hb[u][j] = __builtin_bit_cast(v8h, ld_dev16(rh16, o + 16u * j));
                 }
                 MH_STAMP(12);
-                v4f acc[kRTC];
-#pragma unroll
-                for (int rt = 0; rt < kRTC; ++rt) acc[rt] = v4f{0.f, 0.f, 0.f, 0.f};
-                const int SD = CF | 1;
-#pragma unroll
-                for (int u = 0; u < kQ; ++u) {
-                    const int q = kQ * wv + u;
-                    if (q >= NQC) break;
-                    const int c = min(4 * q + g, CF - 1);   // past F: B is zero
-#pragma unroll
-                    for (int rt = 0; rt < kRTC; ++rt) {
-                        if (16 * rt >= rowsC) break;
-                        const int o = min(16 * rt + m, rowsC - 1) * SD + c;
-                        const mh_u4 qa = *(const mh_u4 *)(s_dw + (size_t)o * 16);
-                        const float sc = mh_f16(s_ds[o]);
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp4x8_f16(dword_of(qa, j), sc), hb[u][j],
-                                                                             acc[rt], 0, 0, 0);
-                    }
-                }
-                // row rho belongs to slot i = rho / RC: its columns 2 i, 2 i + 1
-                float *redw = red + wv * 48;
-#pragma unroll
-                for (int rt = 0; rt < kRTC; ++rt) {
-                    if (16 * rt >= rowsC) break;
-#pragma unroll
-                    for (int ii = 0; ii < 4; ++ii) {
-                        const float v = acc[rt][ii];
-                        const float v1 = dpp_shl<1>(v);
-                        const int rho = 16 * rt + 4 * g + ii;
-                        if (rho < rowsC && m == 2 * (rho / RC)) redw[rho] = v + v1;
-                    }
+                switch ((rowsC + 15) >> 4) {   // block-uniform (plan check: rows <= 16 kRTC)
+                case 1: dn_mfma_t<1>(s_dw, s_ds, hb, CF | 1, CF, rowsC, RC, red); break;
+                case 2: dn_mfma_t<2>(s_dw, s_ds, hb, CF | 1, CF, rowsC, RC, red); break;
+                case 3: dn_mfma_t<3>(s_dw, s_ds, hb, CF | 1, CF, rowsC, RC, red); break;
+                default: break;
                 }
                 MH_STAMP(13);
                 __syncthreads();
@@ -1194,14 +1216,14 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     A.res_floats = std::max(64 * kEL, std::max(2 * PB, A.K * RC)) + 64;
     const int nsB = kThreads / A.CH;
     A.red_floats = std::max(2 * nsB * kUP * A.CH, A.K * RC * A.CF);
+    const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two paths
+    const bool mf = p->mf && !(nm && nm[0] && nm[0] != '0');
     if (A.H > kHMax || A.res_floats > kResMax || A.red_floats > kRedMax)
         return fail(MH_E_UNSUPPORTED, "decode step: shape exceeds the kernel's LDS capacities");
     const size_t lds = 0;
     if (A.trace)   // stamps a block does not reach (a skipped phase) stay 0
         MH_LAUNCH("fill", k_fill_u32, dim3(64), dim3(256), 0, s, (unsigned *)p->trace,
                   (int)(2 * (size_t)kStamps * n_layers * p->nb), 0u);
-    const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two paths
-    const bool mf = p->mf && !(nm && nm[0] && nm[0] != '0');
     int rc;
     if (L0.router.dt == MH_DT_Q8R) {
         if (L0.expert_dt == MH_DT_MXFP4)
