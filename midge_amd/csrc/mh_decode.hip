@@ -7,11 +7,10 @@
 //                 sequence-tagged words), forms xb = rmsnorm(x) * w in LDS;
 //                 the router's rows are spread over the blocks and each
 //                 logit is published as a tagged word.
-//   route         block 0 gathers the tagged logits, ranks them (stable
-//                 top-k, ties to the lower index) and publishes the routing
-//                 record (expert, weight per slot) as tagged words, which
-//                 every other block polls (one poller per word: polling by
-//                 every block congests the lines it polls).
+//   route         every block gathers the tagged logits (from one of
+//                 kLR copies, so that few blocks poll each line) and ranks
+//                 them (stable top-k, ties to the lower index) itself: all
+//                 reach the same selection and weights, with no broadcast.
 //   B  gate/up    each block takes an even share of the routed experts'
 //                 (gate, up) row pairs, with the bias + clamped SwiGLU
 //                 epilogue -> h[k][ffn]; then a grid barrier.
@@ -61,8 +60,8 @@ struct StepArgs {
     int32_t *sel;            // [L][K] or null
     float *w;                // [L][K] or null
     uint32_t *usage;         // [L][E] or null
-    uint64_t *lw;            // [E] tagged logits
-    uint64_t *rec;           // [K] tagged routing record (block 0 -> all)
+    uint64_t *lw;            // [kLR][lws] tagged logits: kLR copies, lws words apart
+    int lws;
     uint64_t *xw;            // [H] tagged x between layers
     float *h;                // [K][F] scratch (VALU path)
     uint16_t *h16;           // [2][K][Fpad] f16 planes of h (MFMA path)
@@ -85,6 +84,9 @@ constexpr int kNX = 8;          // x elements per thread in the router phase (H 
 constexpr unsigned kSpinLimit = 1u << 20;
 constexpr int kStamps = 24;     // phase timestamps per layer and block while profiling
 constexpr int kEL = 2;          // logits per lane in the routing wave (E <= 64 * kEL)
+constexpr int kLR = 8;          // copies of the logits (each polled by NB / kLR blocks)
+constexpr int kGoCopies = 8;    // copies of the barrier's release word
+constexpr int kGoStride = 64;   // words between them (256 B)
 // static LDS capacities of the one-launch step (plan creation checks a
 // stack against them)
 constexpr int kHMax = 3072;         // hidden size
@@ -147,8 +149,9 @@ __device__ __forceinline__ void bar_arrive(unsigned *flags, unsigned seq) {
 }
 
 // Gather/broadcast wait: block 0's first wave polls every block's flag (one
-// load per lane per round) and then publishes `seq` in *go; every other
-// block polls that single word. Returns false (in every thread) if the
+// load per lane per round) and then publishes `seq` in the kGoCopies copies
+// of the release word; every other block polls copy b % kGoCopies (one word
+// polled by every block congests its line). Returns false (in every thread) if the
 // barrier timed out. Loads after the wait are issued only once it has
 // returned, so device-scope loads see every store made before the arrives.
 __device__ __forceinline__ bool bar_wait(const unsigned *flags, unsigned *go, unsigned seq, unsigned *err,
@@ -171,9 +174,11 @@ __device__ __forceinline__ bool bar_wait(const unsigned *flags, unsigned *go, un
                     break;
                 }
             }
-            if (ok && lane == 0) __hip_atomic_store(go, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (ok && lane < kGoCopies)
+                __hip_atomic_store(go + lane * kGoStride, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else if (lane == 0) {
-            while ((int)(__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - seq) < 0) {
+            const unsigned *g = go + (blockIdx.x % kGoCopies) * kGoStride;
+            while ((int)(__hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - seq) < 0) {
                 __builtin_amdgcn_s_sleep(1);
                 if (++spins > kSpinLimit) {
                     ok = false;
@@ -208,14 +213,6 @@ __device__ __forceinline__ void st_tag(uint64_t *p, unsigned tag, float v) {
 }
 __device__ __forceinline__ uint64_t ld_tag(uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Routing record word for slot i: 22 tag bits, 10 expert bits (0x3FF = an
-// unfilled slot), the weight's 32 bits.
-constexpr unsigned kRecTagMask = 0x3FFFFFu;
-__device__ __forceinline__ uint64_t rec_word(unsigned tag, int sel, float w) {
-    const uint64_t code = sel < 0 ? 0x3FFu : (uint64_t)sel;
-    return ((uint64_t)(tag & kRecTagMask) << 42) | (code << 32) | __float_as_uint(w);
 }
 
 // Maximum over the wave (every lane gets it): DPP within rows of 16, then
@@ -562,10 +559,10 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             }
             const float2 sums = block_sum2(ss, dp, s_part);
             const float inv = 1.0f / sqrtf(sums.x / (float)H + A.eps);
-            if (b < E && t == 0) {
+            if (b < E && t < kLR) {   // one copy per logit replica
                 float p = sums.y * inv;
                 if constexpr (RDT == MH_DT_Q8R) p *= pf.rs;
-                st_tag(A.lw + b, tagA, p + pf.rb);
+                st_tag(A.lw + (size_t)t * A.lws + b, tagA, p + pf.rb);
             }
 #pragma unroll
             for (int k = 0; k < kNX; ++k) {
@@ -587,27 +584,32 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 p += mh_dot_chunk<RDT>(q, xbs + (i0 >> 5) * 33 + (i0 & 31));
             }
             p = block_sum(p, s_part);
-            if (t == 0) {
+            if (t < kLR) {
                 if constexpr (RDT == MH_DT_Q8R) p *= Ly.router_s[e];
-                st_tag(A.lw + e, tagA, p + Ly.router_b[e]);
+                st_tag(A.lw + (size_t)t * A.lws + e, tagA, p + Ly.router_b[e]);
             }
         }
         MH_STAMP(1);
 
         // ------------------------------------------------ route
-        if (b == 0) {
-            // one wave gathers the logits (kEL per lane: element lane + 64 j),
-            // selects the stable top-k and publishes the routing record; the
-            // block's other waves wait at the barrier below
+        {
+            // Every block routes: its first wave gathers the logits from
+            // replica b % kLR (kEL per lane: element lane + 64 j) and selects
+            // the stable top-k and the weights, so no routing record has to
+            // be broadcast; all blocks reach the same selection from the same
+            // words. (One copy polled by every block congests its lines: 32
+            // pollers per copy do not.) The block's other waves wait at the
+            // barrier below.
             bool late = false;
             if (wave == 0) {
                 const int lane = t;
                 const int tt = opaque(t);
+                uint64_t *lr = A.lw + (size_t)(b % kLR) * A.lws;
                 uint64_t wv[kEL];
 #pragma unroll
                 for (int j = 0; j < kEL; ++j) {
                     const int e = tt + 64 * j;
-                    wv[j] = e < E ? ld_tag(A.lw + e) : (uint64_t)tagA << 32;
+                    wv[j] = e < E ? ld_tag(lr + e) : (uint64_t)tagA << 32;
                 }
                 for (unsigned spins = 0;; ++spins) {
                     bool ready = true;
@@ -622,7 +624,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
 #pragma unroll
                     for (int j = 0; j < kEL; ++j) {
                         const int e = tt + 64 * j;
-                        if (e < E && (unsigned)(wv[j] >> 32) != tagA) wv[j] = ld_tag(A.lw + e);
+                        if (e < E && (unsigned)(wv[j] >> 32) != tagA) wv[j] = ld_tag(lr + e);
                     }
                 }
                 MH_STAMP(16);
@@ -644,35 +646,14 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                     const int ln = opaque(lane);
                     s_sel[ln] = my_sel;
                     s_w[ln] = my_w;
-                    __hip_atomic_store(A.rec + ln, rec_word(tagA, my_sel, my_w), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                    if (A.sel) A.sel[(size_t)l * K + ln] = my_sel;
-                    if (A.w) A.w[(size_t)l * K + ln] = my_w;
-                    if (A.usage && my_sel >= 0)
-                        __hip_atomic_fetch_add(&A.usage[(size_t)l * E + my_sel], 1u, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            if (__syncthreads_or(late)) {
-                if (t == 0) __hip_atomic_store(A.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                return;
-            }
-        } else {
-            bool late = false;
-            const int tt = opaque(t);
-            if (tt < K) {
-                uint64_t w = ld_tag(A.rec + tt);
-                for (unsigned spins = 0; (unsigned)(w >> 42) != (tagA & kRecTagMask); ++spins) {
-                    if (spins > kSpinLimit) {
-                        late = true;
-                        break;
+                    if (b == 0) {
+                        if (A.sel) A.sel[(size_t)l * K + ln] = my_sel;
+                        if (A.w) A.w[(size_t)l * K + ln] = my_w;
+                        if (A.usage && my_sel >= 0)
+                            __hip_atomic_fetch_add(&A.usage[(size_t)l * E + my_sel], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
                     }
-                    __builtin_amdgcn_s_sleep(1);
-                    w = ld_tag(A.rec + tt);
                 }
-                const int code = (int)((w >> 32) & 0x3FFu);
-                s_sel[tt] = code == 0x3FF ? -1 : code;
-                s_w[tt] = __uint_as_float((uint32_t)w);
             }
             if (__syncthreads_or(late)) {
                 if (t == 0) __hip_atomic_store(A.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -1038,11 +1019,16 @@ int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
 
 }  // namespace
 
+// Barrier words: nb flags, then (from a 128-byte line) kGoCopies release
+// words kGoStride apart.
+static int go_offset(int nb) { return (nb + 63) / 32 * 32; }
+static int flag_words(int nb) { return go_offset(nb) + kGoCopies * kGoStride; }
+
 // Scratch and tables a stack keeps for the one-launch path.
 struct StepPlan {
     StepLayer *layers = nullptr;   // device [L]
-    unsigned *flags = nullptr;     // device [nb + 64]: flags, then the go word on its own line
-    uint64_t *tagged = nullptr;    // device: logits [E] | record [16] | x [H], tagged words
+    unsigned *flags = nullptr;     // device [flag_words(nb)]: flags, then the release word's copies
+    uint64_t *tagged = nullptr;    // device: logit copies [kLR][lws] | x [H], tagged words
     size_t tagged_words = 0;
     unsigned long long *trace = nullptr;   // device [L][16][nb] (filled while profiling)
     int n_layers = 0;
@@ -1117,14 +1103,14 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     }
     MH_HIP(hipMalloc(&p->layers, sizeof(StepLayer) * (size_t)n_layers));
     MH_HIP(hipMemcpy(p->layers, host.data(), sizeof(StepLayer) * (size_t)n_layers, hipMemcpyHostToDevice));
-    MH_HIP(hipMalloc(&p->flags, sizeof(unsigned) * (size_t)(nb + 64)));
+    MH_HIP(hipMalloc(&p->flags, sizeof(unsigned) * (size_t)flag_words(nb)));
     MH_HIP(hipMalloc(&p->trace, sizeof(unsigned long long) * kStamps * (size_t)n_layers * (size_t)nb));
     p->n_layers = n_layers;
     MH_HIP(hipHostMalloc((void **)&p->err, sizeof(unsigned), hipHostMallocMapped));
     *p->err = 0;
     MH_HIP(hipHostGetDevicePointer((void **)&p->err_dev, p->err, 0));
     watch_async_error(p->err, "decode step: a grid barrier timed out (blocks not co-resident)");
-    p->tagged_words = (size_t)L0.n_experts + 16 + (size_t)L0.hidden;
+    p->tagged_words = (size_t)kLR * ((L0.n_experts + 15) / 16 * 16 + 32) + (size_t)L0.hidden;
     MH_HIP(hipMalloc(&p->tagged, sizeof(uint64_t) * p->tagged_words));
     MH_HIP(hipMemset(p->tagged, 0, sizeof(uint64_t) * p->tagged_words));
     MH_HIP(hipMalloc(&p->h, sizeof(float) * (size_t)L0.top_k * (size_t)L0.ffn));
@@ -1147,7 +1133,7 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
         (void)hipFree(bad);
         if (hb) p->mf = 0;   // the VALU path handles any f16 scale
     }
-    MH_HIP(hipMemset(p->flags, 0, sizeof(unsigned) * (size_t)(nb + 64)));
+    MH_HIP(hipMemset(p->flags, 0, sizeof(unsigned) * (size_t)flag_words(nb)));
     MH_HIP(hipDeviceSynchronize());
     p->seq = 1;
     p->nb = nb;
@@ -1193,10 +1179,10 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     A.sel = sel;
     A.w = w;
     A.usage = usage;
+    A.lws = (A.E + 15) / 16 * 16 + 32;   // copies 256 B past a line boundary apart
     A.lw = p->tagged;
-    A.rec = p->tagged + A.E;
-    A.xw = p->tagged + A.E + 16;
-    A.go = p->flags + ((p->nb + 63) / 32) * 32;   // a separate 128-byte line
+    A.xw = p->tagged + (size_t)kLR * A.lws;
+    A.go = p->flags + go_offset(p->nb);
     A.h = p->h;
     A.h16 = p->h16;
     A.Fpad = p->Fpad;
@@ -1205,7 +1191,7 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
     A.err = p->err_dev;
     const unsigned nbar = 3u * (unsigned)n_layers;
     if (p->seq > 0xF0000000u) {   // wrap: restart the sequence from a clean slate
-        MH_LAUNCH("fill", k_fill_u32, dim3(1), dim3(256), 0, s, p->flags, p->nb + 64, 0u);
+        MH_LAUNCH("fill", k_fill_u32, dim3(1), dim3(256), 0, s, p->flags, flag_words(p->nb), 0u);
         MH_LAUNCH("fill", k_fill_u32, dim3(8), dim3(256), 0, s, (unsigned *)p->tagged, (int)(2 * p->tagged_words), 0u);
         p->seq = 1;
     }
