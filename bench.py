@@ -203,6 +203,8 @@ def run_gpu(args, shape):
                "bytes": gu_bytes_per_launch(shape, args.batch * k), "avg_us": kern["expert_gu"]["avg_us"]}
     dom["GBps"] = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
     extra["gemv"] = gemv_probe(ev, s)
+    if not args.no_refbench:
+        extra["reference_bench"] = reference_bench(ev, s)
     if not args.no_prefill:
         extra["prefill"] = prefill_probe(ev, s, args.seed)
     for b in bufs:
@@ -239,6 +241,61 @@ def gemv_probe(ev, s, rows: int = 262144, cols: int = 2880, reps: int = 20) -> d
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"kernel": "gemv (MXFP4)", "shape": [rows, cols], "bytes": nbytes, "avg_us": ms * 1e3,
             "GBps": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS}
+
+
+def reference_bench(ev, s, seconds: float = 1.0) -> dict:
+    """The reference's own kernel figure, run_bench (engine/midge.c:687-720):
+    a q4g32 2880x2880 matvec over fixed synthetic data (byte i = (i *
+    2654435761) >> 24, every scale 0x2c00, x = 0.5), looped for >= 1 s,
+    reported as GiB/s of data + scales. Three numbers:
+      cpu          the reference engine compiled from its sources
+                   (oracle/_ref/midged --bench), AVX2 + OpenMP on the host
+      drop_in_gpu  the same engine source with this library's drop-in
+                   header (oracle/_ref/midged_hip --bench): the reference's
+                   own loop, x and y crossing PCIe on every call
+      device       this library's GEMV on the same data with x and y
+                   resident in HBM, timed with HIP events over the loop.
+    The 4.7 MB matrix stays cache-resident on both sides."""
+    import re
+    import subprocess
+    import midge_amd
+    from midge_amd import DT_Q4G32, DevBuf
+    from midge_amd.kern import WT, matvec_dev
+    out = {"workload": "run_bench: q4g32 2880x2880, data + scales GiB/s (engine/midge.c:687-720)"}
+    for key, exe in (("cpu", "midged"), ("drop_in_gpu", "midged_hip")):
+        path = os.path.join(ROOT, "oracle", "_ref", exe)
+        if not os.path.exists(path):
+            out[key] = None
+            continue
+        r = subprocess.run([path, "--bench"], capture_output=True, text=True, timeout=120)
+        m = re.search(r"BENCH q4g32_gbps=([0-9.]+) threads=(\d+)", r.stdout)
+        out[key] = {"GiBps": float(m.group(1)), "threads": int(m.group(2)), "line": m.group(0)} if m else {
+            "error": (r.stdout + r.stderr)[-300:]}
+    rows = cols = 2880
+    db, sb = rows * cols // 2, rows * (cols // 32) * 2
+    data = ((np.arange(db, dtype=np.uint64) * np.uint64(2654435761)) & np.uint64(0xFFFFFFFF)) >> np.uint64(24)
+    dd = DevBuf.from_array(data.astype(np.uint8))
+    sd = DevBuf.from_array(np.full(sb // 2, 0x2C00, np.uint16))
+    xd = DevBuf.from_array(np.full(cols, 0.5, np.float32))
+    yd = DevBuf(rows * 4)
+    t = WT(DT_Q4G32, rows, cols, dd.ptr, sd.ptr)
+    for _ in range(3):
+        matvec_dev(t, xd, yd)
+    midge_amd.sync()
+    a, b = ev.event(), ev.event()
+    iters, el = 0, 0.0
+    while el < seconds:
+        ev.record(a, s)
+        for _ in range(200):
+            matvec_dev(t, xd, yd)
+        ev.record(b, s)
+        el += ev.elapsed_ms(a, b) * 1e-3
+        iters += 200
+    out["device"] = {"GiBps": iters * (db + sb) / el / 2**30, "iters": iters, "seconds": el,
+                     "us_per_call": el / iters * 1e6}
+    for d in (dd, sd, xd, yd):
+        d.free()
+    return out
 
 
 MFMA_FP8_PEAK_TFLOPS = 5000.0   # dense fp8 MFMA (the rate of fp4 x fp8 operands)
@@ -366,6 +423,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b16", action="store_true", help="skip the extra batch-16 measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the expert-major prefill measurement")
+    ap.add_argument("--no-refbench", action="store_true", help="skip the reference's run_bench figure")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device twice (byte-counter calibration)")
     args = ap.parse_args()
