@@ -205,6 +205,8 @@ def run_gpu(args, shape):
     extra["gemv"] = gemv_probe(ev, s)
     if not args.no_refbench:
         extra["reference_bench"] = reference_bench(ev, s)
+    if not args.no_configs:
+        extra["configs"] = config_probes(ev, s, args.seed)
     if not args.no_prefill:
         extra["prefill"] = prefill_probe(ev, s, args.seed)
     for b in bufs:
@@ -295,6 +297,76 @@ def reference_bench(ev, s, seconds: float = 1.0) -> dict:
                      "us_per_call": el / iters * 1e6}
     for d in (dd, sd, xd, yd):
         d.free()
+    return out
+
+
+def config_probes(ev, s, seed: int, reps: int = 20) -> dict:
+    """Configurations 0-2 of the measurement plan beside the headline (cfg 4)
+    and the prefill (cfg 3), each with synthetic device-generated inputs:
+      cfg0  one gpt-oss expert FFN for one token: a one-layer stack of one
+            expert (top-1), through the one-launch step
+      cfg1  one gpt-oss-20b MoE layer (32 experts, top-4), batch 1, a fresh
+            hidden state per step so the routed experts differ
+      cfg2  the int8 (q8r) trunk GEMVs QKV 5120x2880, O 2880x4096 and
+            lm_head 201088x2880 at batch 1 and 32 (the batch-32 launch runs
+            one GEMV per column over the same weights)."""
+    import midge_amd
+    from midge_amd import DT_Q8R, DevBuf, _lib, synth
+    from midge_amd.kern import WT, matvec_dev
+    from midge_amd.moe import Stack
+    from midge_amd.synth import MoEShape
+    out = {}
+    for name, shp in (("cfg0", MoEShape(hidden=2880, ffn=2880, n_experts=1, top_k=1, n_layers=1)),
+                      ("cfg1", MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4, n_layers=1))):
+        st, bufs, keys = Stack.synthetic(shp, seed, 1)
+        xs = DevBuf((reps + 3) * shp.hidden * 4)
+        _lib.call("mh_synth_normal_dev", xs.ptr, (reps + 3) * shp.hidden, synth.hash64_int(keys.x, 5),
+                  float(synth.normal_c(1.0)))
+        for i in range(3):
+            st.decode(xs.ptr + i * shp.hidden * 4, 1)
+        midge_amd.sync()
+        a, b = ev.event(), ev.event()
+        ev.record(a, s)
+        for i in range(reps):
+            st.decode(xs.ptr + (3 + i) * shp.hidden * 4, 1)
+        ev.record(b, s)
+        ms = ev.elapsed_ms(a, b) / reps
+        nbytes = step_bytes(shp, 1, float(shp.top_k))
+        out[name] = {"workload": ("one expert FFN (2880x2880 MXFP4 gate/up/down), one token" if name == "cfg0" else
+                                  "one gpt-oss-20b MoE layer, 32 MXFP4 experts, top-4, batch 1"),
+                     "us_per_token": ms * 1e3, "tok_per_s": 1e3 / ms, "hbm_bytes": nbytes,
+                     "GBps": nbytes / (ms * 1e-3) / 1e9, "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        xs.free()
+        st.destroy()
+        for d in bufs:
+            d.free()
+    gemvs = []
+    for gname, R, Cc in (("qkv", 5120, 2880), ("o", 2880, 4096), ("lm_head", 201088, 2880)):
+        w, sc = DevBuf(R * Cc), DevBuf(R * 4)
+        _lib.call("mh_synth_i8_dev", w.ptr, R * Cc, 901)
+        _lib.call("mh_synth_uniform_dev", sc.ptr, R, 902, 1e-3, float(synth.uniform_c(1e-3, 1e-2)))
+        t = WT(DT_Q8R, R, Cc, w.ptr, sc.ptr)
+        for B in (1, 32):
+            x, y = DevBuf(B * Cc * 4), DevBuf(B * R * 4)
+            _lib.call("mh_synth_normal_dev", x.ptr, B * Cc, 903, float(synth.normal_c(1.0)))
+            for _ in range(3):
+                matvec_dev(t, x, y, B)
+            midge_amd.sync()
+            a, b = ev.event(), ev.event()
+            ev.record(a, s)
+            for _ in range(reps):
+                matvec_dev(t, x, y, B)
+            ev.record(b, s)
+            ms = ev.elapsed_ms(a, b) / reps
+            nbytes = R * Cc + 4 * R + 4 * Cc * B + 4 * R * B
+            gemvs.append({"gemv": gname, "shape": [R, Cc], "batch": B, "us": ms * 1e3,
+                          "GBps": nbytes / (ms * 1e-3) / 1e9, "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                          "GFLOPs": 2.0 * R * Cc * B / (ms * 1e-3) / 1e9})
+            x.free()
+            y.free()
+        w.free()
+        sc.free()
+    out["cfg2"] = {"workload": "int8 (q8r) trunk GEMVs, batch 1 and 32", "gemvs": gemvs}
     return out
 
 
@@ -424,6 +496,7 @@ def main() -> int:
     ap.add_argument("--no-b16", action="store_true", help="skip the extra batch-16 measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the expert-major prefill measurement")
     ap.add_argument("--no-refbench", action="store_true", help="skip the reference's run_bench figure")
+    ap.add_argument("--no-configs", action="store_true", help="skip the configuration 0-2 measurements")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device twice (byte-counter calibration)")
     args = ap.parse_args()

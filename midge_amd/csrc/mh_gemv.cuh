@@ -16,8 +16,19 @@
 
 namespace mh {
 
-constexpr int kGemvU = 4;          // row iterations in flight per thread
+constexpr int kGemvU = 4;          // 16-byte words in flight per thread per step
 constexpr int kGemvThreads = 512;
+
+// A thread's share of a row: W 16-byte words (2 for int8, so that a chunk is
+// 32 elements and a 2880-wide row is 90 chunks, as for the 4-bit types:
+// 5 row slots per 512-thread block instead of 2), E elements; U row
+// iterations in flight, so that U * W words are in flight per thread.
+template <int DT>
+struct gemv_chunk {
+    static constexpr int W = DT == MH_DT_Q8R ? 2 : 1;
+    static constexpr int E = mh_chunk<DT>::E * W;
+    static constexpr int U = kGemvU / W;
+};
 
 // Slots per block for C chunks per row and the thread count that covers them.
 inline void gemv_shape(int C, int *ns, int *nt) {
@@ -65,11 +76,13 @@ __device__ __forceinline__ void block_reduce_rows(const float *red, int C, int n
 template <int DT, int U, class RowFn>
 __device__ __forceinline__ void gemv_load(RowFn rowref, int f0, int nf, int c, int sl, int ns, mh_u4 *q,
                                           uint32_t *sb) {
+    constexpr int W = gemv_chunk<DT>::W;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int f = min(f0 + u * ns + sl, nf - 1);
         const RowRef rr = rowref(f);
-        q[u] = mh_load16(mh_global(rr.data + (size_t)c * 16));
+#pragma unroll
+        for (int w = 0; w < W; ++w) q[u * W + w] = mh_load16(mh_global(rr.data + ((size_t)c * W + w) * 16));
         if constexpr (DT == MH_DT_MXFP4 || DT == MH_DT_Q4G32) sb[u] = mh_load_u16(mh_global(rr.scale + c));
         else sb[u] = 0x3C00u;   // f16 1.0: int8 / f32 rows are scaled by the caller
     }
@@ -79,10 +92,14 @@ __device__ __forceinline__ void gemv_load(RowFn rowref, int f0, int nf, int c, i
 template <int DT, int U>
 __device__ __forceinline__ void gemv_math(const mh_u4 *q, const uint32_t *sb, const float *xr, int f0, int nf,
                                           int slot, int c, int C, int ns, bool active, float *red) {
+    constexpr int W = gemv_chunk<DT>::W, WE = mh_chunk<DT>::E;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const bool valid = active && f0 + u * ns + slot < nf;
-        const float p = mh_dot_chunk<DT>(q[u], xr) * (valid ? mh_f16((uint16_t)sb[u]) : 0.f);
+        float d = mh_dot_chunk<DT>(q[u * W], xr);
+#pragma unroll
+        for (int w = 1; w < W; ++w) d += mh_dot_chunk<DT>(q[u * W + w], xr + w * WE);
+        const float p = d * (valid ? mh_f16((uint16_t)sb[u]) : 0.f);
         if (active) red[(u * ns + slot) * C + c] = p;
     }
 }
@@ -96,7 +113,7 @@ __device__ __forceinline__ void gemv_math(const mh_u4 *q, const uint32_t *sb, co
 // Software-pipelined two deep: while step i (U rows per slot) is computed,
 // synchronised and reduced, the loads of step i + 1 are in flight. Must be
 // called by every thread.
-template <int DT, int U = kGemvU, class RowFn>
+template <int DT, int U = gemv_chunk<DT>::U, class RowFn>
 __device__ __forceinline__ void block_gemv(RowFn rowref, int nf, int C, int ns, const float *xr,
                                            float *red, float *res) {
     const int t = threadIdx.x;
@@ -105,7 +122,7 @@ __device__ __forceinline__ void block_gemv(RowFn rowref, int nf, int C, int ns, 
     const int sl = active ? slot : ns - 1;
     const int step = ns * U;
     const int per = U * ns * C;   // floats of one red buffer
-    mh_u4 qa[U], qb[U];
+    mh_u4 qa[U * gemv_chunk<DT>::W], qb[U * gemv_chunk<DT>::W];
     uint32_t sa[U], sbb[U];
     if (nf <= 0) return;
     gemv_load<DT, U>(rowref, 0, nf, c, sl, ns, qa, sa);
@@ -130,7 +147,7 @@ __device__ __forceinline__ void block_gemv(RowFn rowref, int nf, int C, int ns, 
 // Load this thread's E elements of x (zeros for idle threads).
 template <int DT>
 __device__ __forceinline__ void load_x(const float *x, int C, int ns, float *xr) {
-    constexpr int E = mh_chunk<DT>::E;
+    constexpr int E = gemv_chunk<DT>::E;
     const int t = threadIdx.x;
     const int slot = t / C, c = t - slot * C;
     if (slot < ns) {

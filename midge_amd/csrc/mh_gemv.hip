@@ -15,7 +15,7 @@ template <int DT>
 __global__ void __launch_bounds__(kGemvThreads)
 k_gemv(const uint8_t *__restrict__ W, const void *__restrict__ S, const float *__restrict__ X,
        float *__restrict__ Y, int rows, int cols, int ns, int rpb) {
-    constexpr int E = mh_chunk<DT>::E;
+    constexpr int E = gemv_chunk<DT>::E;
     extern __shared__ float lds[];
     const int C = cols / E;
     float *res = lds;                  // [rpb]
@@ -23,7 +23,7 @@ k_gemv(const uint8_t *__restrict__ W, const void *__restrict__ S, const float *_
     const int b = blockIdx.y;
     const int r0 = blockIdx.x * rpb;
     const int nf = min(rpb, rows - r0);
-    const size_t rowbytes = (size_t)C * 16;
+    const size_t rowbytes = (size_t)C * 16 * gemv_chunk<DT>::W;
     float xr[E];
     load_x<DT>(X + (size_t)b * cols, C, ns, xr);
     const uint16_t *S16 = (const uint16_t *)S;
@@ -144,7 +144,7 @@ k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, float *__res
 
 template <int DT>
 int launch_gemv_t(const DevWT &w, const float *x, float *y, int batch, hipStream_t s) {
-    constexpr int E = mh_chunk<DT>::E;
+    constexpr int E = gemv_chunk<DT>::E;
     const int64_t rows = w.rows, cols = w.cols;
     const bool chunked = cols % E == 0 && cols / E <= kGemvThreads && ((uintptr_t)w.data % 16) == 0 &&
                          ((uintptr_t)x % 16) == 0 && rows <= INT32_MAX;

@@ -142,7 +142,7 @@ template <int DT>
 __global__ void __launch_bounds__(kGemvThreads)
 k_expert_gu(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restrict__ xb,
             float *__restrict__ h, int ns, int rpb) {
-    constexpr int CE = mh_chunk<DT>::E;
+    constexpr int CE = gemv_chunk<DT>::E;
     extern __shared__ float lds[];
     const int a = blockIdx.y;
     const int e = sel[a];
@@ -157,7 +157,7 @@ k_expert_gu(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restri
     float *res = lds;              // [2 * rpb]
     float *red = lds + 2 * rpb;    // [U][ns][C]
     const uint8_t *base = A.experts + (uint64_t)e * A.stride;
-    const size_t rowbytes = (size_t)C * 16;
+    const size_t rowbytes = (size_t)C * 16 * gemv_chunk<DT>::W;
     const size_t srow = (DT == MH_DT_Q8R) ? 0 : (size_t)C;   // f16 scales per row (4-bit)
     float xr[CE];
     load_x<DT>(xb + (size_t)(a / A.k) * A.hidden, C, ns, xr);
@@ -190,7 +190,7 @@ template <int DT>
 __global__ void __launch_bounds__(kGemvThreads)
 k_expert_down(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restrict__ h,
               float *__restrict__ ye, int ns, int rpb) {
-    constexpr int CE = mh_chunk<DT>::E;
+    constexpr int CE = gemv_chunk<DT>::E;
     extern __shared__ float lds[];
     const int a = blockIdx.y;
     const int e = sel[a];
@@ -205,7 +205,7 @@ k_expert_down(ExpertArgs A, const int32_t *__restrict__ sel, const float *__rest
     float *res = lds;
     float *red = lds + rpb;
     const uint8_t *base = A.experts + (uint64_t)e * A.stride;
-    const size_t rowbytes = (size_t)C * 16;
+    const size_t rowbytes = (size_t)C * 16 * gemv_chunk<DT>::W;
     const size_t srow = (DT == MH_DT_Q8R) ? 0 : (size_t)C;
     float xr[CE];
     load_x<DT>(h + (size_t)a * A.ffn, C, ns, xr);
@@ -271,7 +271,7 @@ k_combine_prefill(float *__restrict__ x, const float *__restrict__ ye, const int
 template <int DT>
 int launch_experts_t(const DevLayer &L, int A, const int32_t *sel, const float *xb, float *h, float *ye,
                      hipStream_t s) {
-    constexpr int CE = mh_chunk<DT>::E;
+    constexpr int CE = gemv_chunk<DT>::E;
     ExpertArgs ea;
     ea.experts = L.experts;
     ea.stride = L.expert_stride;
