@@ -308,8 +308,8 @@ def config_probes(ev, s, seed: int, reps: int = 20) -> dict:
       cfg1  one gpt-oss-20b MoE layer (32 experts, top-4), batch 1, a fresh
             hidden state per step so the routed experts differ
       cfg2  the int8 (q8r) trunk GEMVs QKV 5120x2880, O 2880x4096 and
-            lm_head 201088x2880 at batch 1 and 32 (the batch-32 launch runs
-            one GEMV per column over the same weights)."""
+            lm_head 201088x2880 at batch 1 (the GEMV engine) and 32 (one pass
+            over the weights on the int8 matrix cores)."""
     import midge_amd
     from midge_amd import DT_Q8R, DevBuf, _lib, synth
     from midge_amd.kern import WT, matvec_dev
@@ -360,6 +360,7 @@ def config_probes(ev, s, seed: int, reps: int = 20) -> dict:
             ms = ev.elapsed_ms(a, b) / reps
             nbytes = R * Cc + 4 * R + 4 * Cc * B + 4 * R * B
             gemvs.append({"gemv": gname, "shape": [R, Cc], "batch": B, "us": ms * 1e3,
+                          "path": "int8 matrix cores, x as 3 int8 digits" if B > 1 else "GEMV",
                           "GBps": nbytes / (ms * 1e-3) / 1e9, "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                           "GFLOPs": 2.0 * R * Cc * B / (ms * 1e-3) / 1e9})
             x.free()

@@ -88,6 +88,241 @@ k_gemv_rowwave(const uint8_t *__restrict__ W, const void *__restrict__ S, const 
     }
 }
 
+// ------------------------------------------- batched int8 on the matrix cores
+//
+// Y[b] = diag(S) W X[b] for a batch of columns, reading each weight byte
+// once per 32 columns (the per-column GEMV above reads W once per column).
+// Each column of X is written as a 22-bit fixed-point number under a
+// power-of-two scale, x = 2^sh * (65536 d0 + 256 d1 + d2), with balanced
+// int8 digits d0, d1, d2 (|d0| <= 65). The int8 weights then meet the digits
+// on v_mfma_i32_16x16x64_i8, whose int32 sums are exact, and the three sums
+// are combined in f32: y = S * 2^sh * (65536 A0 + (256 A1 + A2)). The only
+// rounding of x is to 2^-22 of the column's largest magnitude (relative
+// error of a dot product ~1e-7, against the f32 sequential sum of mv_q8r,
+// engine/mkern.h:23-31, which rounds at every step).
+
+constexpr int kQ8Cols = 32;            // columns per group: NT 16-column tiles
+constexpr int kQ8MaxK = 65536;         // |A0| <= 127 * 65 * K stays below 2^31
+constexpr int kQ8NonFinite = -100000;  // shift marking a column with inf/nan
+
+typedef int mh_i4 __attribute__((ext_vector_type(4)));
+
+// Digits of column c = 32 * blockIdx.x + blockIdx.y, laid out as the B
+// operand of the MFMA: word (group, kc, digit, n, lane) holds, for lane
+// l = 16 kg + cn, the digits of column 32 group + 16 n + cn at k = 64 kc +
+// 16 kg .. +15. Columns past `batch` get zero digits.
+template <int NT>
+__global__ void __launch_bounds__(256)
+k_xdigits(const float *__restrict__ X, int K, int batch, uint8_t *__restrict__ xq, int *__restrict__ shift) {
+    __shared__ float part[4];
+    const int grp = blockIdx.x, cl = blockIdx.y, c = grp * kQ8Cols + cl;
+    const int n = cl >> 4, cn = cl & 15, KC = K >> 6;
+    const bool live = c < batch;
+    const float *x = X + (size_t)(live ? c : 0) * K;
+    float m = 0.f;
+    if (live)
+        for (int k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(x[k]));
+    bool bad = false;
+    if (live)
+        for (int k = threadIdx.x; k < K; k += blockDim.x) bad |= !__builtin_isfinite(x[k]);
+    m = __builtin_isfinite(m) ? m : __builtin_inff();
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const bool anybad = __syncthreads_or(bad);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    int e = 0;
+    if (m > 0.f && !anybad) (void)frexpf(m, &e);   // 2^(e-1) <= m < 2^e
+    if (threadIdx.x == 0) shift[c] = anybad ? kQ8NonFinite : e - 22;
+    for (int p = threadIdx.x; p < KC * 4; p += blockDim.x) {
+        const int kc = p >> 2, kg = p & 3;
+        uint32_t dw[3][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int q = 0;
+                if (live && !anybad) q = (int)rintf(ldexpf(x[p * 16 + 4 * j + i], 22 - e));   // |q| <= 2^22
+                const int d2 = ((q + 128) & 255) - 128;
+                const int q1 = (q - d2) >> 8;
+                const int d1 = ((q1 + 128) & 255) - 128;
+                const int d0 = (q1 - d1) >> 8;
+                b0 |= (uint32_t)(d0 & 255) << (8 * i);
+                b1 |= (uint32_t)(d1 & 255) << (8 * i);
+                b2 |= (uint32_t)(d2 & 255) << (8 * i);
+            }
+            dw[0][j] = b0;
+            dw[1][j] = b1;
+            dw[2][j] = b2;
+        }
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+            const size_t word = ((((size_t)grp * KC + kc) * 3 + d) * NT + n) * 64 + kg * 16 + cn;
+            *(mh_u4 *)(xq + word * 16) = mh_u4{dw[d][0], dw[d][1], dw[d][2], dw[d][3]};
+        }
+    }
+}
+
+// Tile shapes of the batched kernel: a wave owns MT 16-row tiles; a block is
+// RW row-waves times S waves that split K between them (chunks s, s + S, ...
+// of wave s), their int32 sums added in LDS (exact in any order). Weights
+// are loaded DA 64-wide chunks ahead of the matrix instructions.
+template <int MT_, int RW_, int S_, int DA_>
+struct Q8Tile {
+    static constexpr int MT = MT_, RW = RW_, S = S_, DA = DA_;
+    static constexpr int threads = 64 * RW * S;
+    static constexpr int rows = 16 * MT * RW;   // rows per block
+};
+using Q8Long = Q8Tile<4, 4, 1, 2>;    // long matrices: all of K per wave, equal row shares
+using Q8Short = Q8Tile<1, 1, 8, 3>;   // short ones: 16 rows per block, K split 8 ways
+
+// A wave computes rows 16 MT at a time as MT 16-row tiles, the columns of
+// group blockIdx.y as NT 16-column tiles, three digits each: MT * NT * 3
+// int32 accumulator tiles. Weight tile m, lane l = 16 g + i holds row r0 +
+// 16 m + i at k = 64 kc + 16 g .. +15, the same k as the digit word of lane l,
+// so every product pairs equal k. Each step issues the digit loads (L2 hits,
+// one chunk ahead) before the weight loads (DA chunks ahead): loads complete
+// in issue order, so waiting for a step's digits does not wait for younger
+// weights. With S = 1 the grid is sized to the machine and each wave takes an
+// equal contiguous share of the rows (no tail of partly filled rounds); with
+// S > 1 a block owns 16 MT RW rows. Rows past a wave's share re-read its last
+// row and are not stored.
+template <int NT, class T>
+__global__ void __launch_bounds__(T::threads, 2)
+k_gemm_q8r(const int8_t *__restrict__ W, const float *__restrict__ S, const uint8_t *__restrict__ xq,
+           const int *__restrict__ shift, const float *__restrict__ X, float *__restrict__ Y, int R, int K,
+           int batch) {
+    constexpr int MT = T::MT, SP = T::S, DA = T::DA, NA = DA + 1;
+    constexpr int NACC = MT * NT * 3;
+    constexpr int UNR = NA % 2 ? 2 * NA : NA;   // a multiple of both set counts
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rw = wave / SP, sp = wave - rw * SP;
+    const int grp = blockIdx.y, KC = K >> 6;
+    const int i = lane & 15, g = lane >> 4;
+    const int nk = sp < KC ? (KC - sp + SP - 1) / SP : 0;   // chunks of this wave
+    int rbeg, rend;
+    if constexpr (SP == 1) {
+        const int64_t nw = (int64_t)gridDim.x * T::RW, gw = (int64_t)blockIdx.x * T::RW + rw;
+        rbeg = (int)(gw * R / nw);
+        rend = (int)((gw + 1) * R / nw);
+    } else {
+        rbeg = (blockIdx.x * T::RW + rw) * (16 * MT);
+        rend = min(rbeg + 16 * MT, R);
+    }
+    const int rlast = max(min(rend, R) - 1, 0);
+    const int ngroups = SP > 1 ? 1 : (rend - rbeg + 16 * MT - 1) / (16 * MT);
+    const mh_gbytes bp = mh_global(xq + ((size_t)grp * KC * 3 * NT * 64 + lane) * 16);
+    auto chunk = [&](int it) { return min(sp + it * SP, KC - 1); };
+    for (int gi = 0; gi < ngroups; ++gi) {
+        const int r0 = rbeg + gi * 16 * MT;
+        mh_gbytes ap[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const int r = min(r0 + 16 * m + i, rlast);
+            ap[m] = mh_global(W + (size_t)r * K + 16 * g);
+        }
+        mh_i4 acc[MT][NT][3];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+                for (int d = 0; d < 3; ++d) acc[m][n][d] = mh_i4{0, 0, 0, 0};
+        mh_u4 a[NA][MT], b[2][3 * NT];
+        auto load_a = [&](int set, int kc) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) a[set][m] = mh_load16(ap[m] + (size_t)kc * 64);
+        };
+        auto load_b = [&](int set, int kc) {
+#pragma unroll
+            for (int j = 0; j < 3 * NT; ++j)
+                b[set][j] =
+                    *(const mh_u4 __attribute__((address_space(1))) *)(bp + ((size_t)kc * 3 * NT + j) * 1024);
+        };
+        auto step = [&](int j, int it) {   // j: position in the unrolled group (register sets)
+            load_b((j + 1) % 2, chunk(it + 1));
+            load_a((j + DA) % NA, chunk(it + DA));
+            __builtin_amdgcn_sched_barrier(0);   // keep the issue order: loads, then this step's math
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+#pragma unroll
+                    for (int d = 0; d < 3; ++d)
+                        acc[m][n][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            (mh_i4)a[j % NA][m], (mh_i4)b[j % 2][d * NT + n], acc[m][n][d], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        load_b(0, chunk(0));
+#pragma unroll
+        for (int d = 0; d < DA; ++d) load_a(d, chunk(d));
+        int it = 0;
+        for (; it + UNR <= nk; it += UNR) {
+#pragma unroll
+            for (int j = 0; j < UNR; ++j) step(j, it + j);
+        }
+#pragma unroll
+        for (int j = 0; j < UNR - 1; ++j)
+            if (it + j < nk) step(j, it + j);
+        if constexpr (SP > 1) {
+            __shared__ mh_i4 red[T::RW * (SP - 1) * NACC * 64];
+            if (sp > 0) {
+                mh_i4 *o = red + ((size_t)(rw * (SP - 1) + sp - 1) * NACC) * 64 + lane;
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int n = 0; n < NT; ++n)
+#pragma unroll
+                        for (int d = 0; d < 3; ++d) o[((m * NT + n) * 3 + d) * 64] = acc[m][n][d];
+            }
+            __syncthreads();
+            if (sp > 0) return;
+            for (int w = 0; w < SP - 1; ++w) {
+                const mh_i4 *o = red + ((size_t)(rw * (SP - 1) + w) * NACC) * 64 + lane;
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int n = 0; n < NT; ++n)
+#pragma unroll
+                        for (int d = 0; d < 3; ++d) acc[m][n][d] += o[((m * NT + n) * 3 + d) * 64];
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const int col = grp * kQ8Cols + 16 * n + i;
+            if (col >= batch) continue;
+            const int sh = shift[col];
+            float *yc = Y + (size_t)col * R;
+            if (sh == kQ8NonFinite) {
+                // a column holding inf or nan: the plain f32 sum, so the
+                // pattern of infinities and nans is that of mv_q8r
+                const float *xc = X + (size_t)col * K;
+#pragma unroll 1
+                for (int e = 0; e < 4 * MT; ++e) {
+                    const int row = r0 + 16 * (e >> 2) + 4 * g + (e & 3);
+                    if (row >= rend) continue;
+                    const int8_t *wr = W + (size_t)row * K;
+                    float t = 0.f;
+                    for (int k = 0; k < K; ++k) t = __builtin_fmaf((float)wr[k], xc[k], t);
+                    yc[row] = t * S[row];
+                }
+                continue;
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int row = r0 + 16 * m + 4 * g + q;
+                    if (row >= rend) continue;
+                    const float t = (float)acc[m][n][0][q] * 65536.f +
+                                    ((float)acc[m][n][1][q] * 256.f + (float)acc[m][n][2][q]);
+                    yc[row] = ldexpf(t, sh) * S[row];
+                }
+        }
+    }
+}
+
 // ------------------------------------------------------------ dequant
 
 // out[i][c] = W[r0+i][c] dequantized, bit-exact with wk_row.
@@ -167,6 +402,48 @@ int launch_gemv_t(const DevWT &w, const float *x, float *y, int batch, hipStream
                            s, w.data, w.scales, x, y, rows, cols);
     }
     return hip_check(hipGetLastError(), "gemv launch");
+}
+
+// Batched int8 GEMV on the matrix cores when the shape fits it (int8 rows of
+// 64-multiple width up to kQ8MaxK, 16-byte aligned operands, 2+ columns);
+// *done = false leaves the call to the per-column kernel.
+int launch_gemm_q8r(const DevWT &w, const float *x, float *y, int batch, hipStream_t s, bool *done) {
+    *done = false;
+    const int64_t R = w.rows, K = w.cols;
+    if (w.dt != MH_DT_Q8R || batch < 2 || R < 1 || K < 64 || K % 64 != 0 || K > kQ8MaxK || R > (int64_t)INT32_MAX - 4096 ||
+        (uintptr_t)w.data % 16 != 0)
+        return MH_OK;
+    const char *off = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two paths
+    if (off && *off && *off != '0') return MH_OK;
+    const int groups = (batch + kQ8Cols - 1) / kQ8Cols;
+    const int NT = batch > 16 ? 2 : 1;
+    const uint64_t qbytes = (uint64_t)groups * (K / 64) * 3 * NT * 1024;
+    void *p;
+    MH_TRY(scratch(S_XQ, qbytes + (uint64_t)groups * kQ8Cols * 4, &p));
+    uint8_t *xq = (uint8_t *)p;
+    int *sh = (int *)(xq + qbytes);
+    if (NT == 2)
+        MH_LAUNCH("xdigits", k_xdigits<2>, dim3((unsigned)groups, 32), dim3(256), 0, s, x, (int)K, batch, xq, sh);
+    else
+        MH_LAUNCH("xdigits", k_xdigits<1>, dim3((unsigned)groups, 16), dim3(256), 0, s, x, (int)K, batch, xq, sh);
+    // the long tiling when it gives every SIMD two waves, else the K-split one
+    const bool longm = (R + Q8Long::rows - 1) / Q8Long::rows * (Q8Long::threads / 64) >= 2 * 4 * device_cus();
+    // long: two blocks per CU, each wave an equal share of the rows
+    const int64_t nlong = std::min<int64_t>((R + Q8Long::rows - 1) / Q8Long::rows, 2 * (int64_t)device_cus());
+    auto go = [&](auto kern, int rows, int threads) {
+        const int64_t nb = longm ? nlong : (R + rows - 1) / rows;
+        MH_LAUNCH("gemm_q8r", kern, dim3((unsigned)nb, (unsigned)groups), dim3(threads), 0, s,
+                  (const int8_t *)w.data, (const float *)w.scales, xq, sh, x, y, (int)R, (int)K, batch);
+    };
+    if (longm) {
+        if (NT == 2) go(k_gemm_q8r<2, Q8Long>, Q8Long::rows, Q8Long::threads);
+        else go(k_gemm_q8r<1, Q8Long>, Q8Long::rows, Q8Long::threads);
+    } else {
+        if (NT == 2) go(k_gemm_q8r<2, Q8Short>, Q8Short::rows, Q8Short::threads);
+        else go(k_gemm_q8r<1, Q8Short>, Q8Short::rows, Q8Short::threads);
+    }
+    *done = true;
+    return hip_check(hipGetLastError(), "gemm_q8r launch");
 }
 
 template <int DT>
@@ -267,6 +544,10 @@ int mh_matvec_dev(const mh_wt *t, const float *x, float *y, int batch) {
     MH_TRY(resolve_wt(t, &w, "mh_matvec_dev weights"));
     MH_TRY(resolve_dev(x, (uint64_t)batch * w.cols * 4, "mh_matvec_dev x"));
     MH_TRY(resolve_dev(y, (uint64_t)batch * w.rows * 4, "mh_matvec_dev y"));
+    if (batch > 65535) return fail(MH_E_ARG, "batch %d out of range [1, 65535]", batch);
+    bool done;
+    MH_TRY(launch_gemm_q8r(w, x, y, batch, stream(), &done));
+    if (done) return MH_OK;
     return launch_gemv(w, x, y, batch, stream());
 }
 

@@ -117,6 +117,105 @@ def test_matvec_dev_batch(mh, dt, batch):
         d.free()
 
 
+def _batched_q8r(rows, cols, batch, X):
+    data, sc = make_tensor(DT_Q8R, rows, cols, rng=RNG)
+    wd, sd = DevBuf.from_array(data), DevBuf.from_array(sc)
+    xd, yd = DevBuf.from_array(X), DevBuf(batch * rows * 4)
+    t = WT(DT_Q8R, rows, cols, wd.ptr, sd.ptr)
+    matvec_dev(t, xd, yd, batch)
+    Y = yd.download(np.float32, (batch, rows))
+    for d in (wd, sd, xd, yd):
+        d.free()
+    return Y, data, sc
+
+
+# int8 batches of 2+ columns run on the matrix cores (x as three int8 digits
+# under a power-of-two scale per column). Shapes: the trunk's QKV and O at
+# batch 32 (O has 64 chunks of 64 columns, not a multiple of the unroll),
+# tails of rows below one block and one tile, one and two 16-column tiles,
+# two column groups, one 64-wide chunk.
+@pytest.mark.parametrize("rows,cols,batch", [(5120, 2880, 32), (2880, 4096, 32), (300, 640, 17), (5, 64, 2),
+                                             (1000, 192, 33), (2000, 2880, 16), (257, 128, 64)])
+def test_matvec_dev_q8r_batched(mh, rows, cols, batch):
+    say(f"matvec_dev q8r batched {rows}x{cols} batch={batch}")
+    X = RNG.standard_normal((batch, cols)).astype(np.float32)
+    # column magnitudes from 1e-20 to 1e20, one all-zero column, one column
+    # whose largest element is a power of two (the digit scale's edge)
+    X *= (10.0 ** RNG.uniform(-20, 20, batch)).astype(np.float32)[:, None]
+    X[batch // 2] = 0.0
+    if batch - 1 != batch // 2:
+        X[-1, 3] = np.float32(2.0 ** np.ceil(np.log2(2.0 * np.abs(X[-1]).max())))
+    Y, data, sc = _batched_q8r(rows, cols, batch, X)
+    for b in range(batch):
+        want = po.matvec(DT_Q8R, data, sc, X[b], rows, cols)
+        assert rel_l2(Y[b], want) < 1e-5, b
+    assert not Y[batch // 2].any()
+
+
+def test_matvec_dev_q8r_batched_nonfinite(mh):
+    # a column holding inf or nan gives the inf/nan pattern of the f32 sum
+    rows, cols, batch = 700, 256, 5
+    say(f"matvec_dev q8r batched non-finite {rows}x{cols} batch={batch}")
+    X = RNG.standard_normal((batch, cols)).astype(np.float32)
+    X[1, 17] = np.inf
+    X[2, 5] = np.nan
+    X[3, 9], X[3, 200] = np.inf, -np.inf
+    Y, data, sc = _batched_q8r(rows, cols, batch, X)
+    for b in range(batch):
+        want = po.matvec(DT_Q8R, data, sc, X[b], rows, cols)
+        fin = np.isfinite(want)
+        assert np.array_equal(np.isnan(Y[b]), np.isnan(want)), b
+        assert np.array_equal(np.isposinf(Y[b]), np.isposinf(want)), b
+        assert np.array_equal(np.isneginf(Y[b]), np.isneginf(want)), b
+        if fin.any():
+            assert rel_l2(Y[b][fin], want[fin]) < 1e-5, b
+
+
+def test_matvec_dev_q8r_batched_paths_agree(mh, monkeypatch):
+    # the matrix-core path and the per-column GEMV (MIDGE_HIP_NO_MFMA=1)
+    rows, cols, batch = 4096, 2880, 8
+    say(f"matvec_dev q8r batched vs per-column {rows}x{cols} batch={batch}")
+    data, sc = make_tensor(DT_Q8R, rows, cols, rng=RNG)
+    X = RNG.standard_normal((batch, cols)).astype(np.float32)
+    wd, sd = DevBuf.from_array(data), DevBuf.from_array(sc)
+    xd, y1, y2 = DevBuf.from_array(X), DevBuf(batch * rows * 4), DevBuf(batch * rows * 4)
+    t = WT(DT_Q8R, rows, cols, wd.ptr, sd.ptr)
+    matvec_dev(t, xd, y1, batch)
+    monkeypatch.setenv("MIDGE_HIP_NO_MFMA", "1")
+    matvec_dev(t, xd, y2, batch)
+    a, b = y1.download(np.float32, (batch, rows)), y2.download(np.float32, (batch, rows))
+    for d in (wd, sd, xd, y1, y2):
+        d.free()
+    assert rel_l2(a, b) < 1e-5
+
+
+def test_lm_head_batch32_sampled_rows(mh):
+    # int8 lm_head 201088 x 2880 at batch 32 on the matrix cores: sampled rows
+    # of every column against the oracle, and per column the linearity
+    # identity sum_r y_r / s_r = (sum_r W_r) . x over all rows
+    rows, cols, batch = 201088, 2880, 32
+    say("lm_head q8r 201088x2880 batch 32")
+    k = synth.Keys(78)
+    data = po.synth_i8(k.router_w, rows * cols)
+    sc = synth.synth_uniform(k.router_s, rows, 1e-3, synth.uniform_c(1e-3, 1e-2))
+    X = RNG.standard_normal((batch, cols)).astype(np.float32)
+    wd, sd = DevBuf.from_array(data), DevBuf.from_array(sc)
+    xd, yd = DevBuf.from_array(X), DevBuf(batch * rows * 4)
+    matvec_dev(WT(DT_Q8R, rows, cols, wd.ptr, sd.ptr), xd, yd, batch)
+    Y = yd.download(np.float32, (batch, rows))
+    for d in (wd, sd, xd, yd):
+        d.free()
+    W = data.reshape(rows, cols)
+    idx = np.sort(RNG.choice(rows, 256, replace=False))
+    sub, ssub = np.ascontiguousarray(W[idx]), np.ascontiguousarray(sc[idx])
+    colsum = W.sum(axis=0, dtype=np.int64).astype(np.float64)
+    for b in range(batch):
+        assert rel_l2(Y[b][idx], po.matvec(DT_Q8R, sub, ssub, X[b], len(idx), cols)) < 1e-5, b
+        lhs = float(np.sum(Y[b].astype(np.float64) / sc.astype(np.float64)))
+        rhs = float(colsum @ X[b].astype(np.float64))
+        assert abs(lhs - rhs) <= 1e-5 * float(np.abs(colsum) @ np.abs(X[b])), b
+
+
 @pytest.mark.parametrize("dt,rows,cols", [(DT_F32, 7, 37), (DT_Q8R, 5, 100), (DT_F32, 3, 8192)])
 def test_matvec_fallback_shapes(mh, dt, rows, cols):
     say(f"matvec fallback dt={dt} {rows}x{cols}")
