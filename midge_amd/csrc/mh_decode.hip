@@ -766,7 +766,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 }
             }
             __syncthreads();
-            block_reduce_rows(red, C, 2 * np, res, [](int) { return true; });
+            block_reduce_rows(red, C, 2 * np, kThreads / 64, res, [](int) { return true; });
             __syncthreads();
             MH_STAMP(11);
             if constexpr (MF) {
@@ -949,7 +949,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             if (t < K * nr) bds[t] = bd_pref;
             MH_STAMP(13);
             __syncthreads();
-            block_reduce_rows(red, C, K * RC, res, [&](int it) { return it % RC < nr; });
+            block_reduce_rows(red, C, K * RC, kThreads / 64, res, [&](int it) { return it % RC < nr; });
             __syncthreads();
             MH_STAMP(14);
             // combine in selection order: moe = sum_i w_i (dot_i + bd_i); x += moe

@@ -18,6 +18,7 @@ namespace mh {
 
 constexpr int kGemvU = 4;          // 16-byte words in flight per thread per step
 constexpr int kGemvThreads = 512;
+constexpr int kGemvNB = 2;         // register sets: loads run NB - 1 steps ahead of the math
 
 // A thread's share of a row: W 16-byte words (2 for int8, so that a chunk is
 // 32 elements and a 2880-wide row is 90 chunks, as for the 4-bit types:
@@ -42,20 +43,40 @@ inline void gemv_shape(int C, int *ns, int *nt) {
 // LDS floats needed by block_gemv for ns slots of C chunks (two buffers).
 inline size_t gemv_lds_floats(int ns, int C) { return (size_t)2 * kGemvU * ns * C; }
 
-// Row source for block_gemv: flat row f -> (data pointer, scale pointer).
-// `scale` is the f16 group scales for 4-bit types, unused otherwise.
-struct RowRef {
-    const uint8_t *data;
-    const uint16_t *scale;
+// Buffer resources: the engine addresses rows by 32-bit byte offsets from a
+// block-uniform base (buffer loads), so a row's address costs a 24-bit
+// multiply-add, not 64-bit pointer arithmetic. Reads past `bytes` return 0.
+typedef __amdgpu_buffer_rsrc_t mh_rsrc;
+constexpr int kGemvNT = 2;   // cache-policy bits of weight loads: nontemporal
+__device__ __forceinline__ mh_rsrc gemv_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t v = (uint64_t)p;   // made scalar: the resource is uniform
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    void *u = (void *)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// a * b for a, b < 2^24 (full-rate v_mul_u32_u24), low 32 bits of the product
+__device__ __forceinline__ uint32_t mul24(uint32_t a, uint32_t b) { return (uint32_t)__umul24(a, b); }
+
+// Row source for block_gemv: flat row f -> byte offsets of its data (in the
+// data resource) and of its f16 group scales (in the scale resource; 4-bit
+// types only).
+struct RowOff {
+    uint32_t data, scale;
 };
 
 // Sums each row of red[nrows][C] (row-major) into out[row]. A wave takes 8
 // rows at a time: 8 lanes per row each add every 8th partial, then three
 // xor-shuffles combine them (a fixed order, so results are deterministic).
 // Rows in `skip` (out[row] untouched) are those the caller marks invalid.
+// nw is the block's wave count, passed in: reading blockDim inside a
+// pipelined loop is a memory load whose wait also waits for every weight
+// load in flight.
 template <class Keep>
-__device__ __forceinline__ void block_reduce_rows(const float *red, int C, int nrows, float *out, Keep keep) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+__device__ __forceinline__ void block_reduce_rows(const float *red, int C, int nrows, int nw, float *out,
+                                                  Keep keep) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rl = lane >> 3, part = lane & 7;
     for (int r0 = wave * 8; r0 < nrows; r0 += nw * 8) {
         const int r = r0 + rl;
@@ -74,17 +95,20 @@ __device__ __forceinline__ void block_reduce_rows(const float *red, int C, int n
 // and are masked out in the math). Scale bits stay raw f16 here: converting
 // inside the load loop would make every iteration wait for its load.
 template <int DT, int U, class RowFn>
-__device__ __forceinline__ void gemv_load(RowFn rowref, int f0, int nf, int c, int sl, int ns, mh_u4 *q,
-                                          uint32_t *sb) {
+__device__ __forceinline__ void gemv_load(mh_rsrc rd, mh_rsrc rs, RowFn rowoff, int f0, int nf, int c, int sl,
+                                          int ns, mh_u4 *q, uint32_t *sb) {
     constexpr int W = gemv_chunk<DT>::W;
+    const uint32_t cw = (uint32_t)c * (16u * W), cs = (uint32_t)c * 2u;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int f = min(f0 + u * ns + sl, nf - 1);
-        const RowRef rr = rowref(f);
+        const RowOff o = rowoff(min(f0 + u * ns + sl, nf - 1));
 #pragma unroll
-        for (int w = 0; w < W; ++w) q[u * W + w] = mh_load16(mh_global(rr.data + ((size_t)c * W + w) * 16));
-        if constexpr (DT == MH_DT_MXFP4 || DT == MH_DT_Q4G32) sb[u] = mh_load_u16(mh_global(rr.scale + c));
-        else sb[u] = 0x3C00u;   // f16 1.0: int8 / f32 rows are scaled by the caller
+        for (int w = 0; w < W; ++w)
+            q[u * W + w] = __builtin_amdgcn_raw_buffer_load_b128(rd, o.data + cw + 16u * w, 0, kGemvNT);
+        if constexpr (DT == MH_DT_MXFP4 || DT == MH_DT_Q4G32)
+            sb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, o.scale + cs, 0, kGemvNT);
+        else
+            sb[u] = 0x3C00u;   // f16 1.0: int8 / f32 rows are scaled by the caller
     }
 }
 
@@ -104,43 +128,53 @@ __device__ __forceinline__ void gemv_math(const mh_u4 *q, const uint32_t *sb, co
     }
 }
 
-// Computes res[f] = sum over chunks of dot(row f, x) for f in [0, nf).
+// Computes res[f] = sum over chunks of dot(row f, x) for f in [0, nf), rows
+// addressed through rowoff(f) in the resources rd (data) and rs (scales).
 // For 4-bit types the f16 group scale is applied per chunk (exact: powers of
 // two commute with rounding; non-power-of-two scales multiply the group's
 // partial sum once, as the reference does). For int8 the per-row scale is the
 // caller's. `xr` holds this thread's E elements of x; `red` is LDS of
 // gemv_lds_floats(ns, C) (two buffers); `res` is LDS of at least nf floats.
-// Software-pipelined two deep: while step i (U rows per slot) is computed,
-// synchronised and reduced, the loads of step i + 1 are in flight. Must be
-// called by every thread.
-template <int DT, int U = gemv_chunk<DT>::U, class RowFn>
-__device__ __forceinline__ void block_gemv(RowFn rowref, int nf, int C, int ns, const float *xr,
-                                           float *red, float *res) {
+// Software-pipelined NB deep: while step i (U rows per slot) is computed,
+// synchronised and reduced, the loads of steps i + 1 .. i + NB - 1 are in
+// flight. Must be called by every thread.
+template <int DT, int U = gemv_chunk<DT>::U, int NB = kGemvNB, class RowFn>
+__device__ __forceinline__ void block_gemv(mh_rsrc rd, mh_rsrc rs, RowFn rowoff, int nf, int C, int ns,
+                                           const float *xr, float *red, float *res) {
+    constexpr int WW = gemv_chunk<DT>::W;
     const int t = threadIdx.x;
     const int slot = t / C, c = t - slot * C;
     const bool active = slot < ns;
     const int sl = active ? slot : ns - 1;
     const int step = ns * U;
     const int per = U * ns * C;   // floats of one red buffer
-    mh_u4 qa[U * gemv_chunk<DT>::W], qb[U * gemv_chunk<DT>::W];
-    uint32_t sa[U], sbb[U];
+    const int nw = (ns * C + 63) >> 6;   // the launch's waves (gemv_shape)
+    mh_u4 q[NB][U * WW];
+    uint32_t sc[NB][U];
     if (nf <= 0) return;
-    gemv_load<DT, U>(rowref, 0, nf, c, sl, ns, qa, sa);
-    for (int f0 = 0; f0 < nf; f0 += 2 * step) {
-        // even step f0 from qa; odd step f0 + step from qb
-        const bool odd = f0 + step < nf;
-        if (odd) gemv_load<DT, U>(rowref, f0 + step, nf, c, sl, ns, qb, sbb);
+#pragma unroll
+    for (int j = 0; j < NB - 1; ++j) gemv_load<DT, U>(rd, rs, rowoff, j * step, nf, c, sl, ns, q[j], sc[j]);
+    // step j of a group of NB: loads of step fj + NB - 1 (rows clamped, so
+    // steps past the end re-read the last row), then the math of step fj
+    auto stepj = [&](int j, int fj) {
+        gemv_load<DT, U>(rd, rs, rowoff, fj + (NB - 1) * step, nf, c, sl, ns, q[(j + NB - 1) % NB],
+                         sc[(j + NB - 1) % NB]);
         __builtin_amdgcn_sched_barrier(0);
-        gemv_math<DT, U>(qa, sa, xr, f0, nf, slot, c, C, ns, active, red);
+        float *rb = red + ((fj / step) & 1) * per;
+        gemv_math<DT, U>(q[j], sc[j], xr, fj, nf, slot, c, C, ns, active, rb);
         __syncthreads();
-        block_reduce_rows(red, C, step, res + f0, [&](int it) { return f0 + it < nf; });
-        if (!odd) break;
-        if (f0 + 2 * step < nf) gemv_load<DT, U>(rowref, f0 + 2 * step, nf, c, sl, ns, qa, sa);
-        __builtin_amdgcn_sched_barrier(0);
-        gemv_math<DT, U>(qb, sbb, xr, f0 + step, nf, slot, c, C, ns, active, red + per);
-        __syncthreads();
-        block_reduce_rows(red + per, C, step, res + f0 + step, [&](int it) { return f0 + step + it < nf; });
+        block_reduce_rows(rb, C, step, nw, res + fj, [&](int it) { return fj + it < nf; });
+    };
+    // whole groups without exits (an exit inside the unrolled group makes the
+    // compiler wait for every load in flight at the loop edge), then the rest
+    int f0 = 0;
+    for (; f0 + (NB - 1) * step < nf; f0 += NB * step) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) stepj(j, f0 + j * step);
     }
+#pragma unroll
+    for (int j = 0; j < NB - 1; ++j)
+        if (f0 + j * step < nf) stepj(j, f0 + j * step);
     __syncthreads();
 }
 

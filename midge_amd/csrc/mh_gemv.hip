@@ -23,15 +23,13 @@ k_gemv(const uint8_t *__restrict__ W, const void *__restrict__ S, const float *_
     const int b = blockIdx.y;
     const int r0 = blockIdx.x * rpb;
     const int nf = min(rpb, rows - r0);
-    const size_t rowbytes = (size_t)C * 16 * gemv_chunk<DT>::W;
+    const uint32_t rowbytes = (uint32_t)C * 16u * gemv_chunk<DT>::W;
     float xr[E];
     load_x<DT>(X + (size_t)b * cols, C, ns, xr);
-    const uint16_t *S16 = (const uint16_t *)S;
+    const mh_rsrc rd = gemv_rsrc(W + (size_t)r0 * rowbytes, (uint32_t)nf * rowbytes);
+    const mh_rsrc rs = gemv_rsrc((const uint16_t *)S + (size_t)r0 * C, (uint32_t)nf * (uint32_t)C * 2u);
     block_gemv<DT>(
-        [&](int f) {
-            int r = r0 + f;
-            return RowRef{W + (size_t)r * rowbytes, S16 + (size_t)r * C};
-        },
+        rd, rs, [&](int f) { return RowOff{mul24((uint32_t)f, rowbytes), mul24((uint32_t)f, 2u * C)}; },
         nf, C, ns, xr, red, res);
     for (int f = threadIdx.x; f < nf; f += blockDim.x) {
         float v = res[f];

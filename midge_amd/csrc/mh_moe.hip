@@ -157,15 +157,18 @@ k_expert_gu(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restri
     float *res = lds;              // [2 * rpb]
     float *red = lds + 2 * rpb;    // [U][ns][C]
     const uint8_t *base = A.experts + (uint64_t)e * A.stride;
-    const size_t rowbytes = (size_t)C * 16 * gemv_chunk<DT>::W;
-    const size_t srow = (DT == MH_DT_Q8R) ? 0 : (size_t)C;   // f16 scales per row (4-bit)
+    const uint32_t rowbytes = (uint32_t)C * 16u * gemv_chunk<DT>::W;
+    const uint32_t srow = (DT == MH_DT_Q8R) ? 0u : 2u * (uint32_t)C;   // f16 scale bytes per row (4-bit)
     float xr[CE];
     load_x<DT>(xb + (size_t)(a / A.k) * A.hidden, C, ns, xr);
+    const mh_rsrc rx = gemv_rsrc(base, (uint32_t)A.stride);   // stride < 4 GiB: checked at launch
+    const uint32_t od[2] = {(uint32_t)A.off[0], (uint32_t)A.off[3]}, os[2] = {(uint32_t)A.off[1], (uint32_t)A.off[4]};
     block_gemv<DT>(
+        rx, rx,
         [&](int f) {
-            const int m = f & 1, r = r0 + (f >> 1);
-            return RowRef{base + A.off[3 * m] + (size_t)r * rowbytes,
-                          (const uint16_t *)(base + A.off[3 * m + 1]) + (size_t)r * srow};
+            const int m = f & 1;
+            const uint32_t r = (uint32_t)(r0 + (f >> 1));
+            return RowOff{(m ? od[1] : od[0]) + mul24(r, rowbytes), (m ? os[1] : os[0]) + mul24(r, srow)};
         },
         2 * nr, C, ns, xr, red, res);
     const float *bg = (const float *)(base + A.off[2]);
@@ -205,15 +208,17 @@ k_expert_down(ExpertArgs A, const int32_t *__restrict__ sel, const float *__rest
     float *res = lds;
     float *red = lds + rpb;
     const uint8_t *base = A.experts + (uint64_t)e * A.stride;
-    const size_t rowbytes = (size_t)C * 16 * gemv_chunk<DT>::W;
-    const size_t srow = (DT == MH_DT_Q8R) ? 0 : (size_t)C;
+    const uint32_t rowbytes = (uint32_t)C * 16u * gemv_chunk<DT>::W;
+    const uint32_t srow = (DT == MH_DT_Q8R) ? 0u : 2u * (uint32_t)C;
     float xr[CE];
     load_x<DT>(h + (size_t)a * A.ffn, C, ns, xr);
+    const mh_rsrc rx = gemv_rsrc(base, (uint32_t)A.stride);
+    const uint32_t od = (uint32_t)A.off[6], os = (uint32_t)A.off[7];
     block_gemv<DT>(
+        rx, rx,
         [&](int f) {
-            const int r = r0 + f;
-            return RowRef{base + A.off[6] + (size_t)r * rowbytes,
-                          (const uint16_t *)(base + A.off[7]) + (size_t)r * srow};
+            const uint32_t r = (uint32_t)(r0 + f);
+            return RowOff{od + mul24(r, rowbytes), os + mul24(r, srow)};
         },
         nr, C, ns, xr, red, res);
     const float *bd = (const float *)(base + A.off[8]);
@@ -419,7 +424,10 @@ int validate_layer(const mh_moe_layer *L) {
     if (L->expert_stride != ((pos + 63) & ~63ull))
         return fail(MH_E_ARG, "layer: expert_stride=%llu, expected %llu", (unsigned long long)L->expert_stride,
                     (unsigned long long)((pos + 63) & ~63ull));
-    const int ce = (L->expert_dt == MH_DT_F32) ? 4 : (L->expert_dt == MH_DT_Q8R) ? 16 : 32;
+    if (L->expert_stride > 0xFFFFFFFFull)   // the kernels address an expert with 32-bit offsets
+        return fail(MH_E_UNSUPPORTED, "layer: expert_stride=%llu exceeds 4 GiB", (unsigned long long)L->expert_stride);
+    // elements per chunk of the GEMV engine (gemv_chunk<DT>::E)
+    const int ce = (L->expert_dt == MH_DT_F32) ? 4 : 32;
     if (L->hidden % ce || L->ffn % ce || L->hidden / ce > kGemvThreads || L->ffn / ce > kGemvThreads)
         return fail(MH_E_UNSUPPORTED, "layer: hidden=%lld / ffn=%lld not a multiple of %d elements or wider "
                     "than %d chunks", (long long)L->hidden, (long long)L->ffn, ce, kGemvThreads);
