@@ -250,7 +250,7 @@ k_combine_decode(float *__restrict__ x, const float *__restrict__ ye, const floa
 // order (slot order among equal ids, as the reference's loops give).
 __global__ void __launch_bounds__(256)
 k_combine_prefill(float *__restrict__ x, const float *__restrict__ ye, const int32_t *__restrict__ sel,
-                  const float *__restrict__ w, int64_t H, int k) {
+                  const float *__restrict__ w, int64_t H, int k, int E) {
 #pragma clang fp contract(off)
     const int t = blockIdx.y;
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -268,6 +268,8 @@ k_combine_prefill(float *__restrict__ x, const float *__restrict__ ye, const int
     float acc = x[(size_t)t * H + r];
     for (int j = 0; j < k; ++j) {
         const int i = order[j];
+        const int e = sel[(size_t)t * k + i];
+        if (e < 0 || e >= E) continue;   // an unroutable slot adds nothing (its ye row is not written)
         acc = acc + w[(size_t)t * k + i] * ye[((size_t)t * k + i) * H + r];
     }
     x[(size_t)t * H + r] = acc;
@@ -385,7 +387,7 @@ int run_expert_major(const DevLayer &L, int n, const float *xb, const int32_t *s
     if (prefill_mfma_ok(L)) MH_TRY(run_expert_major_mfma(L, n, xb, sel, b.ye, s));
     else MH_TRY(launch_experts(L, n * L.top_k, sel, xb, b.h, b.ye, s));
     MH_LAUNCH("combine_prefill", k_combine_prefill, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s,
-                       x, b.ye, sel, w, L.hidden, L.top_k);
+                       x, b.ye, sel, w, L.hidden, L.top_k, L.n_experts);
     return hip_check(hipGetLastError(), "prefill combine launch");
 }
 

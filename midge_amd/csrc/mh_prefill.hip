@@ -53,36 +53,63 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------- lists
 
-__global__ void k_plist_count(const int32_t *sel, int N, int E, int *cnt, int *rank) {
-    const int a = blockIdx.x * blockDim.x + threadIdx.x;
-    if (a >= N) return;
-    const int e = sel[a];
-    rank[a] = (e >= 0 && e < E) ? atomicAdd(&cnt[e], 1) : -1;
-}
-
-__global__ void k_plist_offsets(const int *cnt, int E, int *offs) {
-    if (threadIdx.x == 0) {
-        int s = 0;
-        for (int e = 0; e < E; ++e) {
-            offs[e] = s;
-            s += cnt[e];
+// The lists in one block (E <= kPlistMaxE): ranks by LDS atomics, an
+// exclusive scan of the counts, then the scatter. Positions within an
+// expert's list follow the atomics' order; every output is per assignment,
+// so the order does not change any result.
+constexpr int kPlistMaxE = 4096;
+__global__ void __launch_bounds__(1024)
+k_plist_one(const int32_t *sel, int N, int E, int k, int *rank, int *offs, int *list_tok, int *slot_of) {
+    __shared__ int cnt[kPlistMaxE];
+    __shared__ int wsum[16];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    for (int i = t; i < E; i += 1024) cnt[i] = 0;
+    __syncthreads();
+    for (int a = t; a < N; a += 1024) {
+        const int e = sel[a];
+        rank[a] = (e >= 0 && e < E) ? atomicAdd(&cnt[e], 1) : -1;
+    }
+    __syncthreads();
+    // thread t owns counters [t * ch, t * ch + ch): local sum, block scan
+    const int ch = (E + 1023) / 1024;
+    int own = 0;
+    for (int i = 0; i < ch; ++i) {
+        const int e = t * ch + i;
+        if (e < E) own += cnt[e];
+    }
+    int v = own;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
+    }
+    if (lane == 63) wsum[wv] = v;
+    __syncthreads();
+    int run = v - own, total = 0;
+    for (int i = 0; i < 16; ++i) {
+        if (i < wv) run += wsum[i];
+        total += wsum[i];
+    }
+    for (int i = 0; i < ch; ++i) {
+        const int e = t * ch + i;
+        if (e < E) {
+            const int c = cnt[e];
+            cnt[e] = run;
+            offs[e] = run;
+            run += c;
         }
-        offs[E] = s;
+    }
+    if (t == 0) offs[E] = total;
+    __syncthreads();
+    for (int a = t; a < N; a += 1024) {
+        const int r = rank[a];
+        if (r >= 0) {
+            const int p = cnt[sel[a]] + r;
+            list_tok[p] = a / k;
+            slot_of[p] = a;
+        }
     }
 }
 
-__global__ void k_plist_scatter(const int32_t *sel, const int *rank, const int *offs, int N, int k, int *list_tok,
-                                int *slot_of) {
-    const int a = blockIdx.x * blockDim.x + threadIdx.x;
-    if (a >= N || rank[a] < 0) return;
-    const int p = offs[sel[a]] + rank[a];
-    list_tok[p] = a / k;
-    slot_of[p] = a;
-}
-
-__global__ void k_fill_i32(int *p, int n, int v) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
-}
 
 // ---------------------------------------------------------------- quantize
 
@@ -94,11 +121,11 @@ __device__ __forceinline__ int fp8_block_exp(float m) {
 }
 
 // Rows of K f32 (row r of the input = in[(map ? map[r] : r) * K ...]) ->
-// kTerms planes q[t][r][K] (e4m3) and sc[t][r][K / 32] (e8m0), one scale per
-// 32-column block b (thread = (row, block)).
+// kTerms planes q[t][r][K] (e4m3) and sc[t][r][scs] (e8m0, scs >= K / 32: rows
+// padded to 16 bytes), one scale per 32-column block b (thread = (row, block)).
 __global__ void __launch_bounds__(256)
 k_quant_terms(const float *__restrict__ in, const int *__restrict__ map, int rows, int K,
-              uint8_t *__restrict__ q, uint8_t *__restrict__ sc) {
+              uint8_t *__restrict__ q, uint8_t *__restrict__ sc, int scs) {
     const int nb = K / 32;
     const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= (int64_t)rows * nb) return;
@@ -133,7 +160,7 @@ k_quant_terms(const float *__restrict__ in, const int *__restrict__ map, int row
         uint8_t *qr = q + ((int64_t)t * rows + r) * K + 32 * b;
         *(uint4 *)qr = make_uint4(w[0], w[1], w[2], w[3]);
         *(uint4 *)(qr + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-        sc[((int64_t)t * rows + r) * nb + b] = (uint8_t)(e + 127);
+        sc[((int64_t)t * rows + r) * scs + b] = (uint8_t)(e + 127);
     }
 }
 
@@ -164,15 +191,37 @@ __device__ __forceinline__ int e8m0_of_f16(uint32_t h, unsigned *bad) {
     return (int)((f >> 23) & 0xFFu);  // a zero scale (an e8m0 below f16's range) becomes 2^-127
 }
 
-// LDS of the GEMM block: two buffers of one K step's B operands for every
-// (term, token tile, half, lane) as 16-byte pieces, their scales, and one
-// 32 x 33 transpose tile per wave.
+// LDS of the GEMM block, for K columns and nmat weight matrices:
+//   bbuf   two buffers of one K step's B operands for every (term, token
+//          tile, half, lane) as 16-byte pieces
+//   tiles  one 32 x 33 f32 transpose tile per wave
+//   asc    the f16 scales of each wave's 32 weight rows, all of K (loaded
+//          once per block: [wave][matrix][row][K / 32])
+//   bsc    the e8m0 scales of the pass's tokens, all of K ([term][token]
+//          rows of bss bytes: 8-aligned, +8 so that 32 lanes reading one
+//          column fall in distinct banks)
 constexpr int kBPieces = kTerms * kNT * 2 * 64;              // 16-byte pieces per K step
-constexpr int kBScales = kTerms * kNT * 64;                  // scale bytes per K step
 constexpr int kPiecesPerThread = kBPieces / (64 * kWaves);   // 6
-constexpr int kScalesPerThread = (kBScales + 64 * kWaves - 1) / (64 * kWaves);
-constexpr size_t kGemmLds = 2 * (size_t)kBPieces * 16 + 2 * (size_t)kBScales + sizeof(float) * kWaves * 32 * 33;
 static_assert(kBPieces % (64 * kWaves) == 0, "B pieces must split evenly over the block");
+constexpr size_t kLdsMax = 160 * 1024;                       // LDS per workgroup on gfx950
+
+// e8m0 scale row stride of the quantized activations in memory (16-byte rows)
+__host__ __device__ inline int bscale_stride(int K) { return ((K / 32) + 15) & ~15; }
+
+struct GemmLds {
+    size_t tiles, asc, bsc, total;
+    int bss;
+};
+__host__ __device__ inline GemmLds gemm_lds(int K, int nmat) {
+    const int nsc = K / 32;
+    GemmLds L;
+    L.bss = ((nsc + 7) & ~7) + 8;
+    L.tiles = 2 * (size_t)kBPieces * 16;
+    L.asc = L.tiles + sizeof(float) * kWaves * 32 * 33;
+    L.bsc = L.asc + (size_t)kWaves * nmat * 32 * nsc * 2;
+    L.total = L.bsc + (size_t)kTerms * kNT * 32 * L.bss;
+    return L;
+}
 
 // MODE 0: gate/up (K = H, rows = F, B rows = tokens through list_tok);
 // MODE 1: down (K = F, rows = H, B rows = list positions).
@@ -183,15 +232,25 @@ static_assert(kBPieces % (64 * kWaves) == 0, "B pieces must split evenly over th
 // steps ahead in registers.
 template <int MODE>
 __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
+    constexpr int NM = MODE == 0 ? 2 : 1;   // weight matrices: gate and up, or down
     extern __shared__ __attribute__((aligned(16))) uint8_t glds[];
-    mh_u4 *bbuf = (mh_u4 *)glds;                                    // [2][kBPieces]
-    uint8_t *sbuf = glds + 2 * (size_t)kBPieces * 16;                // [2][kBScales]
-    float(*tiles)[32][33] = (float(*)[32][33])(sbuf + 2 * kBScales);
     const int K = MODE == 0 ? A.H : A.F;
+    const GemmLds LL = gemm_lds(K, NM);
+    mh_u4 *bbuf = (mh_u4 *)glds;                                    // [2][kBPieces]
+    float(*tiles)[32][33] = (float(*)[32][33])(glds + LL.tiles);
+    uint16_t *asc = (uint16_t *)(glds + LL.asc);
+    uint8_t *bsc = glds + LL.bsc;
+    const int bss = LL.bss, scs = bscale_stride(K);
     const int R = MODE == 0 ? A.F : A.H;
     const int RT = R / 32;
     const int groups = (RT + kWaves - 1) / kWaves;
-    const int e = blockIdx.x / groups, rgrp = blockIdx.x - e * groups;
+    // XCD-aware order: the dispatcher deals blocks to the 8 XCDs round
+    // robin (block b to XCD b % 8), so logical block lin = (b % 8) * (nb / 8)
+    // + b / 8 puts an expert's row groups on one XCD, where its tokens' B
+    // operands stay in that XCD's L2 (the grid is a multiple of 8)
+    const int lin = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+    if (lin >= A.E * groups) return;   // block-uniform: padding to a multiple of 8
+    const int e = lin / groups, rgrp = lin - e * groups;
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int rt = rgrp * kWaves + wave;
     const bool wact = rt < RT;                 // inactive waves still stage B
@@ -202,37 +261,55 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
     const uint8_t *ex = A.experts + (uint64_t)e * A.stride;
     const int rowbytes = K / 2, nsc = K / 32, steps = K / 64;
     const uint8_t *a0 = ex + A.off[MODE == 0 ? 0 : 6] + (size_t)row * rowbytes;
-    const uint16_t *s0 = (const uint16_t *)(ex + A.off[MODE == 0 ? 1 : 7]) + (size_t)row * nsc;
     const uint8_t *a1 = ex + A.off[3] + (size_t)row * rowbytes;
-    const uint16_t *s1 = (const uint16_t *)(ex + A.off[4]) + (size_t)row * nsc;
     unsigned bad = 0;
     float(*tl)[33] = tiles[wave];
+    // the wave's weight scales, all of K, as contiguous dwords (the 32 rows'
+    // scales are one run: 32 * nsc u16, nsc even); read by this wave only
+    uint16_t *wsc = asc + (size_t)wave * NM * 32 * nsc;
+    if (wact) {
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) {
+            const uint32_t *src = (const uint32_t *)((const uint16_t *)(ex + A.off[MODE == 0 ? 1 + 3 * mt : 7]) +
+                                                     (size_t)rt * 32 * nsc);
+            uint32_t *dst = (uint32_t *)(wsc + (size_t)mt * 32 * nsc);
+            for (int k = l; k < 16 * nsc; k += 64) dst[k] = src[k];
+        }
+    }
     for (int p0 = 0; p0 < T; p0 += 32 * kNT) {
         const int nt = min(kNT, (T - p0 + 31) / 32);
-        // this thread's B pieces: q = tid + 256 i -> (term, tile, half, lane)
+        // this thread's B pieces: q = tid + 256 i -> (term t, tile j, token
+        // n, quarter c) with c fastest, so one load instruction reads 64
+        // contiguous bytes (a K step) of each of 16 tokens; the store puts
+        // quarter c = g + 2 half into the operand slot (t, j, half) lane 32 g
+        // + n. Branch-free: tiles past nt read tile nt - 1 and list positions
+        // past T read position T - 1 (their columns are not stored).
         const uint8_t *bsrc[kPiecesPerThread];
+        int bdst[kPiecesPerThread];
 #pragma unroll
         for (int i = 0; i < kPiecesPerThread; ++i) {
             const int q = tid + 64 * kWaves * i;
-            const int lane = q & 63, half = (q >> 6) & 1, j = (q >> 7) % kNT, t = q / (128 * kNT);
-            const int p = p0 + 32 * j + (lane & 31);
-            int br = -1;
-            if (j < nt && p < T) br = MODE == 0 ? A.list_tok[base + p] : base + p;
-            bsrc[i] = br < 0 ? nullptr
-                             : A.bq + ((size_t)t * A.b_rows + br) * K + 16 * (lane >> 5) + 32 * half;
+            const int c = q & 3, n = (q >> 2) & 31, jj = (q >> 7) % kNT, t = q / (128 * kNT);
+            const int j = min(jj, nt - 1);
+            const int p = min(p0 + 32 * j + n, T - 1);
+            const int br = MODE == 0 ? A.list_tok[base + p] : base + p;
+            bsrc[i] = A.bq + ((size_t)t * A.b_rows + br) * K + 16 * c;
+            bdst[i] = ((t * kNT + jj) * 2 + (c >> 1)) * 64 + 32 * (c & 1) + n;
         }
-        const uint8_t *ssrc[kScalesPerThread];
-#pragma unroll
-        for (int i = 0; i < kScalesPerThread; ++i) {
-            const int q = tid + 64 * kWaves * i;
-            ssrc[i] = nullptr;
-            if (q < kBScales) {
-                const int lane = q & 63, j = (q >> 6) % kNT, t = q / (64 * kNT);
-                const int p = p0 + 32 * j + (lane & 31);
-                if (j < nt && p < T) {
-                    const int br = MODE == 0 ? A.list_tok[base + p] : base + p;
-                    ssrc[i] = A.bs + ((size_t)t * A.b_rows + br) * nsc + (lane >> 5);
-                }
+        // the pass's activation scales, all of K: rows (term, token) of scs
+        // bytes in memory (16-byte pieces) into LDS rows of bss bytes; the
+        // previous pass ended with a barrier, so bsc is free
+        {
+            const int pr = scs / 16, nrow = kTerms * kNT * 32;
+            for (int q = tid; q < nrow * pr; q += 64 * kWaves) {
+                const int ri = q / pr, pc = q - ri * pr;
+                const int t = ri / (kNT * 32), tok = ri - t * (kNT * 32);
+                const int p = min(p0 + tok, T - 1);
+                const int br = MODE == 0 ? A.list_tok[base + p] : base + p;
+                const mh_u4 v = mh_load16(mh_global(A.bs + ((size_t)t * A.b_rows + br) * scs + 16 * pc));
+                uint2 *d = (uint2 *)(bsc + (size_t)ri * bss + 16 * pc);
+                d[0] = make_uint2(v.x, v.y);
+                d[1] = make_uint2(v.z, v.w);
             }
         }
         v16f acc0[kNT], acc1[kNT];
@@ -241,94 +318,79 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
             acc0[j] = v16f{};
             acc1[j] = v16f{};
         }
-        // stage step 0
-        {
-            mh_u4 rb[kPiecesPerThread];
-            uint32_t rs[kScalesPerThread];
-#pragma unroll
-            for (int i = 0; i < kPiecesPerThread; ++i)
-                rb[i] = bsrc[i] ? *(const mh_u4 *)bsrc[i] : mh_u4{0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int i = 0; i < kScalesPerThread; ++i) rs[i] = ssrc[i] ? *ssrc[i] : 0u;
-#pragma unroll
-            for (int i = 0; i < kPiecesPerThread; ++i) bbuf[tid + 64 * kWaves * i] = rb[i];
-#pragma unroll
-            for (int i = 0; i < kScalesPerThread; ++i)
-                if (tid + 64 * kWaves * i < kBScales) sbuf[tid + 64 * kWaves * i] = (uint8_t)rs[i];
-        }
-        // A for steps 0 and 1
+        // Register sets are indexed at compile time (a runtime index turns
+        // every load into a wait and an indexed move): A (weights) in three
+        // sets and B in two, both loaded two steps ahead, B then staged into
+        // two LDS buffers. Steps run in groups of 6 = lcm(3, 2).
         mh_u4 wa0[3], wa1[3];
-        uint32_t ws0[3], ws1[3];
+        mh_u4 rb[2][kPiecesPerThread];
+        auto load_a = [&](int set, int st) {
+            const int c = 2 * min(st, steps - 1) + g;
+            wa0[set] = mh_load16(mh_global(a0 + c * 16));
+            if constexpr (MODE == 0) wa1[set] = mh_load16(mh_global(a1 + c * 16));
+        };
+        auto load_b = [&](int set, int st) {
+            const int sc = min(st, steps - 1);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int c = 2 * min(u, steps - 1) + g;
-            wa0[u] = mh_load16(mh_global(a0 + c * 16));
-            ws0[u] = mh_load_u16(mh_global(s0 + c));
+            for (int i = 0; i < kPiecesPerThread; ++i) rb[set][i] = mh_load16(mh_global(bsrc[i] + 64 * sc));
+        };
+        auto store_b = [&](int set, int buf) {
+            mh_u4 *nb = bbuf + (size_t)buf * kBPieces;
+#pragma unroll
+            for (int i = 0; i < kPiecesPerThread; ++i) nb[bdst[i]] = rb[set][i];
+        };
+        auto math = [&](int u, int buf, int st) {
+            const int blk = 2 * st + g;   // this lane's scale block
+            v8i qa0 = {}, qa1 = {};
+            qa0[0] = (int)wa0[u].x; qa0[1] = (int)wa0[u].y; qa0[2] = (int)wa0[u].z; qa0[3] = (int)wa0[u].w;
+            const int sa0 = e8m0_of_f16(wsc[(size_t)m * nsc + blk], &bad);
+            int sa1 = 127;
             if constexpr (MODE == 0) {
-                wa1[u] = mh_load16(mh_global(a1 + c * 16));
-                ws1[u] = mh_load_u16(mh_global(s1 + c));
+                qa1[0] = (int)wa1[u].x; qa1[1] = (int)wa1[u].y; qa1[2] = (int)wa1[u].z; qa1[3] = (int)wa1[u].w;
+                sa1 = e8m0_of_f16(wsc[(size_t)(32 + m) * nsc + blk], &bad);
             }
-        }
-        __syncthreads();
-        for (int s = 0; s < steps; ++s) {
-            const int cur = s & 1;
-            // memory for step s+1 (B pieces, into registers) and step s+2 (A)
-            mh_u4 rb[kPiecesPerThread];
-            uint32_t rs[kScalesPerThread];
-            const bool more = s + 1 < steps;
+            const mh_u4 *bb = bbuf + (size_t)buf * kBPieces;
 #pragma unroll
-            for (int i = 0; i < kPiecesPerThread; ++i)
-                rb[i] = (more && bsrc[i]) ? *(const mh_u4 *)(bsrc[i] + 64 * (s + 1)) : mh_u4{0u, 0u, 0u, 0u};
+            for (int t = 0; t < kTerms; ++t) {
 #pragma unroll
-            for (int i = 0; i < kScalesPerThread; ++i) rs[i] = (more && ssrc[i]) ? ssrc[i][2 * (s + 1)] : 0u;
-            {
-                const int c = 2 * min(s + 2, steps - 1) + g;
-                wa0[(s + 2) % 3] = mh_load16(mh_global(a0 + c * 16));
-                ws0[(s + 2) % 3] = mh_load_u16(mh_global(s0 + c));
-                if constexpr (MODE == 0) {
-                    wa1[(s + 2) % 3] = mh_load16(mh_global(a1 + c * 16));
-                    ws1[(s + 2) % 3] = mh_load_u16(mh_global(s1 + c));
+                for (int j = 0; j < kNT; ++j) {
+                    if (j >= nt) break;
+                    const mh_u4 lo = bb[((t * kNT + j) * 2 + 0) * 64 + l];
+                    const mh_u4 hi = bb[((t * kNT + j) * 2 + 1) * 64 + l];
+                    const v8i qb = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                                    (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+                    const int sbv = bsc[(size_t)((t * kNT + j) * 32 + m) * bss + blk];
+                    acc0[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa0, qb, acc0[j], 4, 0, 0, sa0, 0, sbv);
+                    if constexpr (MODE == 0)
+                        acc1[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa1, qb, acc1[j], 4, 0, 0, sa1, 0, sbv);
                 }
             }
-            if (wact) {
-                const int u = s % 3;
-                v8i qa0 = {}, qa1 = {};
-                qa0[0] = (int)wa0[u].x; qa0[1] = (int)wa0[u].y; qa0[2] = (int)wa0[u].z; qa0[3] = (int)wa0[u].w;
-                const int sa0 = e8m0_of_f16(ws0[u], &bad);
-                int sa1 = 127;
-                if constexpr (MODE == 0) {
-                    qa1[0] = (int)wa1[u].x; qa1[1] = (int)wa1[u].y; qa1[2] = (int)wa1[u].z; qa1[3] = (int)wa1[u].w;
-                    sa1 = e8m0_of_f16(ws1[u], &bad);
-                }
-                const mh_u4 *bb = bbuf + (size_t)cur * kBPieces;
-                const uint8_t *sb8 = sbuf + (size_t)cur * kBScales;
-#pragma unroll
-                for (int t = 0; t < kTerms; ++t) {
-#pragma unroll
-                    for (int j = 0; j < kNT; ++j) {
-                        if (j >= nt) break;
-                        const mh_u4 lo = bb[((t * kNT + j) * 2 + 0) * 64 + l];
-                        const mh_u4 hi = bb[((t * kNT + j) * 2 + 1) * 64 + l];
-                        const v8i qb = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-                        const int sbv = sb8[(t * kNT + j) * 64 + l];
-                        acc0[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa0, qb, acc0[j], 4, 0, 0, sa0, 0, sbv);
-                        if constexpr (MODE == 0)
-                            acc1[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa1, qb, acc1[j], 4, 0, 0, sa1, 0, sbv);
-                    }
-                }
-            }
-            if (more) {
-                mh_u4 *nb = bbuf + (size_t)(cur ^ 1) * kBPieces;
-#pragma unroll
-                for (int i = 0; i < kPiecesPerThread; ++i) nb[tid + 64 * kWaves * i] = rb[i];
-                uint8_t *ns = sbuf + (size_t)(cur ^ 1) * kBScales;
-#pragma unroll
-                for (int i = 0; i < kScalesPerThread; ++i)
-                    if (tid + 64 * kWaves * i < kBScales) ns[tid + 64 * kWaves * i] = (uint8_t)rs[i];
-            }
+        };
+        // step st at position j of its group: B and A of st + 2 issued, the
+        // MFMAs of st, then B of st + 1 (loaded a step ago) into the other
+        // LDS buffer: each load has two steps of MFMAs to arrive
+        auto step = [&](int j, int st) {
+            load_b(j % 2, st + 2);
+            load_a((j + 2) % 3, st + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            if (wact) math(j % 3, j % 2, st);
+            store_b((j + 1) % 2, (j + 1) % 2);
             __syncthreads();
+        };
+        load_b(0, 0);
+        store_b(0, 0);
+        load_b(1, 1);
+        load_a(0, 0);
+        load_a(1, 1);
+        __syncthreads();
+        int st = 0;
+        for (; st + 6 <= steps; st += 6) {
+#pragma unroll
+            for (int j = 0; j < 6; ++j) step(j, st + j);
         }
+#pragma unroll
+        for (int j = 0; j < 5; ++j)
+            if (st + j < steps) step(j, st + j);
         if (wact) {
             // epilogue through the wave's LDS tile: lane (m, g) owns column m
             // (token p0 + 32 j + m) and rows 8 (i / 4) + 4 g + i % 4; after the
@@ -379,25 +441,28 @@ unsigned *g_scale_err_dev = nullptr;
 }  // namespace
 
 // True when the scaled-MFMA path handles this layer (MXFP4 experts, shapes
-// that tile by 64 along K and 32 along rows).
+// that tile by 64 along K and 32 along rows, whose scales fit the GEMM's LDS).
 bool prefill_mfma_ok(const DevLayer &L) {
     const char *off = getenv("MIDGE_HIP_NO_MFMA");
     if (off && off[0] && off[0] != '0') return false;
     return L.expert_dt == MH_DT_MXFP4 && L.hidden % 64 == 0 && L.ffn % 64 == 0 && L.top_k >= 1 &&
-           L.n_experts <= 65535;
+           L.n_experts <= kPlistMaxE && L.hidden <= INT32_MAX && L.ffn <= INT32_MAX &&
+           gemm_lds((int)L.hidden, 2).total <= kLdsMax && gemm_lds((int)L.ffn, 1).total <= kLdsMax;
 }
 
 // Expert-major MoE of n tokens: x[t] += sum over t's slots, in ascending
 // expert order, of w * expert(xb[t]); ye is [n * k][H] scratch read by the
-// prefill combine (launched by the caller).
+// prefill combine (launched by the caller), written for routed slots only.
 int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32_t *sel, float *ye,
                           hipStream_t s) {
     const int k = L.top_k, E = L.n_experts, N = n * k;
     const int H = (int)L.hidden, F = (int)L.ffn;
+    if (!prefill_mfma_ok(L)) return fail(MH_E_UNSUPPORTED, "prefill: layer shape not handled by the MFMA path");
+    const size_t lds_gu = gemm_lds(H, 2).total, lds_dn = gemm_lds(F, 1).total;
     static bool lds_set = false;
     if (!lds_set) {
-        MH_HIP(hipFuncSetAttribute((const void *)k_moe_gemm<0>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds));
-        MH_HIP(hipFuncSetAttribute((const void *)k_moe_gemm<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds));
+        MH_HIP(hipFuncSetAttribute((const void *)k_moe_gemm<0>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax));
+        MH_HIP(hipFuncSetAttribute((const void *)k_moe_gemm<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax));
         lds_set = true;
     }
     if (!g_scale_err) {
@@ -406,26 +471,21 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
         MH_HIP(hipHostGetDevicePointer((void **)&g_scale_err_dev, g_scale_err, 0));
         watch_async_error(g_scale_err, "prefill: an MXFP4 scale is not a positive power of two (e8m0 cannot hold it)");
     }
-    // lists: cnt[E], offs[E + 1], rank[N], list_tok[N], slot_of[N]
+    // lists: offs[E + 1], rank[N], list_tok[N], slot_of[N]
     void *pl;
-    MH_TRY(scratch(S_LIST, sizeof(int) * ((size_t)2 * E + 1 + 3 * (size_t)N), &pl));
-    int *cnt = (int *)pl, *offs = cnt + E, *rank = offs + E + 1, *list_tok = rank + N, *slot_of = list_tok + N;
+    MH_TRY(scratch(S_LIST, sizeof(int) * ((size_t)E + 1 + 3 * (size_t)N), &pl));
+    int *offs = (int *)pl, *rank = offs + E + 1, *list_tok = rank + N, *slot_of = list_tok + N;
     // quantized activations: the larger of x (n rows of H) and h (N rows of F)
     const size_t qx = (size_t)kTerms * n * H, qh = (size_t)kTerms * N * F;
-    const size_t qbytes = std::max(qx + qx / 32, qh + qh / 32);
+    const size_t qbytes = std::max(qx + (size_t)kTerms * n * bscale_stride(H), qh + (size_t)kTerms * N * bscale_stride(F));
     void *pq, *ph;
     MH_TRY(scratch(S_Q, qbytes, &pq));
     MH_TRY(scratch(S_H, sizeof(float) * (size_t)N * F, &ph));
     uint8_t *q = (uint8_t *)pq;
     float *hbuf = (float *)ph;
 
-    MH_LAUNCH("plist", k_fill_i32, dim3(1), dim3(256), 0, s, cnt, E, 0);
-    MH_LAUNCH("plist", k_plist_count, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, sel, N, E, cnt, rank);
-    MH_LAUNCH("plist", k_plist_offsets, dim3(1), dim3(64), 0, s, cnt, E, offs);
-    MH_LAUNCH("plist", k_plist_scatter, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, sel, rank, offs, N, k,
-              list_tok, slot_of);
-    // ye rows of unfilled slots stay zero (a fill kernel: callers may capture this in a graph)
-    MH_LAUNCH("plist", k_fill_i32, dim3(1024), dim3(256), 0, s, (int *)ye, N * H, 0);
+    MH_LAUNCH("plist", k_plist_one, dim3(1), dim3(1024), 0, s, sel, N, E, k, rank, offs, list_tok, slot_of);
+    // ye rows of unroutable slots are not written: the combine skips them
 
     GemmArgs A;
     A.experts = L.experts;
@@ -451,9 +511,10 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
         A.bs = q + (size_t)kTerms * n * H;
         A.b_rows = n;
         MH_LAUNCH("quant_x", k_quant_terms, dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, xb, nullptr, n, H,
-                  q, q + (size_t)kTerms * n * H);
+                  q, q + (size_t)kTerms * n * H, bscale_stride(H));
         const int groups = (F / 32 + kWaves - 1) / kWaves;
-        MH_LAUNCH("moe_gu_mfma", k_moe_gemm<0>, dim3((unsigned)(E * groups)), dim3(64 * kWaves), kGemmLds, s, A);
+        MH_LAUNCH("moe_gu_mfma", k_moe_gemm<0>, dim3((unsigned)((E * groups + 7) / 8 * 8)), dim3(64 * kWaves), lds_gu,
+                  s, A);
     }
     // down over the quantized h (list order)
     {
@@ -462,9 +523,10 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
         A.bs = q + (size_t)kTerms * N * F;
         A.b_rows = N;
         MH_LAUNCH("quant_h", k_quant_terms, dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, hbuf, nullptr, N,
-                  F, q, q + (size_t)kTerms * N * F);
+                  F, q, q + (size_t)kTerms * N * F, bscale_stride(F));
         const int groups = (H / 32 + kWaves - 1) / kWaves;
-        MH_LAUNCH("moe_down_mfma", k_moe_gemm<1>, dim3((unsigned)(E * groups)), dim3(64 * kWaves), kGemmLds, s, A);
+        MH_LAUNCH("moe_down_mfma", k_moe_gemm<1>, dim3((unsigned)((E * groups + 7) / 8 * 8)), dim3(64 * kWaves),
+                  lds_dn, s, A);
     }
     return hip_check(hipGetLastError(), "prefill MFMA launches");
 }
