@@ -37,6 +37,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "mh_internal.h"
 
@@ -201,8 +202,7 @@ __device__ __forceinline__ int e8m0_of_f16(uint32_t h, unsigned *bad) {
 //          rows of bss bytes: 8-aligned, +8 so that 32 lanes reading one
 //          column fall in distinct banks)
 constexpr int kBPieces = kTerms * kNT * 2 * 64;              // 16-byte pieces per K step
-constexpr int kPiecesPerThread = kBPieces / (64 * kWaves);   // 6
-static_assert(kBPieces % (64 * kWaves) == 0, "B pieces must split evenly over the block");
+static_assert(kTerms * 128 == 64 * kWaves + 128, "a tile's B pieces: one per thread, two in waves 0-1");
 constexpr size_t kLdsMax = 160 * 1024;                       // LDS per workgroup on gfx950
 
 // e8m0 scale row stride of the quantized activations in memory (16-byte rows)
@@ -266,50 +266,74 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
     float(*tl)[33] = tiles[wave];
     // the wave's weight scales, all of K, as contiguous dwords (the 32 rows'
     // scales are one run: 32 * nsc u16, nsc even); read by this wave only
+    // (loads in batches of 16 per lane, then the stores: one memory latency
+    // per batch instead of one per dword)
     uint16_t *wsc = asc + (size_t)wave * NM * 32 * nsc;
     if (wact) {
+        const int nd = 16 * nsc;   // dwords per matrix
 #pragma unroll
         for (int mt = 0; mt < NM; ++mt) {
             const uint32_t *src = (const uint32_t *)((const uint16_t *)(ex + A.off[MODE == 0 ? 1 + 3 * mt : 7]) +
                                                      (size_t)rt * 32 * nsc);
             uint32_t *dst = (uint32_t *)(wsc + (size_t)mt * 32 * nsc);
-            for (int k = l; k < 16 * nsc; k += 64) dst[k] = src[k];
+            for (int k0 = 0; k0 < nd; k0 += 64 * 16) {
+                uint32_t v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) v[u] = src[min(k0 + 64 * u + l, nd - 1)];
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    if (k0 + 64 * u + l < nd) dst[k0 + 64 * u + l] = v[u];
+            }
         }
     }
     for (int p0 = 0; p0 < T; p0 += 32 * kNT) {
         const int nt = min(kNT, (T - p0 + 31) / 32);
-        // this thread's B pieces: q = tid + 256 i -> (term t, tile j, token
-        // n, quarter c) with c fastest, so one load instruction reads 64
-        // contiguous bytes (a K step) of each of 16 tokens; the store puts
-        // quarter c = g + 2 half into the operand slot (t, j, half) lane 32 g
-        // + n. Branch-free: tiles past nt read tile nt - 1 and list positions
-        // past T read position T - 1 (their columns are not stored).
-        const uint8_t *bsrc[kPiecesPerThread];
-        int bdst[kPiecesPerThread];
+        // B pieces of tile j: 384 (term t, token n, quarter c), c fastest,
+        // so one load instruction reads 64 contiguous bytes (a K step) of
+        // each of 16 tokens. Thread tid loads piece tid (t = tid / 128) and,
+        // in waves 0-1, piece tid + 256 (t = 2), both of token n = (tid / 4)
+        // % 32 and quarter c = tid % 4; the store puts quarter c = g + 2 half
+        // into the operand slot (t, j, half) lane 32 g + n. Only the pass's
+        // nt tiles are loaded; list positions past T read position T - 1
+        // (their columns are not stored).
+        const int bc = tid & 3, bn = (tid >> 2) & 31, bt = tid >> 7;
+        const bool two = tid < 128;   // wave-uniform
+        const size_t tstride = (size_t)A.b_rows * K;
+        const uint8_t *bsrc[kNT];
 #pragma unroll
-        for (int i = 0; i < kPiecesPerThread; ++i) {
-            const int q = tid + 64 * kWaves * i;
-            const int c = q & 3, n = (q >> 2) & 31, jj = (q >> 7) % kNT, t = q / (128 * kNT);
-            const int j = min(jj, nt - 1);
-            const int p = min(p0 + 32 * j + n, T - 1);
+        for (int j = 0; j < kNT; ++j) {
+            const int p = min(p0 + 32 * min(j, nt - 1) + bn, T - 1);
             const int br = MODE == 0 ? A.list_tok[base + p] : base + p;
-            bsrc[i] = A.bq + ((size_t)t * A.b_rows + br) * K + 16 * c;
-            bdst[i] = ((t * kNT + jj) * 2 + (c >> 1)) * 64 + 32 * (c & 1) + n;
+            bsrc[j] = A.bq + (size_t)br * K + 16 * bc;
         }
+        auto bdst = [&](int t, int j) { return ((t * kNT + j) * 2 + (bc >> 1)) * 64 + 32 * (bc & 1) + bn; };
         // the pass's activation scales, all of K: rows (term, token) of scs
         // bytes in memory (16-byte pieces) into LDS rows of bss bytes; the
         // previous pass ended with a barrier, so bsc is free
         {
-            const int pr = scs / 16, nrow = kTerms * kNT * 32;
-            for (int q = tid; q < nrow * pr; q += 64 * kWaves) {
-                const int ri = q / pr, pc = q - ri * pr;
-                const int t = ri / (kNT * 32), tok = ri - t * (kNT * 32);
-                const int p = min(p0 + tok, T - 1);
-                const int br = MODE == 0 ? A.list_tok[base + p] : base + p;
-                const mh_u4 v = mh_load16(mh_global(A.bs + ((size_t)t * A.b_rows + br) * scs + 16 * pc));
-                uint2 *d = (uint2 *)(bsc + (size_t)ri * bss + 16 * pc);
-                d[0] = make_uint2(v.x, v.y);
-                d[1] = make_uint2(v.z, v.w);
+            const int pr = scs / 16, total = kTerms * kNT * 32 * pr;
+            constexpr int kB = 9;   // 16-byte pieces per thread per batch
+            for (int q0 = 0; q0 < total; q0 += 64 * kWaves * kB) {
+                mh_u4 v[kB];
+#pragma unroll
+                for (int u = 0; u < kB; ++u) {
+                    const int q = min(q0 + 64 * kWaves * u + tid, total - 1);
+                    const int ri = q / pr, pc = q - ri * pr;
+                    const int t = ri / (kNT * 32), tok = ri - t * (kNT * 32);
+                    const int p = min(p0 + tok, T - 1);
+                    const int br = MODE == 0 ? A.list_tok[base + p] : base + p;
+                    v[u] = mh_load16(mh_global(A.bs + ((size_t)t * A.b_rows + br) * scs + 16 * pc));
+                }
+#pragma unroll
+                for (int u = 0; u < kB; ++u) {
+                    const int q = q0 + 64 * kWaves * u + tid;
+                    if (q < total) {
+                        const int ri = q / pr, pc = q - ri * pr;
+                        uint2 *d = (uint2 *)(bsc + (size_t)ri * bss + 16 * pc);
+                        d[0] = make_uint2(v[u].x, v[u].y);
+                        d[1] = make_uint2(v[u].z, v[u].w);
+                    }
+                }
             }
         }
         v16f acc0[kNT], acc1[kNT];
@@ -323,23 +347,35 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
         // sets and B in two, both loaded two steps ahead, B then staged into
         // two LDS buffers. Steps run in groups of 6 = lcm(3, 2).
         mh_u4 wa0[3], wa1[3];
-        mh_u4 rb[2][kPiecesPerThread];
+        mh_u4 rb[2][2 * kNT];
         auto load_a = [&](int set, int st) {
             const int c = 2 * min(st, steps - 1) + g;
             wa0[set] = mh_load16(mh_global(a0 + c * 16));
             if constexpr (MODE == 0) wa1[set] = mh_load16(mh_global(a1 + c * 16));
         };
-        auto load_b = [&](int set, int st) {
+        auto load_b = [&](auto ntc, int set, int st) {
+            constexpr int NTT = decltype(ntc)::value;
             const int sc = min(st, steps - 1);
 #pragma unroll
-            for (int i = 0; i < kPiecesPerThread; ++i) rb[set][i] = mh_load16(mh_global(bsrc[i] + 64 * sc));
+            for (int j = 0; j < NTT; ++j) {
+                rb[set][2 * j] = mh_load16(mh_global(bsrc[j] + (size_t)bt * tstride + 64 * sc));
+                if (two) rb[set][2 * j + 1] = mh_load16(mh_global(bsrc[j] + 2 * tstride + 64 * sc));
+            }
         };
-        auto store_b = [&](int set, int buf) {
+        auto store_b = [&](auto ntc, int set, int buf) {
+            constexpr int NTT = decltype(ntc)::value;
             mh_u4 *nb = bbuf + (size_t)buf * kBPieces;
 #pragma unroll
-            for (int i = 0; i < kPiecesPerThread; ++i) nb[bdst[i]] = rb[set][i];
+            for (int j = 0; j < NTT; ++j) {
+                nb[bdst(bt, j)] = rb[set][2 * j];
+                if (two) nb[bdst(2, j)] = rb[set][2 * j + 1];
+            }
         };
-        auto math = [&](int u, int buf, int st) {
+        // the MFMAs of step st over NTT token tiles (NTT = nt as a compile-time
+        // instantiation: no per-tile guards), reading tile j + 1's B operands
+        // from LDS while tile j's MFMAs run
+        auto math = [&](auto ntc, int u, int buf, int st) {
+            constexpr int NTT = decltype(ntc)::value;
             const int blk = 2 * st + g;   // this lane's scale block
             v8i qa0 = {}, qa1 = {};
             qa0[0] = (int)wa0[u].x; qa0[1] = (int)wa0[u].y; qa0[2] = (int)wa0[u].z; qa0[3] = (int)wa0[u].w;
@@ -350,62 +386,105 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
                 sa1 = e8m0_of_f16(wsc[(size_t)(32 + m) * nsc + blk], &bad);
             }
             const mh_u4 *bb = bbuf + (size_t)buf * kBPieces;
+            v8i qb[2][kTerms];
+            int sbv[2][kTerms];
+            auto rd = [&](int j, int slot) {
 #pragma unroll
-            for (int t = 0; t < kTerms; ++t) {
-#pragma unroll
-                for (int j = 0; j < kNT; ++j) {
-                    if (j >= nt) break;
+                for (int t = 0; t < kTerms; ++t) {
                     const mh_u4 lo = bb[((t * kNT + j) * 2 + 0) * 64 + l];
                     const mh_u4 hi = bb[((t * kNT + j) * 2 + 1) * 64 + l];
-                    const v8i qb = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                                    (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-                    const int sbv = bsc[(size_t)((t * kNT + j) * 32 + m) * bss + blk];
-                    acc0[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa0, qb, acc0[j], 4, 0, 0, sa0, 0, sbv);
+                    qb[slot][t] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+                    sbv[slot][t] = bsc[(size_t)((t * kNT + j) * 32 + m) * bss + blk];
+                }
+            };
+            rd(0, 0);
+#pragma unroll
+            for (int j = 0; j < NTT; ++j) {
+                if (j + 1 < NTT) rd(j + 1, (j + 1) & 1);
+#pragma unroll
+                for (int t = 0; t < kTerms; ++t) {
+                    acc0[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa0, qb[j & 1][t], acc0[j], 4, 0, 0, sa0,
+                                                                             0, sbv[j & 1][t]);
                     if constexpr (MODE == 0)
-                        acc1[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa1, qb, acc1[j], 4, 0, 0, sa1, 0, sbv);
+                        acc1[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa1, qb[j & 1][t], acc1[j], 4, 0, 0,
+                                                                                 sa1, 0, sbv[j & 1][t]);
                 }
             }
+            // pin that order for the scheduler (left alone, it reuses one
+            // operand set and waits for every read): the weight scales and
+            // tile 0's reads, then per tile the next tile's reads (9 DS
+            // reads) ahead of this tile's MFMAs
+            constexpr int kDsRead = 0x100, kMfma = 0x008, kPerTile = kTerms * NM;
+            __builtin_amdgcn_sched_group_barrier(kDsRead, 3 * kTerms + NM, 0);
+#pragma unroll
+            for (int j = 0; j + 1 < NTT; ++j) {
+                __builtin_amdgcn_sched_group_barrier(kDsRead, 3 * kTerms, 0);
+                __builtin_amdgcn_sched_group_barrier(kMfma, kPerTile, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(kMfma, kPerTile, 0);
         };
         // step st at position j of its group: B and A of st + 2 issued, the
         // MFMAs of st, then B of st + 1 (loaded a step ago) into the other
         // LDS buffer: each load has two steps of MFMAs to arrive
-        auto step = [&](int j, int st) {
-            load_b(j % 2, st + 2);
-            load_a((j + 2) % 3, st + 2);
-            __builtin_amdgcn_sched_barrier(0);
-            if (wact) math(j % 3, j % 2, st);
-            store_b((j + 1) % 2, (j + 1) % 2);
+        auto run_steps = [&](auto ntc) {
+            load_b(ntc, 0, 0);
+            store_b(ntc, 0, 0);
+            load_b(ntc, 1, 1);
+            load_a(0, 0);
+            load_a(1, 1);
             __syncthreads();
+            auto step = [&](int j, int st) {
+                load_b(ntc, j % 2, st + 2);
+                load_a((j + 2) % 3, st + 2);
+                __builtin_amdgcn_sched_barrier(0);
+                if (wact) math(ntc, j % 3, j % 2, st);
+                store_b(ntc, (j + 1) % 2, (j + 1) % 2);
+                __syncthreads();
+            };
+            int st = 0;
+            for (; st + 6 <= steps; st += 6) {
+#pragma unroll
+                for (int j = 0; j < 6; ++j) step(j, st + j);
+            }
+#pragma unroll
+            for (int j = 0; j < 5; ++j)
+                if (st + j < steps) step(j, st + j);
         };
-        load_b(0, 0);
-        store_b(0, 0);
-        load_b(1, 1);
-        load_a(0, 0);
-        load_a(1, 1);
-        __syncthreads();
-        int st = 0;
-        for (; st + 6 <= steps; st += 6) {
-#pragma unroll
-            for (int j = 0; j < 6; ++j) step(j, st + j);
+        static_assert(kNT == 4, "one instantiation per tile count");
+        switch (nt) {   // block-uniform
+        case 1: run_steps(std::integral_constant<int, 1>{}); break;
+        case 2: run_steps(std::integral_constant<int, 2>{}); break;
+        case 3: run_steps(std::integral_constant<int, 3>{}); break;
+        default: run_steps(std::integral_constant<int, 4>{}); break;
         }
-#pragma unroll
-        for (int j = 0; j < 5; ++j)
-            if (st + j < steps) step(j, st + j);
         if (wact) {
             // epilogue through the wave's LDS tile: lane (m, g) owns column m
             // (token p0 + 32 j + m) and rows 8 (i / 4) + 4 g + i % 4; after the
-            // transpose lane l writes row 32 rt + m of tokens 2 q + g
+            // transpose lane l writes row 32 rt + m of tokens 2 q + g. The
+            // lane's 16 rows' biases are loaded once, together, before any
+            // store (stores may alias them, so they are not reloaded per tile)
+            float bias0[16], bias1[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const size_t grow4 = (size_t)(rt * 32 + 8 * (i / 4) + 4 * g + (i % 4)) * 4;
+                bias0[i] = *(const float *)(ex + A.off[MODE == 0 ? 2 : 8] + grow4);
+                if constexpr (MODE == 0) bias1[i] = *(const float *)(ex + A.off[5] + grow4);
+            }
 #pragma unroll
             for (int j = 0; j < kNT; ++j) {
                 if (j >= nt) break;
+                int dst[16];   // MODE 1: the slot of each token this lane writes
+                if constexpr (MODE == 1) {
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) dst[q] = A.slot_of[base + min(p0 + 32 * j + 2 * q + g, T - 1)];
+                }
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int rr = 8 * (i / 4) + 4 * g + (i % 4);
-                    const size_t grow4 = (size_t)(rt * 32 + rr) * 4;
                     float v;
                     if constexpr (MODE == 0) {
-                        float gg = acc0[j][i] + *(const float *)(ex + A.off[2] + grow4);
-                        float uu = acc1[j][i] + *(const float *)(ex + A.off[5] + grow4);
+                        float gg = acc0[j][i] + bias0[i];
+                        float uu = acc1[j][i] + bias1[i];
                         if (A.act_plain) {
                             v = gg / (1.0f + expf(-gg)) * uu;
                         } else {
@@ -415,17 +494,18 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
                             v = gg / (1.0f + expf(-A.alpha * gg)) * (uu + 1.0f);
                         }
                     } else {
-                        v = acc0[j][i] + *(const float *)(ex + A.off[8] + grow4);
+                        v = acc0[j][i] + bias0[i];
                     }
                     tl[m][rr] = v;   // [token][row]
                 }
                 __builtin_amdgcn_wave_barrier();
+#pragma unroll
                 for (int q = 0; q < 16; ++q) {
                     const int tok = 2 * q + g, p = p0 + 32 * j + tok;
                     if (p < T) {
                         const float v = tl[tok][m];
                         if constexpr (MODE == 0) A.hbuf[(size_t)(base + p) * A.F + rt * 32 + m] = v;
-                        else A.ye[(size_t)A.slot_of[base + p] * A.H + rt * 32 + m] = v;
+                        else A.ye[(size_t)dst[q] * A.H + rt * 32 + m] = v;
                     }
                 }
                 __builtin_amdgcn_wave_barrier();
