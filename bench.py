@@ -215,10 +215,11 @@ def run_gpu(args, shape):
     return ms, unique, kern, dom, extra
 
 
-def gemv_probe(ev, s, rows: int = 262144, cols: int = 2880, reps: int = 20) -> dict:
-    """The MXFP4 GEMV engine alone: y = W x over a 262144 x 2880 matrix
-    (424 MB of nibbles + f16 scales, larger than the 256 MB Infinity Cache),
-    timed with HIP events over `reps` launches."""
+def gemv_probe(ev, s, rows: int = 524288, cols: int = 2880, reps: int = 20) -> dict:
+    """The MXFP4 GEMV engine alone: y = W x over a 524288 x 2880 matrix
+    (849 MB of nibbles + f16 scales, over three times the 256 MB Infinity
+    Cache), timed with HIP events over `reps` back-to-back launches (so the
+    figure includes the few microseconds between launches)."""
     import midge_amd
     from midge_amd import DT_MXFP4, DevBuf, _lib, synth
     from midge_amd.kern import WT, matvec_dev
