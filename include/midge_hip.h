@@ -128,7 +128,11 @@ int mh_row(const mh_wt *t, int64_t r, float *out);
 /* y[b][rows] = W x[b][cols] for b < batch (device arrays, row-major, one
  * token per row). batch = 1 is wk_matvec on device memory; batch > 1 is the
  * reference's per-token loop of wk_matvec calls (engine/midge.c:586-590,
- * 613-618) done as one launch. */
+ * 613-618) done in one pass. For int8 (q8r) weights with batch >= 2 and cols
+ * a multiple of 64 (<= 65536), each weight byte is read once per 32 tokens
+ * on the int8 matrix cores, x written as three int8 digits under a power of
+ * two per token (exact int32 sums; x rounded to 2^-22 of its largest
+ * element; a token holding inf/nan gets the plain f32 sum). */
 int mh_matvec_dev(const mh_wt *t, const float *x, float *y, int batch);
 
 /* out[n][cols] = rows r0 .. r0+n-1 of W dequantized (device out). */
