@@ -23,12 +23,12 @@ constexpr int kMaxExperts = 1024;  // one wave holds 16 logits per lane
 // engine/midge.c:476-486 and 410-422 produce exactly this). Unfilled slots
 // get sel = `unfilled` (-1 for moe(), 0 for route_topk()) and value -1e30.
 // Weights as engine/midge.c:502-512. usage (may be NULL) += 1 per filled slot.
-__global__ void __launch_bounds__(256)
-k_topk(const float *__restrict__ rl, const float *__restrict__ bias, int n, int E, int k, int router_norm,
-       int unfilled, int32_t *__restrict__ sel, float *__restrict__ w, uint32_t *__restrict__ usage) {
-    const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+// The top-k of one token's logits rl[E] by one whole wave (every lane calls
+// it); lane 0 writes sel[k], w[k] and the usage counts.
+__device__ __forceinline__ void wave_topk_token(const float *rl, const float *__restrict__ bias, int E, int k,
+                                                int router_norm, int unfilled, int32_t *__restrict__ sel,
+                                                float *__restrict__ w, uint32_t *__restrict__ usage) {
     const int lane = threadIdx.x & 63;
-    if (t >= n) return;
     constexpr int PER = kMaxExperts / 64;
     float v[PER];
     bool taken[PER];
@@ -38,7 +38,7 @@ k_topk(const float *__restrict__ rl, const float *__restrict__ bias, int n, int 
         v[j] = -INFINITY;
         taken[j] = true;
         if (e < E) {
-            v[j] = bias ? rl[(size_t)t * E + e] + bias[e] : rl[(size_t)t * E + e];
+            v[j] = bias ? rl[e] + bias[e] : rl[e];
             taken[j] = false;
         }
     }
@@ -107,11 +107,20 @@ k_topk(const float *__restrict__ rl, const float *__restrict__ bias, int n, int 
             for (int i = 0; i < k; ++i) wt[i] = expf(val[i] - fmx) / fden;
         }
         for (int i = 0; i < k; ++i) {
-            sel[(size_t)t * k + i] = idx[i];
-            w[(size_t)t * k + i] = wt[i];
+            sel[i] = idx[i];
+            w[i] = wt[i];
             if (usage && idx[i] >= 0 && idx[i] < E && val[i] > -1e30f) atomicAdd(&usage[idx[i]], 1u);
         }
     }
+}
+
+__global__ void __launch_bounds__(256)
+k_topk(const float *__restrict__ rl, const float *__restrict__ bias, int n, int E, int k, int router_norm,
+       int unfilled, int32_t *__restrict__ sel, float *__restrict__ w, uint32_t *__restrict__ usage) {
+    const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (t >= n) return;   // wave-uniform
+    wave_topk_token(rl + (size_t)t * E, bias, E, k, router_norm, unfilled, sel + (size_t)t * k, w + (size_t)t * k,
+                    usage);
 }
 
 // ------------------------------------------------------- expert FFN

@@ -128,6 +128,36 @@ def test_moe_dev_batch(mh, batch):
     lay.release()
 
 
+@pytest.mark.parametrize("router_dt", [_lib.DT_Q8R, _lib.DT_F32])
+def test_moe_dev_batch16_128_experts(mh, router_dt):
+    # the per-layer decode path at batch 16 with 128 experts x 2880 router
+    # rows (the 120b router shape), int8 and f32 routers, against the oracle
+    shape = MoEShape(hidden=2880, ffn=256, n_experts=128, top_k=4, router_dt=router_dt)
+    say(f"moe_dev batch 16, 128 experts, router dt={router_dt}")
+    keys = Keys(21)
+    ex = synth.host_layer_experts(shape, keys, 0)
+    w, s, b, nw = synth.host_router(shape, keys, 0)
+    if router_dt == _lib.DT_F32:
+        w, s = (w.astype(np.float32) * s[:, None]).astype(np.float32), None
+    lay = MoELayer.host(shape, ex, w, s, b, nw)
+    _LIVE.append(lay)
+    L = po.layer_struct(shape, ex, w, s, b, nw)
+    X = synth.host_x(shape, keys, 16)
+    xd = DevBuf.from_array(X)
+    sd, wd = DevBuf(16 * shape.top_k * 4), DevBuf(16 * shape.top_k * 4)
+    moe_dev(lay, xd, 16, sd, wd)
+    x1, s1, w1 = (xd.download(np.float32, X.shape), sd.download(np.int32, (16, shape.top_k)),
+                  wd.download(np.float32, (16, shape.top_k)))
+    for d in (xd, sd, wd):
+        d.free()
+    for t in range(16):
+        xr, selr, wr = po.moe_decode(L, X[t])
+        assert (s1[t] == selr).all(), t
+        assert np.allclose(w1[t], wr, **WTOL), t
+        assert rel_l2(x1[t], xr) < TOL, t
+    lay.release()
+
+
 @pytest.mark.parametrize("name", ["tiny", "mid"])
 def test_prefill_vs_oracle(mh, name, prefill_path):
     shape = SHAPES[name]
