@@ -83,6 +83,14 @@ struct DevLayer {
 int validate_layer(const mh_moe_layer *L);
 int resolve_layer(const mh_moe_layer *L, DevLayer *out);
 
+// Assignments of sel[N] (N = tokens * k) grouped by expert (mh_prefill.hip):
+// offs[E + 1] into the list, the token (assignment / k) and the slot
+// (assignment) of each list position; in the S_LIST scratch, E <= 4096.
+struct ExpertLists {
+    int *offs, *list_tok, *slot_of;
+};
+int launch_expert_lists(const int32_t *sel, int N, int E, int k, ExpertLists *out, hipStream_t s);
+
 // Expert-major prefill with scaled MFMA (mh_prefill.hip): the routed
 // experts of n tokens into ye[n * k][hidden] (slot order); the caller adds
 // them to x with the prefill combine.

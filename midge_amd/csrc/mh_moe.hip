@@ -171,13 +171,14 @@ k_expert_gu(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restri
     float xr[CE];
     load_x<DT>(xb + (size_t)(a / A.k) * A.hidden, C, ns, xr);
     const mh_rsrc rx = gemv_rsrc(base, (uint32_t)A.stride);   // stride < 4 GiB: checked at launch
-    const uint32_t od[2] = {(uint32_t)A.off[0], (uint32_t)A.off[3]}, os[2] = {(uint32_t)A.off[1], (uint32_t)A.off[4]};
+    const uint32_t od0 = (uint32_t)A.off[0], od1 = (uint32_t)A.off[3], os0 = (uint32_t)A.off[1],
+                   os1 = (uint32_t)A.off[4];
     block_gemv<DT>(
         rx, rx,
         [&](int f) {
             const int m = f & 1;
             const uint32_t r = (uint32_t)(r0 + (f >> 1));
-            return RowOff{(m ? od[1] : od[0]) + mul24(r, rowbytes), (m ? os[1] : os[0]) + mul24(r, srow)};
+            return RowOff{(m ? od1 : od0) + mul24(r, rowbytes), (m ? os1 : os0) + mul24(r, srow)};
         },
         2 * nr, C, ns, xr, red, res);
     const float *bg = (const float *)(base + A.off[2]);

@@ -520,6 +520,20 @@ unsigned *g_scale_err_dev = nullptr;
 
 }  // namespace
 
+// Assignments grouped by expert (offsets[E + 1], token and slot of each list
+// position) in the S_LIST scratch; E <= 4096.
+int launch_expert_lists(const int32_t *sel, int N, int E, int k, ExpertLists *out, hipStream_t s) {
+    if (E > kPlistMaxE) return fail(MH_E_UNSUPPORTED, "expert lists: %d experts > %d", E, kPlistMaxE);
+    void *pl;
+    MH_TRY(scratch(S_LIST, sizeof(int) * ((size_t)E + 1 + 3 * (size_t)N), &pl));
+    int *offs = (int *)pl, *rank = offs + E + 1;
+    out->offs = offs;
+    out->list_tok = rank + N;
+    out->slot_of = rank + 2 * (size_t)N;
+    MH_LAUNCH("plist", k_plist_one, dim3(1), dim3(1024), 0, s, sel, N, E, k, rank, offs, out->list_tok, out->slot_of);
+    return hip_check(hipGetLastError(), "expert lists launch");
+}
+
 // True when the scaled-MFMA path handles this layer (MXFP4 experts, shapes
 // that tile by 64 along K and 32 along rows, whose scales fit the GEMM's LDS).
 bool prefill_mfma_ok(const DevLayer &L) {
@@ -551,10 +565,9 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
         MH_HIP(hipHostGetDevicePointer((void **)&g_scale_err_dev, g_scale_err, 0));
         watch_async_error(g_scale_err, "prefill: an MXFP4 scale is not a positive power of two (e8m0 cannot hold it)");
     }
-    // lists: offs[E + 1], rank[N], list_tok[N], slot_of[N]
-    void *pl;
-    MH_TRY(scratch(S_LIST, sizeof(int) * ((size_t)E + 1 + 3 * (size_t)N), &pl));
-    int *offs = (int *)pl, *rank = offs + E + 1, *list_tok = rank + N, *slot_of = list_tok + N;
+    ExpertLists lists;
+    MH_TRY(launch_expert_lists(sel, N, E, k, &lists, s));
+    const int *offs = lists.offs, *list_tok = lists.list_tok, *slot_of = lists.slot_of;
     // quantized activations: the larger of x (n rows of H) and h (N rows of F)
     const size_t qx = (size_t)kTerms * n * H, qh = (size_t)kTerms * N * F;
     const size_t qbytes = std::max(qx + (size_t)kTerms * n * bscale_stride(H), qh + (size_t)kTerms * N * bscale_stride(F));
@@ -564,7 +577,6 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
     uint8_t *q = (uint8_t *)pq;
     float *hbuf = (float *)ph;
 
-    MH_LAUNCH("plist", k_plist_one, dim3(1), dim3(1024), 0, s, sel, N, E, k, rank, offs, list_tok, slot_of);
     // ye rows of unroutable slots are not written: the combine skips them
 
     GemmArgs A;
