@@ -24,12 +24,13 @@ constexpr int kMaxExperts = 1024;  // one wave holds 16 logits per lane
 // get sel = `unfilled` (-1 for moe(), 0 for route_topk()) and value -1e30.
 // Weights as engine/midge.c:502-512. usage (may be NULL) += 1 per filled slot.
 // The top-k of one token's logits rl[E] by one whole wave (every lane calls
-// it); lane 0 writes sel[k], w[k] and the usage counts.
+// it); lane 0 writes sel[k], w[k] and the usage counts. PER logits per lane
+// (E <= 64 PER).
+template <int PER>
 __device__ __forceinline__ void wave_topk_token(const float *rl, const float *__restrict__ bias, int E, int k,
                                                 int router_norm, int unfilled, int32_t *__restrict__ sel,
                                                 float *__restrict__ w, uint32_t *__restrict__ usage) {
     const int lane = threadIdx.x & 63;
-    constexpr int PER = kMaxExperts / 64;
     float v[PER];
     bool taken[PER];
 #pragma unroll
@@ -114,13 +115,14 @@ __device__ __forceinline__ void wave_topk_token(const float *rl, const float *__
     }
 }
 
+template <int PER>
 __global__ void __launch_bounds__(256)
 k_topk(const float *__restrict__ rl, const float *__restrict__ bias, int n, int E, int k, int router_norm,
        int unfilled, int32_t *__restrict__ sel, float *__restrict__ w, uint32_t *__restrict__ usage) {
     const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (t >= n) return;   // wave-uniform
-    wave_topk_token(rl + (size_t)t * E, bias, E, k, router_norm, unfilled, sel + (size_t)t * k, w + (size_t)t * k,
-                    usage);
+    wave_topk_token<PER>(rl + (size_t)t * E, bias, E, k, router_norm, unfilled, sel + (size_t)t * k,
+                         w + (size_t)t * k, usage);
 }
 
 // ------------------------------------------------------- expert FFN
@@ -347,8 +349,15 @@ int launch_experts(const DevLayer &L, int A, const int32_t *sel, const float *xb
 int launch_topk(const float *rl, const float *bias, int n, int E, int k, int router_norm, int unfilled,
                 int32_t *sel, float *w, uint32_t *usage, hipStream_t s) {
     const int per_block = 4;
-    MH_LAUNCH("topk", k_topk, dim3((unsigned)((n + per_block - 1) / per_block)), dim3(64 * per_block), 0, s, rl,
-                       bias, n, E, k, router_norm, unfilled, sel, w, usage);
+    const dim3 grid((unsigned)((n + per_block - 1) / per_block)), block(64 * per_block);
+    // logits per lane: the smallest instantiation that holds E (E <= kMaxExperts)
+    if (E <= 128)
+        MH_LAUNCH("topk", k_topk<2>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel, w, usage);
+    else if (E <= 256)
+        MH_LAUNCH("topk", k_topk<4>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel, w, usage);
+    else
+        MH_LAUNCH("topk", k_topk<kMaxExperts / 64>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel,
+                  w, usage);
     return hip_check(hipGetLastError(), "topk launch");
 }
 
