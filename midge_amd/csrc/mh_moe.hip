@@ -115,14 +115,39 @@ __device__ __forceinline__ void wave_topk_token(const float *rl, const float *__
     }
 }
 
+// Assignments a block can sort (16 tokens of up to kMaxTopK slots).
+constexpr int kMaxOrder = 16 * kMaxTopK;
+
+// One wave per token. With `order` (one block holding all n tokens, n k <=
+// kMaxOrder), the block then sorts the assignments by expert id, stably,
+// unroutable slots last: order[r] = assignment a, order[n k + r] = sel[a].
+// The expert kernels walk assignments in that order, so the assignments of
+// one expert run side by side and share its weight lines in the caches.
 template <int PER>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(1024)
 k_topk(const float *__restrict__ rl, const float *__restrict__ bias, int n, int E, int k, int router_norm,
-       int unfilled, int32_t *__restrict__ sel, float *__restrict__ w, uint32_t *__restrict__ usage) {
+       int unfilled, int32_t *__restrict__ sel, float *__restrict__ w, uint32_t *__restrict__ usage,
+       int32_t *__restrict__ order) {
     const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (t >= n) return;   // wave-uniform
-    wave_topk_token<PER>(rl + (size_t)t * E, bias, E, k, router_norm, unfilled, sel + (size_t)t * k,
-                         w + (size_t)t * k, usage);
+    if (t < n)   // wave-uniform
+        wave_topk_token<PER>(rl + (size_t)t * E, bias, E, k, router_norm, unfilled, sel + (size_t)t * k,
+                             w + (size_t)t * k, usage);
+    if (order == nullptr) return;   // grid-uniform
+    __shared__ int skey[kMaxOrder];
+    const int N = n * k;
+    __syncthreads();   // every wave's sel stores are visible to the block
+    for (int i = threadIdx.x; i < N; i += blockDim.x) {
+        const int e = sel[i];
+        skey[i] = (e >= 0 && e < E ? e : E) * N + i;   // distinct keys
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < N; i += blockDim.x) {
+        const int ki = skey[i];
+        int r = 0;
+        for (int j = 0; j < N; ++j) r += skey[j] < ki;
+        order[r] = i;
+        order[N + r] = ki / N < E ? ki / N : -1;
+    }
 }
 
 // ------------------------------------------------------- expert FFN
@@ -146,17 +171,29 @@ __device__ __forceinline__ float act_fn(float g, float u, float alpha, float lim
     return a * (u + 1.0f);
 }
 
-// Gate and up rows of the expert routed for assignment a = blockIdx.y
-// (token a / k), rows [blockIdx.x * rpb, +rpb): h[a][r] = act(g + bg, u + bu).
-// Flat row f interleaves the two matrices: f = 2i (gate row i), 2i+1 (up row i).
+// The assignment of grid row y and its expert: y itself, or the y-th of the
+// expert-sorted order (order[y], order[A + y] for A assignments).
+struct Assignment {
+    int a, e;
+};
+__device__ __forceinline__ Assignment assignment_of(const int32_t *__restrict__ sel,
+                                                    const int32_t *__restrict__ order) {
+    const int y = blockIdx.y;
+    if (order) return {order[y], order[gridDim.y + y]};
+    return {y, sel[y]};
+}
+
+// Gate and up rows of the expert routed for assignment a (token a / k),
+// rows [blockIdx.x * rpb, +rpb): h[a][r] = act(g + bg, u + bu). Flat row f
+// interleaves the two matrices: f = 2i (gate row i), 2i+1 (up row i).
 template <int DT>
 __global__ void __launch_bounds__(kGemvThreads)
-k_expert_gu(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restrict__ xb,
-            float *__restrict__ h, int ns, int rpb) {
+k_expert_gu(ExpertArgs A, const int32_t *__restrict__ sel, const int32_t *__restrict__ order,
+            const float *__restrict__ xb, float *__restrict__ h, int ns, int rpb) {
     constexpr int CE = gemv_chunk<DT>::E;
     extern __shared__ float lds[];
-    const int a = blockIdx.y;
-    const int e = sel[a];
+    const Assignment as = assignment_of(sel, order);
+    const int a = as.a, e = as.e;
     const int r0 = blockIdx.x * rpb;
     const int nr = (int)min((int64_t)rpb, A.ffn - r0);
     float *hout = h + (size_t)a * A.ffn;
@@ -199,16 +236,15 @@ k_expert_gu(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restri
     }
 }
 
-// Down rows of the expert for assignment a = blockIdx.y:
-// ye[a][r] = Wd[r] . h[a] + bd[r].
+// Down rows of the expert for assignment a: ye[a][r] = Wd[r] . h[a] + bd[r].
 template <int DT>
 __global__ void __launch_bounds__(kGemvThreads)
-k_expert_down(ExpertArgs A, const int32_t *__restrict__ sel, const float *__restrict__ h,
-              float *__restrict__ ye, int ns, int rpb) {
+k_expert_down(ExpertArgs A, const int32_t *__restrict__ sel, const int32_t *__restrict__ order,
+              const float *__restrict__ h, float *__restrict__ ye, int ns, int rpb) {
     constexpr int CE = gemv_chunk<DT>::E;
     extern __shared__ float lds[];
-    const int a = blockIdx.y;
-    const int e = sel[a];
+    const Assignment as = assignment_of(sel, order);
+    const int a = as.a, e = as.e;
     const int r0 = blockIdx.x * rpb;
     const int nr = (int)min((int64_t)rpb, A.hidden - r0);
     float *yout = ye + (size_t)a * A.hidden;
@@ -288,8 +324,8 @@ k_combine_prefill(float *__restrict__ x, const float *__restrict__ ye, const int
 }
 
 template <int DT>
-int launch_experts_t(const DevLayer &L, int A, const int32_t *sel, const float *xb, float *h, float *ye,
-                     hipStream_t s) {
+int launch_experts_t(const DevLayer &L, int A, const int32_t *sel, const int32_t *order, const float *xb, float *h,
+                     float *ye, hipStream_t s) {
     constexpr int CE = gemv_chunk<DT>::E;
     ExpertArgs ea;
     ea.experts = L.experts;
@@ -314,8 +350,8 @@ int launch_experts_t(const DevLayer &L, int A, const int32_t *sel, const float *
         if (rpb > 2048) rpb = 2048;
         const int64_t nblk = (L.ffn + rpb - 1) / rpb;
         const size_t lds = ((size_t)2 * rpb + gemv_lds_floats(ns, C)) * sizeof(float);
-        MH_LAUNCH("expert_gu", k_expert_gu<DT>, dim3((unsigned)nblk, (unsigned)A), dim3(nt), lds, s, ea, sel, xb, h,
-                           ns, (int)rpb);
+        MH_LAUNCH("expert_gu", k_expert_gu<DT>, dim3((unsigned)nblk, (unsigned)A), dim3(nt), lds, s, ea, sel, order, xb,
+                           h, ns, (int)rpb);
         MH_TRY(hip_check(hipGetLastError(), "expert gate/up launch"));
     }
     {   // down: hidden rows per assignment
@@ -328,36 +364,41 @@ int launch_experts_t(const DevLayer &L, int A, const int32_t *sel, const float *
         if (rpb > 4096) rpb = 4096;
         const int64_t nblk = (L.hidden + rpb - 1) / rpb;
         const size_t lds = ((size_t)rpb + gemv_lds_floats(ns, C)) * sizeof(float);
-        MH_LAUNCH("expert_down", k_expert_down<DT>, dim3((unsigned)nblk, (unsigned)A), dim3(nt), lds, s, ea, sel, h, ye,
-                           ns, (int)rpb);
+        MH_LAUNCH("expert_down", k_expert_down<DT>, dim3((unsigned)nblk, (unsigned)A), dim3(nt), lds, s, ea, sel, order, h,
+                           ye, ns, (int)rpb);
         MH_TRY(hip_check(hipGetLastError(), "expert down launch"));
     }
     return MH_OK;
 }
 
-int launch_experts(const DevLayer &L, int A, const int32_t *sel, const float *xb, float *h, float *ye,
-                   hipStream_t s) {
+// order: null (grid row y = assignment y) or the expert-sorted order of k_topk.
+int launch_experts(const DevLayer &L, int A, const int32_t *sel, const int32_t *order, const float *xb, float *h,
+                   float *ye, hipStream_t s) {
     switch (L.expert_dt) {
-    case MH_DT_F32: return launch_experts_t<MH_DT_F32>(L, A, sel, xb, h, ye, s);
-    case MH_DT_Q8R: return launch_experts_t<MH_DT_Q8R>(L, A, sel, xb, h, ye, s);
-    case MH_DT_Q4G32: return launch_experts_t<MH_DT_Q4G32>(L, A, sel, xb, h, ye, s);
-    case MH_DT_MXFP4: return launch_experts_t<MH_DT_MXFP4>(L, A, sel, xb, h, ye, s);
+    case MH_DT_F32: return launch_experts_t<MH_DT_F32>(L, A, sel, order, xb, h, ye, s);
+    case MH_DT_Q8R: return launch_experts_t<MH_DT_Q8R>(L, A, sel, order, xb, h, ye, s);
+    case MH_DT_Q4G32: return launch_experts_t<MH_DT_Q4G32>(L, A, sel, order, xb, h, ye, s);
+    case MH_DT_MXFP4: return launch_experts_t<MH_DT_MXFP4>(L, A, sel, order, xb, h, ye, s);
     }
     return fail(MH_E_DTYPE, "unknown expert dtype %d", L.expert_dt);
 }
 
+// order: null, or [2 n k] for the expert-sorted assignment order (n <= 16).
 int launch_topk(const float *rl, const float *bias, int n, int E, int k, int router_norm, int unfilled,
-                int32_t *sel, float *w, uint32_t *usage, hipStream_t s) {
-    const int per_block = 4;
+                int32_t *sel, float *w, uint32_t *usage, int32_t *order, hipStream_t s) {
+    if (order && (n > 16 || n * k > kMaxOrder)) return fail(MH_E_ARG, "topk: %d x %d assignments to order", n, k);
+    const int per_block = order ? n : 4;
     const dim3 grid((unsigned)((n + per_block - 1) / per_block)), block(64 * per_block);
     // logits per lane: the smallest instantiation that holds E (E <= kMaxExperts)
     if (E <= 128)
-        MH_LAUNCH("topk", k_topk<2>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel, w, usage);
+        MH_LAUNCH("topk", k_topk<2>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel, w, usage,
+                  order);
     else if (E <= 256)
-        MH_LAUNCH("topk", k_topk<4>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel, w, usage);
+        MH_LAUNCH("topk", k_topk<4>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel, w, usage,
+                  order);
     else
         MH_LAUNCH("topk", k_topk<kMaxExperts / 64>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel,
-                  w, usage);
+                  w, usage, order);
     return hip_check(hipGetLastError(), "topk launch");
 }
 
@@ -366,6 +407,7 @@ struct LayerBufs {
     float *xb, *rl, *h, *ye;
     int32_t *sel;
     float *w;
+    int32_t *order;   // [2 n k] expert-sorted assignments (n <= 16), else null
 };
 
 int layer_bufs(const DevLayer &L, int n, LayerBufs *b) {
@@ -382,20 +424,27 @@ int layer_bufs(const DevLayer &L, int n, LayerBufs *b) {
     b->sel = (int32_t *)p;
     MH_TRY(scratch(S_W, (uint64_t)n * L.top_k * 4, &p));
     b->w = (float *)p;
+    b->order = nullptr;
+    if (n <= 16) {
+        MH_TRY(scratch(S_ORD, (uint64_t)2 * n * L.top_k * 4, &p));
+        b->order = (int32_t *)p;
+    }
     return MH_OK;
 }
 
-// Router (rmsnorm, logits, top-k) for n tokens into b->xb / b->sel / b->w.
+// Router (rmsnorm, logits, top-k) for n tokens into b->xb / b->sel / b->w
+// (and the expert-sorted order into `order` when it is not null).
 int run_router(const DevLayer &L, const float *x, int n, int unfilled, const LayerBufs &b, uint32_t *usage,
-               hipStream_t s) {
+               int32_t *order, hipStream_t s) {
     MH_TRY(launch_rmsnorm(x, L.mlp_norm, b.xb, L.hidden, L.norm_eps, n, s));
     MH_TRY(launch_gemv(L.router, b.xb, b.rl, n, s));
-    return launch_topk(b.rl, L.router_b, n, L.n_experts, L.top_k, L.router_norm, unfilled, b.sel, b.w, usage, s);
+    return launch_topk(b.rl, L.router_b, n, L.n_experts, L.top_k, L.router_norm, unfilled, b.sel, b.w, usage, order,
+                       s);
 }
 
 int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uint32_t *usage, hipStream_t s) {
-    MH_TRY(run_router(L, x, n, -1, b, usage, s));
-    MH_TRY(launch_experts(L, n * L.top_k, b.sel, b.xb, b.h, b.ye, s));
+    MH_TRY(run_router(L, x, n, -1, b, usage, b.order, s));
+    MH_TRY(launch_experts(L, n * L.top_k, b.sel, b.order, b.xb, b.h, b.ye, s));
     MH_LAUNCH("combine_decode", k_combine_decode, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s, x,
                        b.ye, b.w, L.hidden, L.top_k);
     return hip_check(hipGetLastError(), "combine launch");
@@ -404,7 +453,7 @@ int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uin
 int run_expert_major(const DevLayer &L, int n, const float *xb, const int32_t *sel, const float *w, float *x,
                      const LayerBufs &b, hipStream_t s) {
     if (prefill_mfma_ok(L)) MH_TRY(run_expert_major_mfma(L, n, xb, sel, b.ye, s));
-    else MH_TRY(launch_experts(L, n * L.top_k, sel, xb, b.h, b.ye, s));
+    else MH_TRY(launch_experts(L, n * L.top_k, sel, nullptr, xb, b.h, b.ye, s));
     MH_LAUNCH("combine_prefill", k_combine_prefill, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s,
                        x, b.ye, sel, w, L.hidden, L.top_k, L.n_experts);
     return hip_check(hipGetLastError(), "prefill combine launch");
@@ -544,7 +593,7 @@ int mh_topk_dev(const float *logits, int n, int E, int k, int router_norm, int32
     MH_TRY(resolve_dev(logits, (uint64_t)n * E * 4, "mh_topk_dev logits"));
     MH_TRY(resolve_dev(sel, (uint64_t)n * k * 4, "mh_topk_dev sel"));
     MH_TRY(resolve_dev(w, (uint64_t)n * k * 4, "mh_topk_dev w"));
-    return launch_topk(logits, nullptr, n, E, k, router_norm ? 1 : 0, 0, sel, w, nullptr, stream());
+    return launch_topk(logits, nullptr, n, E, k, router_norm ? 1 : 0, 0, sel, w, nullptr, nullptr, stream());
 }
 
 int mh_expert_major_dev(const mh_moe_layer *Lh, int n, const float *xb, const int32_t *sel, const float *w,
@@ -577,7 +626,7 @@ int mh_moe_prefill_dev(const mh_moe_layer *Lh, int n, float *x, int32_t *sel, fl
     LayerBufs b;
     MH_TRY(layer_bufs(L, n, &b));
     hipStream_t s = stream();
-    MH_TRY(run_router(L, x, n, 0, b, nullptr, s));
+    MH_TRY(run_router(L, x, n, 0, b, nullptr, nullptr, s));
     MH_TRY(run_expert_major(L, n, b.xb, b.sel, b.w, x, b, s));
     if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, (size_t)n * L.top_k * 4, hipMemcpyDeviceToDevice, s));
     if (w) MH_HIP(hipMemcpyAsync(w, b.w, (size_t)n * L.top_k * 4, hipMemcpyDeviceToDevice, s));
@@ -599,7 +648,7 @@ int mh_moe_prefill(const mh_moe_layer *Lh, int n, float *x, int32_t *sel, float 
     hipStream_t s = stream();
     const size_t xbytes = (size_t)n * L.hidden * 4, kbytes = (size_t)n * L.top_k * 4;
     MH_HIP(hipMemcpyAsync(dx, x, xbytes, hipMemcpyHostToDevice, s));
-    MH_TRY(run_router(L, (float *)dx, n, 0, b, nullptr, s));
+    MH_TRY(run_router(L, (float *)dx, n, 0, b, nullptr, nullptr, s));
     MH_TRY(run_expert_major(L, n, b.xb, b.sel, b.w, (float *)dx, b, s));
     MH_HIP(hipMemcpyAsync(x, dx, xbytes, hipMemcpyDeviceToHost, s));
     if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, kbytes, hipMemcpyDeviceToHost, s));
