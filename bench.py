@@ -219,11 +219,12 @@ def gemv_probe(ev, s, rows: int = 262144, cols: int = 2880, reps: int = 10, sust
     """The MXFP4 GEMV engine alone: y = W x over a 262144 x 2880 matrix
     (424 MB of nibbles + f16 scales, past the 256 MB Infinity Cache).
 
-    `avg_us` is the mean of `reps` back-to-back launches, each bracketed by
-    its own HIP events. A longer back-to-back run (`sustain` launches, ~5 ms
-    of streaming) is reported beside it: under sustained streaming at this
-    rate the device slows down after ~2 ms (76 -> 100 us per launch measured),
-    so its first and last five launches are given separately."""
+    `avg_us` is per launch over `reps` back-to-back launches between one
+    pair of HIP events (the short gaps between launches included). A longer
+    back-to-back run (`sustain` launches, ~5 ms of streaming) is reported
+    beside it, timed in groups of 5: under sustained streaming at this rate
+    the device slows down after ~2 ms (72 -> 87 us per launch in a kernel
+    trace), so its first and last groups are given separately."""
     import midge_amd
     from midge_amd import DT_MXFP4, DevBuf, _lib, synth
     from midge_amd.kern import WT, matvec_dev
@@ -237,26 +238,27 @@ def gemv_probe(ev, s, rows: int = 262144, cols: int = 2880, reps: int = 10, sust
         matvec_dev(t, x, y)
     midge_amd.sync()
 
-    def launches(n: int) -> list:
-        evs = [ev.event() for _ in range(n + 1)]
+    def launches(n: int, group: int) -> list:
+        """Per-launch us of each group of `group` back-to-back launches."""
+        evs = [ev.event() for _ in range(n // group + 1)]
         ev.record(evs[0], s)
-        for i in range(n):
-            matvec_dev(t, x, y)
+        for i in range(n // group):
+            for _ in range(group):
+                matvec_dev(t, x, y)
             ev.record(evs[i + 1], s)
         midge_amd.sync()
-        return [1e3 * ev.elapsed_ms(evs[i], evs[i + 1]) for i in range(n)]
+        return [1e3 * ev.elapsed_ms(evs[i], evs[i + 1]) / group for i in range(n // group)]
 
-    us = launches(reps)
+    avg = launches(reps, reps)[0]
     time.sleep(0.2)
-    long = launches(sustain)
+    long = launches(sustain, 5)
     nbytes = rows * cols // 2 + rows * cols // 32 * 2 + cols * 4 + rows * 4
     for d in (data, sc, x, y):
         d.free()
-    avg = sum(us) / len(us)
     gbs = nbytes / (avg * 1e-6) / 1e9
-    first, last = sum(long[:5]) / 5, sum(long[-5:]) / 5
+    first, last = long[0], long[-1]
     return {"kernel": "gemv (MXFP4)", "shape": [rows, cols], "bytes": nbytes, "launches": reps, "avg_us": avg,
-            "min_us": min(us), "GBps": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS,
+            "GBps": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS,
             "sustained": {"launches": sustain, "first5_us": first, "last5_us": last,
                           "first5_frac_of_peak": nbytes / (first * 1e-6) / 1e9 / HBM_PEAK_GBS,
                           "last5_frac_of_peak": nbytes / (last * 1e-6) / 1e9 / HBM_PEAK_GBS}}

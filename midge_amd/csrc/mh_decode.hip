@@ -993,9 +993,18 @@ __global__ void k_scan_scales(const uint8_t *experts, uint64_t stride, uint64_t 
 template <int RDT, int XDT, bool MF>
 int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
     auto k = k_decode_step<RDT, XDT, MF>;
-    MH_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    int per_cu = 0;
-    MH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, lds));
+    // the LDS attribute and the occupancy query once per device and
+    // instantiation (both cost host time comparable to a small step)
+    static int ready_dev = -1, per_cu = 0;
+    static size_t ready_lds = 0;
+    int dev = 0;
+    MH_HIP(hipGetDevice(&dev));
+    if (dev != ready_dev || lds != ready_lds) {
+        MH_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        MH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, lds));
+        ready_dev = dev;
+        ready_lds = lds;
+    }
     if (per_cu < 1) return fail(MH_E_UNSUPPORTED, "decode step: a %d-thread block with %zu B LDS does not fit a CU", kThreads, lds);
     StepArgs a = A;
     void *args[] = {&a};

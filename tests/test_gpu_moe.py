@@ -158,6 +158,37 @@ def test_moe_dev_batch16_128_experts(mh, router_dt):
     lay.release()
 
 
+@pytest.mark.parametrize("expert_dt", [_lib.DT_MXFP4, _lib.DT_Q4G32, _lib.DT_Q8R])
+@pytest.mark.parametrize("n_experts", [4, 32])
+def test_moe_dev_expert_order_bit_exact(mh, expert_dt, n_experts):
+    # Up to 16 tokens, the top-k kernel sorts the assignments by expert and
+    # the expert kernels walk them in that order; at 17 tokens they walk them
+    # in assignment order. The first 16 tokens of a 17-token call must equal
+    # a 16-token call bit for bit, and the oracle. 4 experts x top-4: every
+    # token routes to every expert.
+    shape = MoEShape(hidden=512, ffn=256, n_experts=n_experts, top_k=4, expert_dt=expert_dt)
+    say(f"moe_dev expert order, dt={expert_dt}, {n_experts} experts")
+    keys, arrays, lay, L = build(shape, 33)
+    X = synth.host_x(shape, keys, 17)
+    outs = []
+    for n in (16, 17):
+        xd = DevBuf.from_array(X[:n])
+        sd, wd = DevBuf(n * shape.top_k * 4), DevBuf(n * shape.top_k * 4)
+        moe_dev(lay, xd, n, sd, wd)
+        outs.append((xd.download(np.float32, (n, shape.hidden)), sd.download(np.int32, (n, shape.top_k)),
+                     wd.download(np.float32, (n, shape.top_k))))
+        for d in (xd, sd, wd):
+            d.free()
+    (x16, s16, w16), (x17, s17, w17) = outs
+    assert (s16 == s17[:16]).all()
+    assert (w16 == w17[:16]).all()
+    assert (x16 == x17[:16]).all()
+    for t in range(0, 16, 5):
+        xr, selr, wr = po.moe_decode(L, X[t])
+        assert (s16[t] == selr).all(), t
+        assert rel_l2(x16[t], xr) < TOL, t
+
+
 @pytest.mark.parametrize("name", ["tiny", "mid"])
 def test_prefill_vs_oracle(mh, name, prefill_path):
     shape = SHAPES[name]
