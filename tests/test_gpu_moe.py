@@ -208,23 +208,28 @@ def test_prefill_vs_oracle(mh, name, prefill_path):
     lay.release()
 
 
-def test_topk_dev_ties_and_edges(mh):
-    say("topk_dev ties")
-    rng = np.random.default_rng(3)
-    n, E, k = 64, 128, 4
+# expert counts on both sides of each ranking instantiation (2, 4 and 16
+# logits per lane: E <= 128, <= 256, <= 1024) and the largest top-k (16)
+@pytest.mark.parametrize("E,k,router_norm", [(8, 2, 1), (128, 4, 1), (129, 4, 0), (200, 16, 1), (256, 4, 1),
+                                             (257, 4, 1), (640, 16, 0), (1024, 4, 1)])
+def test_topk_dev_ties_and_edges(mh, E, k, router_norm):
+    say(f"topk_dev ties E={E} k={k} norm={router_norm}")
+    rng = np.random.default_rng(3 + E)
+    n = 64
     logits = rng.standard_normal((n, E)).astype(np.float32)
     logits[::3] = np.round(logits[::3] * 2) / 2          # many exact ties
     logits[5, :] = 0.25                                   # all equal
-    logits[6, 10:] = -np.inf                              # few eligible
+    logits[6, 3:] = -np.inf                               # fewer eligible than k: unfilled slots
+    logits[7, E - 1] = 9.0                                # the winner in the last lane's last slot
     ld = DevBuf.from_array(logits)
     sd, wd = DevBuf(n * k * 4), DevBuf(n * k * 4)
-    topk_dev(ld, n, E, k, 1, sd, wd)
+    topk_dev(ld, n, E, k, router_norm, sd, wd)
     sel = sd.download(np.int32, (n, k))
     w = wd.download(np.float32, (n, k))
     for t in range(n):
         s, v = po.topk(logits[t], k, decode=False)
         assert (sel[t] == s).all(), (t, sel[t], s)
-        assert np.allclose(w[t], po.router_weights(logits[t], v, 1), rtol=1e-5, atol=1e-9)
+        assert np.allclose(w[t], po.router_weights(logits[t], v, router_norm), rtol=1e-5, atol=1e-9)
     for d in (ld, sd, wd):
         d.free()
 
