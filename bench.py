@@ -209,6 +209,8 @@ def run_gpu(args, shape):
         extra["configs"] = config_probes(ev, s, args.seed)
     if not args.no_prefill:
         extra["prefill"] = prefill_probe(ev, s, args.seed)
+    if not args.no_configs:
+        extra["lm_head_sample"] = lm_head_sample_probe(ev, s)
     for b in bufs:
         b.free()
     st.destroy()
@@ -262,6 +264,44 @@ def gemv_probe(ev, s, rows: int = 262144, cols: int = 2880, reps: int = 10, sust
             "sustained": {"launches": sustain, "first5_us": first, "last5_us": last,
                           "first5_frac_of_peak": nbytes / (first * 1e-6) / 1e9 / HBM_PEAK_GBS,
                           "last5_frac_of_peak": nbytes / (last * 1e-6) / 1e9 / HBM_PEAK_GBS}}
+
+
+def lm_head_sample_probe(ev, s, reps: int = 20) -> dict:
+    """The token after the last layer on the device (the next component of
+    the decode path): final rmsnorm, the int8 lm_head GEMV (201088 x 2880)
+    and sample() over the 201088 logits, greedy and temperature 1 / top-p
+    0.9, HIP-event timed per token over `reps` back-to-back tokens."""
+    import midge_amd
+    from midge_amd import DT_Q8R, DevBuf, _lib, synth
+    from midge_amd.kern import WT, matvec_dev, rmsnorm_dev
+    from midge_amd.moe import sample_dev
+    V, H = 201088, 2880
+    w, sc = DevBuf(V * H), DevBuf(V * 4)
+    _lib.call("mh_synth_i8_dev", w.ptr, V * H, 911)
+    _lib.call("mh_synth_uniform_dev", sc.ptr, V, 912, 1e-3, float(synth.uniform_c(1e-3, 1e-2)))
+    nw, x, xb, lg, out = DevBuf(H * 4), DevBuf(H * 4), DevBuf(H * 4), DevBuf(V * 4), DevBuf(4)
+    _lib.call("mh_synth_uniform_dev", nw.ptr, H, 913, 0.5, float(synth.uniform_c(0.5, 1.5)))
+    _lib.call("mh_synth_normal_dev", x.ptr, H, 914, float(synth.normal_c(1.0)))
+    t = WT(DT_Q8R, V, H, w.ptr, sc.ptr)
+    res = {"workload": "final rmsnorm + int8 lm_head 201088x2880 + sample(), one token", "vocab": V}
+    for name, temp, topp in (("greedy", 0.0, 1.0), ("temp1_topp0.9", 1.0, 0.9)):
+        def token(i):
+            rmsnorm_dev(x, nw, xb, H, 1e-5)
+            matvec_dev(t, xb, lg)
+            sample_dev(lg, V, temp, topp, (i * 0.618034) % 1.0, out)
+        for i in range(3):
+            token(i)
+        midge_amd.sync()
+        a, b = ev.event(), ev.event()
+        ev.record(a, s)
+        for i in range(reps):
+            token(i)
+        ev.record(b, s)
+        res[name + "_us"] = 1e3 * ev.elapsed_ms(a, b) / reps
+    midge_amd.sync()
+    for d in (w, sc, nw, x, xb, lg, out):
+        d.free()
+    return res
 
 
 def reference_bench(ev, s, seconds: float = 1.0) -> dict:

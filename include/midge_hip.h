@@ -141,6 +141,16 @@ int mh_dequant_dev(const mh_wt *t, int64_t r0, int64_t n, float *out);
 /* out[b] = rmsnorm(x[b]) * w for b < batch, length n each (engine/mkern.h:238-243). */
 int mh_rmsnorm_dev(const float *x, const float *w, float *out, int64_t n, float eps, int batch);
 
+/* sample() (engine/midge.c:654-679) on device logits[V]: the next token into
+ * device out[0]. temp <= 0 gives the first maximum; otherwise the
+ * temperature softmax, the smallest set of most probable tokens whose
+ * probability reaches topp, and the token where their running sum reaches
+ * u * (their sum). u is the caller's uniform draw in [0, 1), drawn where the
+ * reference draws rng_f() (engine/midge.c:641-646), i.e. only when temp > 0.
+ * Equal probabilities are ordered by token id (the reference's sort order
+ * for equal keys under glibc's qsort). */
+int mh_sample_dev(const float *logits, int64_t V, float temp, float topp, float u, int32_t *out);
+
 /* ------------------------------------------------------- layer level */
 
 /* Decode MoE layer for one token, in place on host x[hidden]: rmsnorm,

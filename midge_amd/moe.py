@@ -117,6 +117,12 @@ def moe_prefill_dev(layer: MoELayer, x, n: int, sel=None, w=None) -> None:
     _lib.call("mh_moe_prefill_dev", C.byref(c), int(n), int(x), int(sel or 0), int(w or 0))
 
 
+def sample_dev(logits, vocab: int, temp: float, topp: float, u: float, out) -> None:
+    """sample() on device logits[vocab] into device out[0] (int32); u is the
+    caller's rng_f() draw (unused when temp <= 0)."""
+    _lib.call("mh_sample_dev", int(logits), int(vocab), float(temp), float(topp), float(u), int(out))
+
+
 def topk_dev(logits, n: int, n_experts: int, k: int, router_norm: int, sel, w) -> None:
     _lib.call("mh_topk_dev", int(logits), int(n), int(n_experts), int(k), int(router_norm), int(sel), int(w))
 

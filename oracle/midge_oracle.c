@@ -24,6 +24,10 @@
  *   mo_moe_decode        compiled moe() on identical inputs
  *   mo_moe_prefill       compiled route_topk/expert_apply in expert-major order
  *   mo_synth_*           numpy restatement of the same counter hash
+ *   mo_rng_f, mo_sample  compiled sample() with the same generator state
+ *                        (through the reference shim), plus the greedy =
+ *                        first argmax, tiny-top-p = argmax and sampled
+ *                        frequency = softmax checks
  */
 #include <math.h>
 #include <stdint.h>
@@ -465,4 +469,83 @@ int mo_synth_expert(uint8_t *dst, int dt, int64_t hidden, int64_t ffn, int64_t n
         mo_synth_normal(mo_hash64(key, kb + 2), (uint64_t)rows[m], bias_c, (float *)(dst + off[3 * m + 2]));
     }
     return 0;
+}
+
+/* ------------------------------------------------------------ sampling */
+
+/* The reference's generator, one draw (engine/midge.c:641-646): xorshift64
+ * on *state, the high 32 bits of the multiplied state, then 24 bits as a
+ * float in [0, 1). */
+float mo_rng_f(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *state = x;
+    const uint32_t u = (uint32_t)((x * 0x2545F4914F6CDD1DULL) >> 32);
+    return (float)(u >> 8) / 16777216.0f;
+}
+
+typedef struct {
+    float p;
+    int i;
+} MoPI;
+
+/* descending probability, then ascending index (a stable sort's order) */
+static int mo_pi_cmp(const void *a, const void *b) {
+    const MoPI *x = (const MoPI *)a, *y = (const MoPI *)b;
+    if (x->p != y->p) return x->p < y->p ? 1 : -1;
+    return x->i < y->i ? -1 : x->i > y->i;
+}
+
+/* sample() (engine/midge.c:654-679) with the uniform draw u = rng_f()
+ * supplied by the caller: temp <= 0 is the first maximum; otherwise the
+ * temperature softmax (f32 terms, f64 denominator), the tokens by falling
+ * probability, the smallest prefix whose f64 sum reaches topp, and the
+ * token where the running f64 sum first reaches u * (that sum). */
+int mo_sample(const float *logits, int64_t V, float temp, float topp, float u) {
+    if (temp <= 0.f) {
+        int best = 0;
+        float bv = logits[0];
+        for (int64_t i = 1; i < V; i++)
+            if (logits[i] > bv) {
+                bv = logits[i];
+                best = (int)i;
+            }
+        return best;
+    }
+    float mx = logits[0];
+    for (int64_t i = 1; i < V; i++)
+        if (logits[i] > mx) mx = logits[i];
+    MoPI *pi = (MoPI *)malloc((size_t)V * sizeof(MoPI));
+    if (!pi) return -1;
+    double den = 0;
+    for (int64_t i = 0; i < V; i++) {
+        pi[i].p = expf((logits[i] - mx) / temp);
+        pi[i].i = (int)i;
+        den += pi[i].p;
+    }
+    for (int64_t i = 0; i < V; i++) pi[i].p /= (float)den;
+    qsort(pi, (size_t)V, sizeof(MoPI), mo_pi_cmp);
+    double cum = 0;
+    int64_t n = 0;
+    for (; n < V; n++) {
+        cum += pi[n].p;
+        if (cum >= topp) {
+            n++;
+            break;
+        }
+    }
+    const float r = u * (float)cum;
+    double acc = 0;
+    int pick = pi[n - 1].i;
+    for (int64_t i = 0; i < n; i++) {
+        acc += pi[i].p;
+        if (r <= acc) {
+            pick = pi[i].i;
+            break;
+        }
+    }
+    free(pi);
+    return pick;
 }

@@ -60,6 +60,8 @@ _ORACLE_SIGS = {
     "mo_synth_normal": ([_U64, _U64, _F, _P], None),
     "mo_synth_uniform": ([_U64, _U64, _F, _F, _P], None),
     "mo_synth_expert": ([_P, _I, _I64, _I64, _I64, _I, _I, _U64, _I, _I, _F], _I),
+    "mo_rng_f": ([_P], _F),
+    "mo_sample": ([_P, _I64, _F, _F, _F], _I),
 }
 
 _REF_SIGS = {
@@ -74,6 +76,7 @@ _REF_SIGS = {
     "ref_moe_decode": ([C.POINTER(MhMoeLayer), _P, _P, _P, _P], _I),
     "ref_moe_prefill": ([C.POINTER(MhMoeLayer), _I, _P, _P, _P], _I),
     "ref_run_bench": ([], _I),
+    "ref_sample": ([_P, _I64, _F, _F, _P], _I),
 }
 
 _cache: dict[str, C.CDLL] = {}
@@ -330,3 +333,24 @@ def ref_moe_prefill(L: MhMoeLayer, x: np.ndarray, scalar: bool = False):
     w = np.empty((n, L.top_k), np.float32)
     _check(ref(scalar).ref_moe_prefill(C.byref(L), n, _p(x), _p(sel), _p(w)), "ref_moe_prefill")
     return x, sel, w
+
+
+def rng_f(state: int) -> tuple[float, int]:
+    """One draw of the reference's generator: (u, next state)."""
+    st = C.c_uint64(state)
+    u = oracle().mo_rng_f(C.byref(st))
+    return float(u), int(st.value)
+
+
+def sample(logits: np.ndarray, temp: float, topp: float, u: float) -> int:
+    """sample() with the uniform draw u supplied."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    return int(oracle().mo_sample(_p(lg), lg.size, temp, topp, u))
+
+
+def ref_sample(logits: np.ndarray, temp: float, topp: float, state: int) -> tuple[int, int]:
+    """The compiled reference sample() from generator state `state`: (token, next state)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    st = C.c_uint64(state)
+    tok = ref().ref_sample(_p(lg), lg.size, temp, topp, C.byref(st))
+    return int(tok), int(st.value)

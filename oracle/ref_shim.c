@@ -154,3 +154,19 @@ int ref_moe_prefill(const mh_moe_layer *L, int n, float *x, int32_t *sel, float 
 /* The reference's own kernel bench (engine/midge.c:687-720): prints
  * "BENCH q4g32_gbps=<GiB/s> threads=N". */
 int ref_run_bench(void) { return run_bench(); }
+
+/* sample() (engine/midge.c:654-679) on logits[V] with the generator state
+ * *rng (updated as the reference's global would be). */
+int ref_sample(const float *logits, int64_t V, float temp, float topp, uint64_t *rng) {
+    Model m;
+    memset(&m, 0, sizeof m);
+    m.s.vocab = V;
+    m.logits = (float *)logits;
+    m.probs = (float *)malloc((size_t)V * sizeof(float));
+    if (!m.probs) return -1;
+    rng_state = *rng;
+    const int tok = sample(&m, temp, topp);
+    *rng = rng_state;
+    free(m.probs);
+    return tok;
+}

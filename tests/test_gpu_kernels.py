@@ -324,3 +324,35 @@ def test_error_paths_on_device(mh):
         assert ei.value.code == _lib.MH_E_NOMEM
     finally:
         del os.environ["MIDGE_HIP_MAX_BYTES"]
+
+
+@pytest.mark.parametrize("V", [1, 8, 1000, 201088])
+def test_sample_dev_vs_oracle(mh, V):
+    # sample() on device logits (the lm_head's 201088-token vocabulary among
+    # them): greedy and temperature/top-p picks equal the oracle's for the
+    # same draws of the reference's generator
+    from midge_amd.moe import sample_dev
+    say(f"sample_dev V={V}")
+    rng = np.random.default_rng(V)
+    st = 0x853C49E6748FEA9B
+    out = DevBuf(4)
+    for case in range(4):
+        lg = (rng.standard_normal(V) * (1 + 2 * case)).astype(np.float32)
+        if case == 3:
+            lg = np.round(lg)   # many equal logits: ties by token id
+        ld = DevBuf.from_array(lg)
+        for temp in (0.0, 0.6, 1.0, 1.5):
+            for topp in (0.05, 0.9, 1.0):
+                u, st = po.rng_f(st) if temp > 0 else (0.0, st)
+                sample_dev(ld, V, temp, topp, u, out)
+                got = int(out.download(np.int32, (1,))[0])
+                want = po.sample(lg, temp, topp, u)
+                assert got == want, (case, temp, topp, u, got, want)
+        ld.free()
+    # greedy: a NaN at token 0 gives token 0 (the reference loop starts there)
+    lg = np.array([np.nan, 1.0, 3.0, 3.0], np.float32)
+    ld = DevBuf.from_array(lg)
+    sample_dev(ld, 4, 0.0, 1.0, 0.0, out)
+    assert int(out.download(np.int32, (1,))[0]) == 0
+    ld.free()
+    out.free()

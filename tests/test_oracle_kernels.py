@@ -211,3 +211,72 @@ def test_layout_mirror_matches_oracle():
             L = ExpertLayout(dt, hidden, ffn, E)
             off, es, ls = po.expert_layout(dt, hidden, ffn, E)
             assert list(L.off) == off and L.expert_stride == es and L.layer_stride == ls
+
+
+# ------------------------------------------------------------- sampling
+
+def test_rng_matches_xorshift_closed_form():
+    # engine/midge.c:641-646: xorshift64 (12, 25, 27), the high word of the
+    # state times 0x2545F4914F6CDD1D, 24 bits / 2^24
+    st = 0x853C49E6748FEA9B
+    for _ in range(100):
+        x = st
+        x ^= x >> 12
+        x = (x ^ (x << 25)) & (2**64 - 1)
+        x ^= x >> 27
+        want = ((((x * 0x2545F4914F6CDD1D) & (2**64 - 1)) >> 32) >> 8) / 16777216.0
+        u, st = po.rng_f(st)
+        assert st == x and u == np.float32(want)
+
+
+def test_sample_greedy_is_first_argmax():
+    rng = np.random.default_rng(5)
+    for V in (1, 7, 1000):
+        lg = np.round(rng.standard_normal(V) * 2).astype(np.float32)   # many ties
+        assert po.sample(lg, 0.0, 0.9, 0.5) == int(np.argmax(lg))
+    lg = np.array([np.nan, 5.0, 7.0], np.float32)   # the loop starts at a NaN: token 0
+    assert po.sample(lg, 0.0, 1.0, 0.0) == 0
+    lg = np.array([1.0, np.nan, 7.0, 7.0], np.float32)
+    assert po.sample(lg, 0.0, 1.0, 0.0) == 2
+
+
+def test_sample_nucleus_special_cases():
+    rng = np.random.default_rng(6)
+    lg = (rng.standard_normal(500) * 2).astype(np.float32)
+    top = int(np.argmax(lg))
+    for u in (0.0, 0.3, 0.999):
+        assert po.sample(lg, 1.0, 1e-9, u) == top      # a nucleus of one
+    assert po.sample(lg, 0.8, 1.0, 0.0) == top          # u = 0: the most probable
+    # three tokens of probability 0.5, 0.3, 0.2 (temp 1): topp 0.75 keeps two
+    lg = np.log(np.array([0.2, 0.5, 0.3], np.float32))
+    assert po.sample(lg, 1.0, 0.75, 0.5) == 1           # r = 0.4 <= 0.5
+    assert po.sample(lg, 1.0, 0.75, 0.99) == 2          # r = 0.792 > 0.5, <= 0.8
+    assert po.sample(lg, 1.0, 1.0, 0.99) == 0           # the whole set: r = 0.99 > 0.8
+
+
+def test_sample_frequencies_follow_the_tempered_softmax():
+    lg = np.array([0.0, 1.0, 2.0, -1.0, 0.5], np.float32)
+    temp = 0.7
+    p = np.exp((lg - lg.max()) / temp)
+    p /= p.sum()
+    st, counts, N = 12345, np.zeros(5), 20000
+    for _ in range(N):
+        u, st = po.rng_f(st)
+        counts[po.sample(lg, temp, 1.0, u)] += 1
+    assert np.abs(counts / N - p).max() < 0.015
+
+
+def test_sample_vs_reference():
+    if not po.have_ref():
+        pytest.skip("reference engine not built (oracle/_ref)")
+    rng = np.random.default_rng(7)
+    st = 0x853C49E6748FEA9B
+    for V in (8, 1000, 20000):
+        for temp in (0.0, 0.5, 1.0, 1.7):
+            for topp in (0.1, 0.9, 1.0):
+                lg = (rng.standard_normal(V) * 3).astype(np.float32)
+                tok_ref, st2 = po.ref_sample(lg, temp, topp, st)
+                u, st3 = po.rng_f(st) if temp > 0 else (0.0, st)
+                assert st3 == st2
+                assert po.sample(lg, temp, topp, u) == tok_ref, (V, temp, topp)
+                st = st2
