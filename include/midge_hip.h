@@ -141,6 +141,32 @@ int mh_dequant_dev(const mh_wt *t, int64_t r0, int64_t n, float *out);
 /* out[b] = rmsnorm(x[b]) * w for b < batch, length n each (engine/mkern.h:238-243). */
 int mh_rmsnorm_dev(const float *x, const float *w, float *out, int64_t n, float eps, int batch);
 
+/* One attention layer of the trunk for one token, attention()
+ * (engine/midge.c:341-400): rmsnorm, q/k/v GEMVs + biases, optional per-head
+ * q/k RMSNorm, RoPE from the given tables, k/v into the f16 cache slot
+ * pos % cap, GQA softmax attention over the cached positions (with an
+ * optional per-head sink logit), the o GEMV + bias, and the residual add.
+ * Device arrays. cap = window if 0 < window < ctx (a sliding layer, a ring of
+ * window slots), else ctx. */
+typedef struct {
+    int64_t hidden;
+    int32_t n_heads, n_kv_heads, head_dim;
+    int32_t ctx;                        /* positions the rope tables hold */
+    int32_t window;                     /* sliding window of this layer, 0 = none */
+    int32_t qk_norm, sinks;             /* flags (Spec.qk_norm, Spec.sinks) */
+    float norm_eps, attn_scale;
+    mh_wt wq, wk, wv, wo;               /* [nh*hd][hidden], [nkv*hd][hidden] x2, [hidden][nh*hd] */
+    const float *bq, *bk, *bv, *bo;     /* biases */
+    const float *attn_norm;             /* [hidden] */
+    const float *qn, *kn;               /* [head_dim] (qk_norm), else NULL */
+    const float *sink;                  /* [n_heads] (sinks), else NULL */
+    const float *rope_cos, *rope_sin;   /* [ctx][head_dim / 2] (rope_init, midge.c:141-175) */
+    uint16_t *kc, *vc;                  /* [cap][n_kv_heads * head_dim] f16 as wk_to_f16 writes */
+} mh_attn_layer;
+
+/* attention(m, layer, pos) on device x[hidden], in place. */
+int mh_attention_dev(const mh_attn_layer *L, float *x, int pos);
+
 /* sample() (engine/midge.c:654-679) on device logits[V]: the next token into
  * device out[0]. temp <= 0 gives the first maximum; otherwise the
  * temperature softmax, the smallest set of most probable tokens whose

@@ -48,6 +48,17 @@ class MhMoeLayer(C.Structure):
                 ("router_b", C.c_void_p), ("mlp_norm", C.c_void_p)]
 
 
+class MhAttnLayer(C.Structure):
+    """mh_attn_layer: one attention layer (attention(), engine/midge.c:341-400)."""
+    _fields_ = [("hidden", C.c_int64), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+                ("head_dim", C.c_int32), ("ctx", C.c_int32), ("window", C.c_int32),
+                ("qk_norm", C.c_int32), ("sinks", C.c_int32), ("norm_eps", C.c_float),
+                ("attn_scale", C.c_float), ("wq", MhWT), ("wk", MhWT), ("wv", MhWT), ("wo", MhWT),
+                ("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p), ("bo", C.c_void_p),
+                ("attn_norm", C.c_void_p), ("qn", C.c_void_p), ("kn", C.c_void_p), ("sink", C.c_void_p),
+                ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("kc", C.c_void_p), ("vc", C.c_void_p)]
+
+
 _P = C.c_void_p
 _I = C.c_int
 _I64 = C.c_int64
@@ -82,6 +93,7 @@ _SIGS = {
     "mh_moe_prefill_dev": [C.POINTER(MhMoeLayer), _I, _P, _P, _P],
     "mh_topk_dev": [_P, _I, _I, _I, _I, _P, _P],
     "mh_sample_dev": [_P, _I64, _F, _F, _F, _P],
+    "mh_attention_dev": [C.POINTER(MhAttnLayer), _P, _I],
     "mh_expert_major_dev": [C.POINTER(MhMoeLayer), _I, _P, _P, _P, _P],
     "mh_stack_create": [C.POINTER(MhMoeLayer), _I, _I, C.POINTER(_P)],
     "mh_stack_decode": [_P, _P, _I, _P, _P, _P],

@@ -1,0 +1,254 @@
+// mh_attn.hip — the trunk's attention for one decode token, attention()
+// (engine/midge.c:341-400), on the device: the next component of the
+// decode step beside the MoE layers.
+//
+//   rmsnorm          launch_rmsnorm (k_rmsnorm)
+//   q, k, v          the GEMV engine (launch_gemv), any weight dtype
+//   k_attn_prep      one thread per head: biases, per-head RMSNorm (the
+//                    reference's sequential sum), RoPE from the given
+//                    tables, k and v to the f16 cache slot pos % cap with
+//                    the reference's conversion (wk_to_f16)
+//   k_attn_heads     one block per query head: scores over the cached
+//                    positions, softmax with the optional sink logit in the
+//                    denominator, the weighted sum of the cached v
+//   o                the GEMV engine, then k_attn_residual: + bias, x += o
+#include "mh_internal.h"
+
+namespace mh {
+namespace {
+
+constexpr int kAttnThreads = 256;
+
+// wk_to_f16 (engine/mkern.h:261-273): round to nearest even; below the
+// normal range a signed zero; at or past the top (inf, NaN) a signed inf.
+__device__ __forceinline__ uint16_t to_f16_ref(float f) {
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    int e = (int)((x >> 23) & 0xff) - 112;
+    const uint32_t man = x & 0x7fffffu;
+    if (e <= 0) return (uint16_t)sign;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    uint32_t m = man >> 13;
+    const uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (m & 1u))) {
+        if (++m == 0x400u) {
+            m = 0;
+            if (++e >= 31) return (uint16_t)(sign | 0x7c00u);
+        }
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | m);
+}
+
+struct PrepArgs {
+    float *q, *k, *v;
+    const float *bq, *bk, *bv, *qn, *kn, *co, *si;
+    uint16_t *kc, *vc;
+    int nh, nkv, hd, slot, qk_norm;
+    float eps;
+};
+
+// One head's vector in place: + bias, RMSNorm with w (if norm), RoPE; the
+// reference's order and roundings (sequential sum, no contraction).
+__device__ void prep_head(float *u, const float *b, const float *w, bool norm, const float *co, const float *si,
+                          int hd, float eps) {
+#pragma clang fp contract(off)
+    for (int i = 0; i < hd; ++i) u[i] = u[i] + b[i];
+    if (norm) {
+        float ss = 0.f;
+        for (int i = 0; i < hd; ++i) ss += u[i] * u[i];
+        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+        for (int i = 0; i < hd; ++i) u[i] = u[i] * inv * w[i];
+    }
+    const int half = hd / 2;
+    for (int i = 0; i < half; ++i) {
+        const float a = u[i], c = u[i + half];
+        u[i] = a * co[i] - c * si[i];
+        u[i + half] = c * co[i] + a * si[i];
+    }
+}
+
+// thread h < nh: query head h; nh <= h < nh + nkv: key/value head h - nh
+__global__ void __launch_bounds__(kAttnThreads) k_attn_prep(PrepArgs A) {
+#pragma clang fp contract(off)
+    for (int h = blockIdx.x * blockDim.x + threadIdx.x; h < A.nh + A.nkv; h += gridDim.x * blockDim.x) {
+        if (h < A.nh) {
+            prep_head(A.q + (size_t)h * A.hd, A.bq + (size_t)h * A.hd, A.qn, A.qk_norm, A.co, A.si, A.hd, A.eps);
+        } else {
+            const int g = h - A.nh;
+            const size_t o = (size_t)g * A.hd, kvd = (size_t)A.nkv * A.hd;
+            float *k = A.k + o;
+            prep_head(k, A.bk + o, A.kn, A.qk_norm, A.co, A.si, A.hd, A.eps);
+            for (int i = 0; i < A.hd; ++i) {
+                A.kc[(size_t)A.slot * kvd + o + i] = to_f16_ref(k[i]);
+                A.vc[(size_t)A.slot * kvd + o + i] = to_f16_ref(A.v[o + i] + A.bv[o + i]);
+            }
+        }
+    }
+}
+
+struct HeadArgs {
+    const float *q, *sink;
+    const uint16_t *kc, *vc;
+    float *att, *ao;
+    int hd, gq, kvd, nctx, cap, sinks;
+    float scale;
+};
+
+__device__ __forceinline__ float block_max_f(float v, float *part) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = part[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = fmaxf(r, part[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ float block_sum_f(float v, float *part) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) r += part[i];
+    __syncthreads();
+    return r;
+}
+
+// Block h = query head h over the nctx cached positions. Scores are the
+// reference's sequential f16 dot (one position per thread); the softmax sum
+// and the weighted sum of v are split over the block (hd dims x 256 / hd
+// position groups), so they round in a different order than the
+// reference's loops.
+__global__ void __launch_bounds__(kAttnThreads) k_attn_heads(HeadArgs A) {
+#pragma clang fp contract(off)
+    __shared__ float part[kAttnThreads / 64];
+    __shared__ float qs[256];
+    __shared__ float acc[kAttnThreads];
+    const int h = blockIdx.x, kh = h / A.gq, hd = A.hd;
+    const float *qh = A.q + (size_t)h * hd;
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) qs[i] = qh[i];
+    __syncthreads();
+    float *sc = A.att + (size_t)h * A.cap;
+    float mx = -1e30f;
+    for (int t = threadIdx.x; t < A.nctx; t += blockDim.x) {
+        const uint16_t *kt = A.kc + (size_t)t * A.kvd + (size_t)kh * hd;
+        float d = 0.f;
+        for (int i = 0; i < hd; ++i) d += qs[i] * mh_f16(kt[i]);
+        d *= A.scale;
+        sc[t] = d;
+        mx = fmaxf(mx, d);
+    }
+    mx = block_max_f(mx, part);
+    const float sinkv = A.sinks ? A.sink[h] : -1e30f;
+    if (sinkv > mx) mx = sinkv;
+    float s = 0.f;
+    for (int t = threadIdx.x; t < A.nctx; t += blockDim.x) {
+        const float e = expf(sc[t] - mx);
+        sc[t] = e;
+        s += e;
+    }
+    const float den = (A.sinks ? expf(sinkv - mx) : 0.f) + block_sum_f(s, part);
+    const float inv = 1.0f / den;
+    // thread (group j, dim i): positions j, j + nq, ... of dim i
+    const int i = threadIdx.x % hd, j = threadIdx.x / hd, nq = blockDim.x / hd;
+    float o = 0.f;
+    if (j < nq)
+        for (int t = j; t < A.nctx; t += nq)
+            o += (sc[t] * inv) * mh_f16(A.vc[(size_t)t * A.kvd + (size_t)kh * hd + i]);
+    if (j < nq) acc[j * hd + i] = o;
+    __syncthreads();
+    if (threadIdx.x < hd) {
+        float r = 0.f;
+        for (int q = 0; q < nq; ++q) r += acc[q * hd + threadIdx.x];
+        A.ao[(size_t)h * hd + threadIdx.x] = r;
+    }
+}
+
+// y = o + bias; x += y (two roundings, as wk_addbias then the residual loop)
+__global__ void __launch_bounds__(kAttnThreads)
+k_attn_residual(float *__restrict__ x, const float *__restrict__ o, const float *__restrict__ bo, int64_t H) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < H) {
+        const float y = o[i] + bo[i];
+        x[i] = x[i] + y;
+    }
+}
+
+}  // namespace
+}  // namespace mh
+
+using namespace mh;
+
+extern "C" {
+
+int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
+    clear_error();
+    if (!L || !x) return fail(MH_E_ARG, "mh_attention_dev: NULL layer or x");
+    const int64_t H = L->hidden;
+    const int nh = L->n_heads, nkv = L->n_kv_heads, hd = L->head_dim;
+    if (H < 1 || nh < 1 || nkv < 1 || nh % nkv != 0 || hd < 2 || hd % 2 != 0 || hd > 256 || L->ctx < 1)
+        return fail(MH_E_ARG, "mh_attention_dev: shape (hidden %lld, heads %d/%d, head_dim %d, ctx %d)", (long long)H,
+                    nh, nkv, hd, L->ctx);
+    if (pos < 0 || pos >= L->ctx) return fail(MH_E_ARG, "mh_attention_dev: position %d outside [0, %d)", pos, L->ctx);
+    if (L->qk_norm && (!L->qn || !L->kn)) return fail(MH_E_ARG, "mh_attention_dev: qk_norm without weights");
+    if (L->sinks && !L->sink) return fail(MH_E_ARG, "mh_attention_dev: sinks without values");
+    const int kvd = nkv * hd, qd = nh * hd;
+    if (L->wq.rows != qd || L->wq.cols != H || L->wk.rows != kvd || L->wk.cols != H || L->wv.rows != kvd ||
+        L->wv.cols != H || L->wo.rows != H || L->wo.cols != qd)
+        return fail(MH_E_ARG, "mh_attention_dev: projection shapes do not match the heads");
+    MH_TRY(require_init());
+    const int cap = (L->window > 0 && L->window < L->ctx) ? L->window : L->ctx;
+    DevWT wq, wk, wv, wo;
+    MH_TRY(resolve_wt(&L->wq, &wq, "attention wq"));
+    MH_TRY(resolve_wt(&L->wk, &wk, "attention wk"));
+    MH_TRY(resolve_wt(&L->wv, &wv, "attention wv"));
+    MH_TRY(resolve_wt(&L->wo, &wo, "attention wo"));
+    const void *bq, *bk, *bv, *bo, *an, *qn = nullptr, *kn = nullptr, *sk = nullptr, *co, *si;
+    MH_TRY(resolve_weight(L->bq, (uint64_t)qd * 4, &bq, "attention bq"));
+    MH_TRY(resolve_weight(L->bk, (uint64_t)kvd * 4, &bk, "attention bk"));
+    MH_TRY(resolve_weight(L->bv, (uint64_t)kvd * 4, &bv, "attention bv"));
+    MH_TRY(resolve_weight(L->bo, (uint64_t)H * 4, &bo, "attention bo"));
+    MH_TRY(resolve_weight(L->attn_norm, (uint64_t)H * 4, &an, "attention norm"));
+    if (L->qk_norm) {
+        MH_TRY(resolve_weight(L->qn, (uint64_t)hd * 4, &qn, "attention q norm"));
+        MH_TRY(resolve_weight(L->kn, (uint64_t)hd * 4, &kn, "attention k norm"));
+    }
+    if (L->sinks) MH_TRY(resolve_weight(L->sink, (uint64_t)nh * 4, &sk, "attention sinks"));
+    const uint64_t tab = (uint64_t)L->ctx * (hd / 2) * 4;
+    MH_TRY(resolve_weight(L->rope_cos, tab, &co, "rope cos"));
+    MH_TRY(resolve_weight(L->rope_sin, tab, &si, "rope sin"));
+    MH_TRY(resolve_dev(L->kc, (uint64_t)cap * kvd * 2, "attention k cache"));
+    MH_TRY(resolve_dev(L->vc, (uint64_t)cap * kvd * 2, "attention v cache"));
+    MH_TRY(resolve_dev(x, (uint64_t)H * 4, "mh_attention_dev x"));
+    // scratch: xb / o [H], q [qd], k, v [kvd], scores [nh][cap], ao [qd]
+    const size_t oq = ((size_t)H * 4 + 255) & ~(size_t)255, ok = oq + (((size_t)qd * 4 + 255) & ~(size_t)255);
+    const size_t ov = ok + (((size_t)kvd * 4 + 255) & ~(size_t)255), oa = ov + (((size_t)kvd * 4 + 255) & ~(size_t)255);
+    const size_t oo = oa + (((size_t)nh * cap * 4 + 255) & ~(size_t)255), total = oo + (size_t)qd * 4;
+    void *p;
+    MH_TRY(scratch(S_ATTN, total, &p));
+    uint8_t *b8 = (uint8_t *)p;
+    float *xb = (float *)b8, *q = (float *)(b8 + oq), *k = (float *)(b8 + ok), *v = (float *)(b8 + ov);
+    float *att = (float *)(b8 + oa), *ao = (float *)(b8 + oo);
+    hipStream_t s = stream();
+    MH_TRY(launch_rmsnorm(x, (const float *)an, xb, H, L->norm_eps, 1, s));
+    MH_TRY(launch_gemv(wq, xb, q, 1, s));
+    MH_TRY(launch_gemv(wk, xb, k, 1, s));
+    MH_TRY(launch_gemv(wv, xb, v, 1, s));
+    PrepArgs P{q, k, v, (const float *)bq, (const float *)bk, (const float *)bv, (const float *)qn, (const float *)kn,
+               (const float *)co + (size_t)pos * (hd / 2), (const float *)si + (size_t)pos * (hd / 2), L->kc, L->vc,
+               nh, nkv, hd, pos % cap, L->qk_norm ? 1 : 0, L->norm_eps};
+    MH_LAUNCH("attn_prep", k_attn_prep, dim3((unsigned)((nh + nkv + kAttnThreads - 1) / kAttnThreads)),
+              dim3(kAttnThreads), 0, s, P);
+    HeadArgs A{q, (const float *)sk, L->kc, L->vc, att, ao, hd, nh / nkv, kvd, pos + 1 < cap ? pos + 1 : cap, cap,
+               L->sinks ? 1 : 0, L->attn_scale};
+    MH_LAUNCH("attn_heads", k_attn_heads, dim3((unsigned)nh), dim3(kAttnThreads), 0, s, A);
+    MH_TRY(launch_gemv(wo, ao, xb, 1, s));
+    MH_LAUNCH("attn_residual", k_attn_residual, dim3((unsigned)((H + kAttnThreads - 1) / kAttnThreads)),
+              dim3(kAttnThreads), 0, s, x, xb, (const float *)bo, H);
+    return hip_check(hipGetLastError(), "attention launch");
+}
+
+}  // extern "C"

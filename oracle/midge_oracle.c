@@ -24,6 +24,9 @@
  *   mo_moe_decode        compiled moe() on identical inputs
  *   mo_moe_prefill       compiled route_topk/expert_apply in expert-major order
  *   mo_synth_*           numpy restatement of the same counter hash
+ *   mo_rope_table        compiled rope_init() tables, bit for bit
+ *   mo_to_f16            compiled wk_to_f16 over sampled and edge inputs
+ *   mo_attention         compiled attention() (scalar kernels), bit for bit
  *   mo_rng_f, mo_sample  compiled sample() with the same generator state
  *                        (through the reference shim), plus the greedy =
  *                        first argmax, tiny-top-p = argmax and sampled
@@ -548,4 +551,159 @@ int mo_sample(const float *logits, int64_t V, float temp, float topp, float u) {
     }
     free(pi);
     return pick;
+}
+
+/* ------------------------------------------------------------ attention */
+
+/* wk_to_f16 (engine/mkern.h:261-273): round to nearest even, results below
+ * the normal range flush to a signed zero, and anything at or past the top
+ * (inf and NaN included) becomes a signed infinity. */
+uint16_t mo_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    int32_t e = (int32_t)((x >> 23) & 0xff) - 112;   /* rebias 127 -> 15 */
+    const uint32_t man = x & 0x7fffffu;
+    if (e <= 0) return (uint16_t)sign;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    uint32_t m = man >> 13;
+    const uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (m & 1u))) {
+        if (++m == 0x400u) {
+            m = 0;
+            if (++e >= 31) return (uint16_t)(sign | 0x7c00u);
+        }
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | m);
+}
+
+#define MO_PI 3.14159265358979323846   /* the value of glibc's M_PI */
+
+/* rope_init (engine/midge.c:141-175): inverse frequencies theta^(-2i/hd) in
+ * f64, with YaRN's ramp between interpolation (inv / factor) and
+ * extrapolation over the band [low, high] of dimensions and its magnitude
+ * scale 0.1 ln(factor) + 1; tables cos/sin(p * inv) * mscale in f32. */
+void mo_rope_table(int hd, float theta, int yarn, float factor, float beta_fast, float beta_slow, int orig_ctx,
+                   int truncate, int ctx, float *cosv, float *sinv) {
+    const int half = hd / 2;
+    double *inv = (double *)malloc((size_t)half * sizeof(double));
+    double mscale = 1.0;
+    for (int i = 0; i < half; i++) inv[i] = 1.0 / pow((double)theta, (double)(2 * i) / hd);
+    if (yarn) {
+        const double f = factor, base = theta, orig = orig_ctx;
+        double low = hd * log(orig / (beta_fast * 2.0 * MO_PI)) / (2.0 * log(base));
+        double high = hd * log(orig / (beta_slow * 2.0 * MO_PI)) / (2.0 * log(base));
+        if (truncate) {
+            low = floor(low);
+            high = ceil(high);
+        }
+        if (low < 0) low = 0;
+        if (high > hd - 1) high = hd - 1;
+        if (high == low) high = low + 0.001;
+        for (int i = 0; i < half; i++) {
+            double ramp = ((double)i - low) / (high - low);
+            if (ramp < 0) ramp = 0;
+            if (ramp > 1) ramp = 1;
+            const double keep = 1.0 - ramp;   /* 1 = the unscaled frequency */
+            inv[i] = inv[i] / f * (1.0 - keep) + inv[i] * keep;
+        }
+        mscale = 0.1 * log(f) + 1.0;
+    }
+    for (int p = 0; p < ctx; p++)
+        for (int i = 0; i < half; i++) {
+            const double a = (double)p * inv[i];
+            cosv[(size_t)p * half + i] = (float)(cos(a) * mscale);
+            sinv[(size_t)p * half + i] = (float)(sin(a) * mscale);
+        }
+    free(inv);
+}
+
+static void mo_rope_rotate(float *v, int heads, int hd, const float *co, const float *si) {
+    const int half = hd / 2;
+    for (int h = 0; h < heads; h++) {
+        float *u = v + (size_t)h * hd;
+        for (int i = 0; i < half; i++) {
+            const float a = u[i], b = u[i + half];
+            u[i] = a * co[i] - b * si[i];
+            u[i + half] = b * co[i] + a * si[i];
+        }
+    }
+}
+
+static int mo_wt_matvec(const mh_wt *t, const float *x, float *y) {
+    return mo_matvec(t->dt, t->data, t->scales, x, y, t->rows, t->cols);
+}
+
+/* attention() (engine/midge.c:341-400) for one token at position pos, host
+ * arrays: rmsnorm, q/k/v + biases, per-head q/k RMSNorm if enabled, RoPE,
+ * k/v to f16 slot pos % cap, per head: scores q.k * scale over the cached
+ * positions, softmax with the sink logit in the denominator, the weighted
+ * sum of v; o + bias; x += o. */
+int mo_attention(const mh_attn_layer *L, float *x, int pos) {
+    const int hd = L->head_dim, nh = L->n_heads, nkv = L->n_kv_heads, half = hd / 2;
+    const int kvd = nkv * hd, gq = nh / nkv;
+    const int64_t H = L->hidden;
+    const int cap = (L->window > 0 && L->window < L->ctx) ? L->window : L->ctx;
+    float *xb = (float *)malloc((size_t)H * 4), *q = (float *)malloc((size_t)nh * hd * 4);
+    float *k = (float *)malloc((size_t)kvd * 4), *v = (float *)malloc((size_t)kvd * 4);
+    float *sc = (float *)malloc((size_t)cap * 4), *ao = (float *)malloc((size_t)nh * hd * 4);
+    if (!xb || !q || !k || !v || !sc || !ao) return -1;
+    mo_rmsnorm(x, L->attn_norm, xb, H, L->norm_eps);
+    mo_wt_matvec(&L->wq, xb, q);
+    mo_addbias(q, L->bq, (int64_t)nh * hd);
+    mo_wt_matvec(&L->wk, xb, k);
+    mo_addbias(k, L->bk, kvd);
+    mo_wt_matvec(&L->wv, xb, v);
+    mo_addbias(v, L->bv, kvd);
+    if (L->qk_norm) {
+        for (int h = 0; h < nh; h++) mo_rmsnorm(q + (size_t)h * hd, L->qn, q + (size_t)h * hd, hd, L->norm_eps);
+        for (int h = 0; h < nkv; h++) mo_rmsnorm(k + (size_t)h * hd, L->kn, k + (size_t)h * hd, hd, L->norm_eps);
+    }
+    const float *co = L->rope_cos + (size_t)pos * half, *si = L->rope_sin + (size_t)pos * half;
+    mo_rope_rotate(q, nh, hd, co, si);
+    mo_rope_rotate(k, nkv, hd, co, si);
+    const int slot = pos % cap;
+    for (int i = 0; i < kvd; i++) {
+        L->kc[(size_t)slot * kvd + i] = mo_to_f16(k[i]);
+        L->vc[(size_t)slot * kvd + i] = mo_to_f16(v[i]);
+    }
+    const int nctx = pos + 1 < cap ? pos + 1 : cap;
+    for (int h = 0; h < nh; h++) {
+        const float *qh = q + (size_t)h * hd;
+        const int kh = h / gq;
+        float mx = -1e30f;
+        for (int t = 0; t < nctx; t++) {
+            const uint16_t *kt = L->kc + (size_t)t * kvd + (size_t)kh * hd;
+            float d = 0.f;
+            for (int i = 0; i < hd; i++) d += qh[i] * mo_f16_to_f32(kt[i]);
+            d *= L->attn_scale;
+            sc[t] = d;
+            if (d > mx) mx = d;
+        }
+        const float sinkv = L->sinks ? L->sink[h] : -1e30f;
+        if (sinkv > mx) mx = sinkv;
+        float den = L->sinks ? expf(sinkv - mx) : 0.f;
+        for (int t = 0; t < nctx; t++) {
+            sc[t] = expf(sc[t] - mx);
+            den += sc[t];
+        }
+        const float inv = 1.0f / den;
+        float *out = ao + (size_t)h * hd;
+        for (int i = 0; i < hd; i++) out[i] = 0.f;
+        for (int t = 0; t < nctx; t++) {
+            const float w = sc[t] * inv;
+            const uint16_t *vt = L->vc + (size_t)t * kvd + (size_t)kh * hd;
+            for (int i = 0; i < hd; i++) out[i] += w * mo_f16_to_f32(vt[i]);
+        }
+    }
+    mo_wt_matvec(&L->wo, ao, xb);
+    mo_addbias(xb, L->bo, H);
+    for (int64_t i = 0; i < H; i++) x[i] += xb[i];
+    free(xb);
+    free(q);
+    free(k);
+    free(v);
+    free(sc);
+    free(ao);
+    return 0;
 }

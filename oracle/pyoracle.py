@@ -26,6 +26,16 @@ class MhWT(C.Structure):
                 ("data", C.c_void_p), ("scales", C.c_void_p)]
 
 
+class MhAttnLayer(C.Structure):
+    _fields_ = [("hidden", C.c_int64), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+                ("head_dim", C.c_int32), ("ctx", C.c_int32), ("window", C.c_int32),
+                ("qk_norm", C.c_int32), ("sinks", C.c_int32), ("norm_eps", C.c_float),
+                ("attn_scale", C.c_float), ("wq", MhWT), ("wk", MhWT), ("wv", MhWT), ("wo", MhWT),
+                ("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p), ("bo", C.c_void_p),
+                ("attn_norm", C.c_void_p), ("qn", C.c_void_p), ("kn", C.c_void_p), ("sink", C.c_void_p),
+                ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("kc", C.c_void_p), ("vc", C.c_void_p)]
+
+
 class MhMoeLayer(C.Structure):
     _fields_ = [("hidden", C.c_int64), ("ffn", C.c_int64),
                 ("n_experts", C.c_int32), ("top_k", C.c_int32),
@@ -61,6 +71,9 @@ _ORACLE_SIGS = {
     "mo_synth_uniform": ([_U64, _U64, _F, _F, _P], None),
     "mo_synth_expert": ([_P, _I, _I64, _I64, _I64, _I, _I, _U64, _I, _I, _F], _I),
     "mo_rng_f": ([_P], _F),
+    "mo_to_f16": ([_F], _U16),
+    "mo_rope_table": ([_I, _F, _I, _F, _F, _F, _I, _I, _I, _P, _P], None),
+    "mo_attention": ([C.POINTER(MhAttnLayer), _P, _I], _I),
     "mo_sample": ([_P, _I64, _F, _F, _F], _I),
 }
 
@@ -77,6 +90,9 @@ _REF_SIGS = {
     "ref_moe_prefill": ([C.POINTER(MhMoeLayer), _I, _P, _P, _P], _I),
     "ref_run_bench": ([], _I),
     "ref_sample": ([_P, _I64, _F, _F, _P], _I),
+    "ref_rope_table": ([_I, _F, _I, _F, _F, _F, _I, _I, _I, _P, _P], None),
+    "ref_to_f16_attn": ([_F], _U16),
+    "ref_attention": ([C.POINTER(MhAttnLayer), _P, _I], _I),
 }
 
 _cache: dict[str, C.CDLL] = {}

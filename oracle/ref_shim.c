@@ -170,3 +170,86 @@ int ref_sample(const float *logits, int64_t V, float temp, float topp, uint64_t 
     free(m.probs);
     return tok;
 }
+
+/* rope_init (engine/midge.c:141-175)'s tables for the given RoPE/YaRN
+ * parameters and ctx positions. */
+void ref_rope_table(int hd, float theta, int yarn, float factor, float beta_fast, float beta_slow, int orig_ctx,
+                    int truncate, int ctx, float *cosv, float *sinv) {
+    Model m;
+    memset(&m, 0, sizeof m);
+    m.s.head_dim = hd;
+    m.s.rope_theta = theta;
+    m.s.yarn = yarn;
+    m.s.yarn_factor = factor;
+    m.s.yarn_beta_fast = beta_fast;
+    m.s.yarn_beta_slow = beta_slow;
+    m.s.yarn_orig_ctx = orig_ctx;
+    m.s.yarn_truncate = truncate;
+    m.ctx = ctx;
+    rope_init(&m);
+    memcpy(cosv, m.rope_cos, (size_t)ctx * (hd / 2) * 4);
+    memcpy(sinv, m.rope_sin, (size_t)ctx * (hd / 2) * 4);
+    free(m.rope_cos);
+    free(m.rope_sin);
+}
+
+uint16_t ref_to_f16_attn(float f) { return wk_to_f16(f); }
+
+/* attention(m, 0, pos) (engine/midge.c:341-400) for a one-layer Model
+ * holding the given layer (host arrays, x in place). */
+int ref_attention(const mh_attn_layer *L, float *x, int pos) {
+    Model m;
+    memset(&m, 0, sizeof m);
+    const int nh = L->n_heads, hd = L->head_dim, kvd = L->n_kv_heads * L->head_dim;
+    int sliding = L->window > 0;
+    WT wq = { L->wq.dt, L->wq.rows, L->wq.cols, L->wq.data, L->wq.scales };
+    WT wk = { L->wk.dt, L->wk.rows, L->wk.cols, L->wk.data, L->wk.scales };
+    WT wv = { L->wv.dt, L->wv.rows, L->wv.cols, L->wv.data, L->wv.scales };
+    WT wo = { L->wo.dt, L->wo.rows, L->wo.cols, L->wo.data, L->wo.scales };
+    const float *bq = L->bq, *bk = L->bk, *bv = L->bv, *bo = L->bo;
+    const float *an = L->attn_norm, *qn = L->qn, *kn = L->kn, *sk = L->sink;
+    uint16_t *kc = L->kc, *vc = L->vc;
+    m.s.hidden = L->hidden;
+    m.s.n_heads = nh;
+    m.s.n_kv_heads = L->n_kv_heads;
+    m.s.head_dim = hd;
+    m.s.qk_norm = L->qk_norm;
+    m.s.sinks = L->sinks;
+    m.s.sliding_window = L->window;
+    m.s.layer_sliding = &sliding;
+    m.s.norm_eps = L->norm_eps;
+    m.s.attn_scale = L->attn_scale;
+    m.ctx = L->ctx;
+    m.wq = &wq;
+    m.wk = &wk;
+    m.wv = &wv;
+    m.wo = &wo;
+    m.bq = &bq;
+    m.bk = &bk;
+    m.bv = &bv;
+    m.bo = &bo;
+    m.attn_norm = &an;
+    m.qn = &qn;
+    m.kn = &kn;
+    m.sink = &sk;
+    m.rope_cos = (float *)L->rope_cos;
+    m.rope_sin = (float *)L->rope_sin;
+    m.kc = &kc;
+    m.vc = &vc;
+    m.x = x;
+    m.xb = (float *)malloc((size_t)L->hidden * 4);
+    m.q = (float *)malloc((size_t)nh * hd * 4);
+    m.k = (float *)malloc((size_t)kvd * 4);
+    m.v = (float *)malloc((size_t)kvd * 4);
+    m.att = (float *)malloc((size_t)nh * L->ctx * 4);
+    m.ao = (float *)malloc((size_t)nh * hd * 4);
+    int rc = (m.xb && m.q && m.k && m.v && m.att && m.ao) ? 0 : -1;
+    if (!rc) attention(&m, 0, pos);
+    free(m.xb);
+    free(m.q);
+    free(m.k);
+    free(m.v);
+    free(m.att);
+    free(m.ao);
+    return rc;
+}

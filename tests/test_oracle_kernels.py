@@ -6,6 +6,8 @@ a stable argsort, float64 softmax / SwiGLU, the closed-form layout at gpt-oss
 shapes, and the reference engine compiled from its sources (bit-exact on its
 scalar path, within f32 rounding on its AVX2+FMA path).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -280,3 +282,111 @@ def test_sample_vs_reference():
                 assert st3 == st2
                 assert po.sample(lg, temp, topp, u) == tok_ref, (V, temp, topp)
                 st = st2
+
+
+# ------------------------------------------------------------- attention
+
+GPT_OSS_ROPE = dict(theta=150000.0, yarn=1, factor=32.0, beta_fast=32.0, beta_slow=1.0, orig_ctx=4096, truncate=0)
+
+
+def rope_tables(hd: int, ctx: int, fn, theta=10000.0, yarn=0, factor=1.0, beta_fast=32.0, beta_slow=1.0,
+                orig_ctx=4096, truncate=0):
+    half = hd // 2
+    co, si = np.zeros((ctx, half), np.float32), np.zeros((ctx, half), np.float32)
+    fn(hd, theta, yarn, factor, beta_fast, beta_slow, orig_ctx, truncate, ctx, co.ctypes.data, si.ctypes.data)
+    return co, si
+
+
+class AttnHost:
+    """One attention layer on host arrays (q8r projections) with its f16
+    caches, as the oracle and the compiled reference take it."""
+
+    def __init__(self, hidden, nh, nkv, hd, ctx, window, qk_norm, sinks, seed, rope=None):
+        rng = np.random.default_rng(seed)
+        self.keep = []
+
+        def q8(rows, cols):
+            w = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+            s = (rng.random(rows) * 2e-3 + 5e-4).astype(np.float32)
+            self.keep += [w, s]
+            return po.MhWT(DT_Q8R, rows, cols, w.ctypes.data, s.ctypes.data)
+
+        def vec(n, mean=0.0, std=0.1):
+            a = (mean + std * rng.standard_normal(n)).astype(np.float32)
+            self.keep.append(a)
+            return a
+
+        self.cap = window if 0 < window < ctx else ctx
+        self.kvd = nkv * hd
+        self.kc = np.zeros((self.cap, self.kvd), np.uint16)
+        self.vc = np.zeros((self.cap, self.kvd), np.uint16)
+        co, si = rope_tables(hd, ctx, po.oracle().mo_rope_table, **(rope or {}))
+        self.co, self.si = co, si
+        L = po.MhAttnLayer()
+        L.hidden, L.n_heads, L.n_kv_heads, L.head_dim, L.ctx, L.window = hidden, nh, nkv, hd, ctx, window
+        L.qk_norm, L.sinks, L.norm_eps, L.attn_scale = qk_norm, sinks, 1e-5, float(1.0 / np.sqrt(hd))
+        L.wq, L.wk, L.wv, L.wo = q8(nh * hd, hidden), q8(self.kvd, hidden), q8(self.kvd, hidden), q8(hidden, nh * hd)
+        L.bq, L.bk, L.bv, L.bo = (vec(nh * hd).ctypes.data, vec(self.kvd).ctypes.data, vec(self.kvd).ctypes.data,
+                                  vec(hidden).ctypes.data)
+        L.attn_norm = vec(hidden, 1.0).ctypes.data
+        L.qn = vec(hd, 1.0).ctypes.data if qk_norm else None
+        L.kn = vec(hd, 1.0).ctypes.data if qk_norm else None
+        L.sink = vec(nh, 0.0, 1.0).ctypes.data if sinks else None
+        L.rope_cos, L.rope_sin = co.ctypes.data, si.ctypes.data
+        L.kc, L.vc = self.kc.ctypes.data, self.vc.ctypes.data
+        self.L = L
+
+    def run(self, fn, x: np.ndarray, pos: int) -> np.ndarray:
+        x = np.array(x, np.float32, copy=True)
+        assert fn(C.byref(self.L), x.ctypes.data, pos) == 0
+        return x
+
+
+ATTN_SHAPES = {
+    "small_sliding_sinks": dict(hidden=256, nh=8, nkv=2, hd=32, ctx=48, window=16, qk_norm=0, sinks=1),
+    "small_full_qknorm": dict(hidden=256, nh=4, nkv=4, hd=32, ctx=40, window=0, qk_norm=1, sinks=0),
+}
+
+
+def test_to_f16_vs_reference():
+    if not po.have_ref():
+        pytest.skip("reference engine not built (oracle/_ref)")
+    rng = np.random.default_rng(8)
+    vals = np.concatenate([rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000),
+                           [0.0, -0.0, 65504.0, 65520.0, 65519.99, 6.1e-5, 6.0e-5, 5.96e-8, np.inf, -np.inf, np.nan,
+                            1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11]]).astype(np.float32)
+    for v in vals:
+        assert po.oracle().mo_to_f16(float(v)) == po.ref().ref_to_f16_attn(float(v)), v
+
+
+@pytest.mark.parametrize("rope", [dict(), GPT_OSS_ROPE, dict(GPT_OSS_ROPE, truncate=1)])
+def test_rope_tables_vs_reference(rope):
+    if not po.have_ref():
+        pytest.skip("reference engine not built (oracle/_ref)")
+    co, si = rope_tables(64, 300, po.oracle().mo_rope_table, **rope)
+    cr, sr = rope_tables(64, 300, po.ref().ref_rope_table, **rope)
+    assert (co.view(np.uint32) == cr.view(np.uint32)).all() and (si.view(np.uint32) == sr.view(np.uint32)).all()
+    # closed form at position 1 without YaRN: cos/sin of theta^(-2i/hd)
+    if not rope:
+        inv = 1.0 / 10000.0 ** (np.arange(32) * 2 / 64)
+        assert np.allclose(co[1], np.cos(inv), atol=1e-7) and np.allclose(si[1], np.sin(inv), atol=1e-7)
+
+
+@pytest.mark.parametrize("name", list(ATTN_SHAPES))
+def test_attention_vs_reference(name):
+    # a sequence of positions past the sliding window (the ring wraps):
+    # bit for bit against the reference's scalar kernels, and within 1e-4
+    # of the reference as shipped (AVX2 matvecs)
+    if not po.have_ref():
+        pytest.skip("reference engine not built (oracle/_ref)")
+    cfg = ATTN_SHAPES[name]
+    a_or, a_sc, a_rf = (AttnHost(**cfg, seed=11) for _ in range(3))
+    rng = np.random.default_rng(12)
+    for pos in range(cfg["ctx"] - 2):
+        x = rng.standard_normal(cfg["hidden"]).astype(np.float32)
+        xo = a_or.run(po.oracle().mo_attention, x, pos)
+        xs = a_sc.run(po.ref(scalar=True).ref_attention, x, pos)
+        xr = a_rf.run(po.ref().ref_attention, x, pos)
+        assert (xo.view(np.uint32) == xs.view(np.uint32)).all(), pos
+        assert (a_or.kc == a_sc.kc).all() and (a_or.vc == a_sc.vc).all(), pos
+        assert np.linalg.norm(xo - xr) / np.linalg.norm(xr - x) < 1e-4, pos
