@@ -211,6 +211,7 @@ def run_gpu(args, shape):
         extra["prefill"] = prefill_probe(ev, s, args.seed)
     if not args.no_configs:
         extra["lm_head_sample"] = lm_head_sample_probe(ev, s)
+        extra["attention"] = attention_probe(ev, s)
     for b in bufs:
         b.free()
     st.destroy()
@@ -300,6 +301,71 @@ def lm_head_sample_probe(ev, s, reps: int = 20) -> dict:
         res[name + "_us"] = 1e3 * ev.elapsed_ms(a, b) / reps
     midge_amd.sync()
     for d in (w, sc, nw, x, xb, lg, out):
+        d.free()
+    return res
+
+
+def attention_probe(ev, s, fill: int = 1024, reps: int = 20) -> dict:
+    """The trunk's attention for one decode token at the gpt-oss-120b shape
+    (hidden 2880, 64 query / 8 key-value heads of 64, int8 projections,
+    sinks): a full-attention layer with `fill` cached positions and a
+    sliding layer (window 128), HIP-event timed per token over `reps`
+    back-to-back positions. Synthetic weights and RoPE tables."""
+    import ctypes as C
+
+    import midge_amd
+    from midge_amd import DT_Q8R, DevBuf, _lib, synth
+    H, nh, nkv, hd, ctx = 2880, 64, 8, 64, fill + reps + 8
+    qd, kvd = nh * hd, nkv * hd
+    keep = []
+
+    def buf(n, kind, key, a=0.0, b=1.0):
+        d = DevBuf(n * 4 if kind != "i8" else n)
+        if kind == "i8":
+            _lib.call("mh_synth_i8_dev", d.ptr, n, key)
+        elif kind == "u":
+            _lib.call("mh_synth_uniform_dev", d.ptr, n, key, a, float(synth.uniform_c(a, b)))
+        else:
+            _lib.call("mh_synth_normal_dev", d.ptr, n, key, float(synth.normal_c(b)))
+        keep.append(d)
+        return d.ptr
+
+    def wt(rows, cols, key):
+        return _lib.MhWT(DT_Q8R, rows, cols, buf(rows * cols, "i8", key), buf(rows, "u", key + 1, 5e-4, 2.5e-3))
+
+    res = {"workload": "attention(), one decode token, gpt-oss-120b shape (2880, 64/8 heads x 64, int8 q/k/v/o)"}
+    for name, window in (("full", 0), ("sliding128", 128)):
+        L = _lib.MhAttnLayer()
+        L.hidden, L.n_heads, L.n_kv_heads, L.head_dim, L.ctx, L.window = H, nh, nkv, hd, ctx, window
+        L.qk_norm, L.sinks, L.norm_eps, L.attn_scale = 0, 1, 1e-5, 0.125
+        L.wq, L.wk, L.wv, L.wo = wt(qd, H, 920), wt(kvd, H, 922), wt(kvd, H, 924), wt(H, qd, 926)
+        L.bq, L.bk, L.bv, L.bo = buf(qd, "n", 930, b=0.1), buf(kvd, "n", 931, b=0.1), buf(kvd, "n", 932, b=0.1), \
+            buf(H, "n", 933, b=0.1)
+        L.attn_norm = buf(H, "u", 934, 0.5, 1.5)
+        L.sink = buf(nh, "n", 935)
+        L.rope_cos, L.rope_sin = buf(ctx * hd // 2, "u", 936, -1.0, 1.0), buf(ctx * hd // 2, "u", 937, -1.0, 1.0)
+        cap = window if 0 < window < ctx else ctx
+        kc, vc = DevBuf(cap * kvd * 2), DevBuf(cap * kvd * 2)
+        keep += [kc, vc]
+        L.kc, L.vc = kc.ptr, vc.ptr
+        xs = DevBuf((fill + reps) * H * 4)
+        keep.append(xs)
+        _lib.call("mh_synth_normal_dev", xs.ptr, (fill + reps) * H, 938, float(synth.normal_c(1.0)))
+        for pos in range(fill):   # fill the cache
+            _lib.call("mh_attention_dev", C.byref(L), xs.ptr + pos * H * 4, pos)
+        midge_amd.sync()
+        a, b = ev.event(), ev.event()
+        t0 = time.perf_counter()
+        ev.record(a, s)
+        for i in range(reps):
+            _lib.call("mh_attention_dev", C.byref(L), xs.ptr + (fill + i) * H * 4, fill + i)
+        ev.record(b, s)
+        host = (time.perf_counter() - t0) / reps * 1e6
+        res[name + "_us"] = 1e3 * ev.elapsed_ms(a, b) / reps
+        res[name + "_host_enqueue_us"] = host
+        res[name + "_cached"] = min(fill + reps, cap)
+    midge_amd.sync()
+    for d in keep:
         d.free()
     return res
 

@@ -4,10 +4,10 @@
 //
 //   rmsnorm          launch_rmsnorm (k_rmsnorm)
 //   q, k, v          the GEMV engine (launch_gemv), any weight dtype
-//   k_attn_prep      one thread per head: biases, per-head RMSNorm (the
-//                    reference's sequential sum), RoPE from the given
-//                    tables, k and v to the f16 cache slot pos % cap with
-//                    the reference's conversion (wk_to_f16)
+//   k_attn_prep      one block per head, one thread per element: biases,
+//                    per-head RMSNorm (the reference's sequential sum), RoPE
+//                    from the given tables, k and v to the f16 cache slot
+//                    pos % cap with the reference's conversion (wk_to_f16)
 //   k_attn_heads     one block per query head: scores over the cached
 //                    positions, softmax with the optional sink logit in the
 //                    denominator, the weighted sum of the cached v
@@ -47,42 +47,53 @@ struct PrepArgs {
     float eps;
 };
 
-// One head's vector in place: + bias, RMSNorm with w (if norm), RoPE; the
-// reference's order and roundings (sequential sum, no contraction).
-__device__ void prep_head(float *u, const float *b, const float *w, bool norm, const float *co, const float *si,
-                          int hd, float eps) {
+// Block h: query head h (h < nh) or key/value head h - nh, one thread per
+// element, the vector in LDS: + bias, RMSNorm with the head norm weights (if
+// enabled; the reference's sequential sum of squares, in one thread), RoPE;
+// q goes back to memory, k and v (+ bias) to the cache slot as f16.
+__global__ void __launch_bounds__(256) k_attn_prep(PrepArgs A) {
 #pragma clang fp contract(off)
-    for (int i = 0; i < hd; ++i) u[i] = u[i] + b[i];
-    if (norm) {
-        float ss = 0.f;
-        for (int i = 0; i < hd; ++i) ss += u[i] * u[i];
-        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
-        for (int i = 0; i < hd; ++i) u[i] = u[i] * inv * w[i];
-    }
-    const int half = hd / 2;
-    for (int i = 0; i < half; ++i) {
-        const float a = u[i], c = u[i + half];
-        u[i] = a * co[i] - c * si[i];
-        u[i + half] = c * co[i] + a * si[i];
-    }
-}
-
-// thread h < nh: query head h; nh <= h < nh + nkv: key/value head h - nh
-__global__ void __launch_bounds__(kAttnThreads) k_attn_prep(PrepArgs A) {
-#pragma clang fp contract(off)
-    for (int h = blockIdx.x * blockDim.x + threadIdx.x; h < A.nh + A.nkv; h += gridDim.x * blockDim.x) {
-        if (h < A.nh) {
-            prep_head(A.q + (size_t)h * A.hd, A.bq + (size_t)h * A.hd, A.qn, A.qk_norm, A.co, A.si, A.hd, A.eps);
-        } else {
-            const int g = h - A.nh;
-            const size_t o = (size_t)g * A.hd, kvd = (size_t)A.nkv * A.hd;
-            float *k = A.k + o;
-            prep_head(k, A.bk + o, A.kn, A.qk_norm, A.co, A.si, A.hd, A.eps);
-            for (int i = 0; i < A.hd; ++i) {
-                A.kc[(size_t)A.slot * kvd + o + i] = to_f16_ref(k[i]);
-                A.vc[(size_t)A.slot * kvd + o + i] = to_f16_ref(A.v[o + i] + A.bv[o + i]);
-            }
+    __shared__ float u[256];
+    __shared__ float s_inv;
+    const int h = blockIdx.x, i = threadIdx.x, hd = A.hd, half = hd / 2;
+    const bool isq = h < A.nh;
+    const int g = isq ? h : h - A.nh;
+    float *src = isq ? A.q + (size_t)h * hd : A.k + (size_t)g * hd;
+    const float *b = isq ? A.bq + (size_t)h * hd : A.bk + (size_t)g * hd;
+    if (i < hd) u[i] = src[i] + b[i];
+    __syncthreads();
+    if (A.qk_norm) {
+        const float *w = isq ? A.qn : A.kn;
+        if (i == 0) {
+            float ss = 0.f;
+            for (int j = 0; j < hd; ++j) ss += u[j] * u[j];
+            s_inv = 1.0f / sqrtf(ss / (float)hd + A.eps);
         }
+        __syncthreads();
+        const float val = i < hd ? u[i] * s_inv * w[i] : 0.f;
+        __syncthreads();
+        if (i < hd) u[i] = val;
+        __syncthreads();
+    }
+    float r0 = 0.f, r1 = 0.f;
+    if (i < half) {
+        const float a = u[i], c = u[i + half];
+        r0 = a * A.co[i] - c * A.si[i];
+        r1 = c * A.co[i] + a * A.si[i];
+    }
+    __syncthreads();
+    if (i < half) {
+        u[i] = r0;
+        u[i + half] = r1;
+    }
+    __syncthreads();
+    if (i >= hd) return;
+    if (isq) {
+        src[i] = u[i];
+    } else {
+        const size_t o = (size_t)A.slot * A.nkv * hd + (size_t)g * hd + i;
+        A.kc[o] = to_f16_ref(u[i]);
+        A.vc[o] = to_f16_ref(A.v[(size_t)g * hd + i] + A.bv[(size_t)g * hd + i]);
     }
 }
 
@@ -240,8 +251,7 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
     PrepArgs P{q, k, v, (const float *)bq, (const float *)bk, (const float *)bv, (const float *)qn, (const float *)kn,
                (const float *)co + (size_t)pos * (hd / 2), (const float *)si + (size_t)pos * (hd / 2), L->kc, L->vc,
                nh, nkv, hd, pos % cap, L->qk_norm ? 1 : 0, L->norm_eps};
-    MH_LAUNCH("attn_prep", k_attn_prep, dim3((unsigned)((nh + nkv + kAttnThreads - 1) / kAttnThreads)),
-              dim3(kAttnThreads), 0, s, P);
+    MH_LAUNCH("attn_prep", k_attn_prep, dim3((unsigned)(nh + nkv)), dim3((unsigned)((hd + 63) / 64 * 64)), 0, s, P);
     HeadArgs A{q, (const float *)sk, L->kc, L->vc, att, ao, hd, nh / nkv, kvd, pos + 1 < cap ? pos + 1 : cap, cap,
                L->sinks ? 1 : 0, L->attn_scale};
     MH_LAUNCH("attn_heads", k_attn_heads, dim3((unsigned)nh), dim3(kAttnThreads), 0, s, A);
