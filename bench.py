@@ -218,16 +218,17 @@ def run_gpu(args, shape):
     return ms, unique, kern, dom, extra
 
 
-def gemv_probe(ev, s, rows: int = 262144, cols: int = 2880, reps: int = 10, sustain: int = 60) -> dict:
-    """The MXFP4 GEMV engine alone: y = W x over a 262144 x 2880 matrix
-    (424 MB of nibbles + f16 scales, past the 256 MB Infinity Cache).
+def gemv_probe(ev, s, rows: int = 524288, cols: int = 2880, reps: int = 8, sustain: int = 30) -> dict:
+    """The MXFP4 GEMV engine alone: y = W x over a 524288 x 2880 matrix
+    (849 MB of nibbles + f16 scales, over three times the 256 MB Infinity
+    Cache).
 
-    `avg_us` is per launch over `reps` back-to-back launches between one
-    pair of HIP events (the short gaps between launches included). A longer
-    back-to-back run (`sustain` launches, ~5 ms of streaming) is reported
-    beside it, timed in groups of 5: under sustained streaming at this rate
-    the device slows down after ~2 ms (72 -> 87 us per launch in a kernel
-    trace), so its first and last groups are given separately."""
+    `avg_us` is per launch over `reps` back-to-back launches (~1.2 ms)
+    between one pair of HIP events, the few microseconds between launches
+    included. A longer back-to-back run (`sustain` launches, ~4.5 ms of
+    streaming) is reported beside it, timed in groups of 5: under sustained
+    streaming at this rate the device slows down after ~2 ms (by ~20% in
+    kernel traces), so its first and last groups are given separately."""
     import midge_amd
     from midge_amd import DT_MXFP4, DevBuf, _lib, synth
     from midge_amd.kern import WT, matvec_dev
