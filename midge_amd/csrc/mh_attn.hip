@@ -18,6 +18,7 @@ namespace mh {
 namespace {
 
 constexpr int kAttnThreads = 256;
+constexpr int kHeadThreads = 1024;   // per query head: positions, then head_dim x position groups
 
 // wk_to_f16 (engine/mkern.h:261-273): round to nearest even; below the
 // normal range a signed zero; at or past the top (inf, NaN) a signed inf.
@@ -102,6 +103,7 @@ struct HeadArgs {
     const uint16_t *kc, *vc;
     float *att, *ao;
     int hd, gq, kvd, nctx, cap, sinks;
+    int kvec;   // 1: cached keys read 16 bytes at a time (hd % 8 == 0, 16-byte aligned cache)
     float scale;
 };
 
@@ -129,14 +131,14 @@ __device__ __forceinline__ float block_sum_f(float v, float *part) {
 
 // Block h = query head h over the nctx cached positions. Scores are the
 // reference's sequential f16 dot (one position per thread); the softmax sum
-// and the weighted sum of v are split over the block (hd dims x 256 / hd
+// and the weighted sum of v are split over the block (hd dims x 1024 / hd
 // position groups), so they round in a different order than the
 // reference's loops.
-__global__ void __launch_bounds__(kAttnThreads) k_attn_heads(HeadArgs A) {
+__global__ void __launch_bounds__(kHeadThreads) k_attn_heads(HeadArgs A) {
 #pragma clang fp contract(off)
-    __shared__ float part[kAttnThreads / 64];
+    __shared__ float part[kHeadThreads / 64];
     __shared__ float qs[256];
-    __shared__ float acc[kAttnThreads];
+    __shared__ float acc[kHeadThreads];
     const int h = blockIdx.x, kh = h / A.gq, hd = A.hd;
     const float *qh = A.q + (size_t)h * hd;
     for (int i = threadIdx.x; i < hd; i += blockDim.x) qs[i] = qh[i];
@@ -146,7 +148,19 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_heads(HeadArgs A) {
     for (int t = threadIdx.x; t < A.nctx; t += blockDim.x) {
         const uint16_t *kt = A.kc + (size_t)t * A.kvd + (size_t)kh * hd;
         float d = 0.f;
-        for (int i = 0; i < hd; ++i) d += qs[i] * mh_f16(kt[i]);
+        if (A.kvec) {   // 16-byte loads of 8 cached values, summed in order
+            for (int i0 = 0; i0 < hd; i0 += 8) {
+                const uint4 w = *(const uint4 *)(kt + i0);
+                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    d += qs[i0 + 2 * j] * mh_f16((uint16_t)(ww[j] & 0xffffu));
+                    d += qs[i0 + 2 * j + 1] * mh_f16((uint16_t)(ww[j] >> 16));
+                }
+            }
+        } else {
+            for (int i = 0; i < hd; ++i) d += qs[i] * mh_f16(kt[i]);
+        }
         d *= A.scale;
         sc[t] = d;
         mx = fmaxf(mx, d);
@@ -252,9 +266,10 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
                (const float *)co + (size_t)pos * (hd / 2), (const float *)si + (size_t)pos * (hd / 2), L->kc, L->vc,
                nh, nkv, hd, pos % cap, L->qk_norm ? 1 : 0, L->norm_eps};
     MH_LAUNCH("attn_prep", k_attn_prep, dim3((unsigned)(nh + nkv)), dim3((unsigned)((hd + 63) / 64 * 64)), 0, s, P);
+    const int kvec = hd % 8 == 0 && (uintptr_t)L->kc % 16 == 0;
     HeadArgs A{q, (const float *)sk, L->kc, L->vc, att, ao, hd, nh / nkv, kvd, pos + 1 < cap ? pos + 1 : cap, cap,
-               L->sinks ? 1 : 0, L->attn_scale};
-    MH_LAUNCH("attn_heads", k_attn_heads, dim3((unsigned)nh), dim3(kAttnThreads), 0, s, A);
+               L->sinks ? 1 : 0, kvec, L->attn_scale};
+    MH_LAUNCH("attn_heads", k_attn_heads, dim3((unsigned)nh), dim3(kHeadThreads), 0, s, A);
     MH_TRY(launch_gemv(wo, ao, xb, 1, s));
     MH_LAUNCH("attn_residual", k_attn_residual, dim3((unsigned)((H + kAttnThreads - 1) / kAttnThreads)),
               dim3(kAttnThreads), 0, s, x, xb, (const float *)bo, H);
