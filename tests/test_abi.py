@@ -102,3 +102,36 @@ def test_no_device_errors_cleanly():
     assert rc == _lib.MH_E_HIP and "device" in _err()
     with pytest.raises(_lib.MidgeHipError):
         _lib.call("mh_init", 0)
+
+
+def _attn(**kw) -> _lib.MhAttnLayer:
+    a = _lib.MhAttnLayer()
+    a.hidden, a.n_heads, a.n_kv_heads, a.head_dim, a.ctx, a.window = 64, 4, 2, 16, 32, 0
+    a.norm_eps, a.attn_scale = 1e-5, 0.25
+    a.wq = _lib.MhWT(_lib.DT_Q8R, 64, 64, 1, 1)
+    a.wk = _lib.MhWT(_lib.DT_Q8R, 32, 64, 1, 1)
+    a.wv = _lib.MhWT(_lib.DT_Q8R, 32, 64, 1, 1)
+    a.wo = _lib.MhWT(_lib.DT_Q8R, 64, 64, 1, 1)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_attention_and_sample_validation_before_device():
+    # argument checks come before any device work (no GPU needed)
+    x = 1
+    assert _rc("mh_attention_dev", None, x, 0) == _lib.MH_E_ARG
+    assert _rc("mh_attention_dev", C.byref(_attn()), x, 32) == _lib.MH_E_ARG       # pos >= ctx
+    assert "position" in _err()
+    assert _rc("mh_attention_dev", C.byref(_attn()), x, -1) == _lib.MH_E_ARG
+    assert _rc("mh_attention_dev", C.byref(_attn(n_kv_heads=3)), x, 0) == _lib.MH_E_ARG   # 4 % 3
+    assert _rc("mh_attention_dev", C.byref(_attn(head_dim=15)), x, 0) == _lib.MH_E_ARG    # odd
+    assert _rc("mh_attention_dev", C.byref(_attn(qk_norm=1)), x, 0) == _lib.MH_E_ARG      # no weights
+    assert _rc("mh_attention_dev", C.byref(_attn(sinks=1)), x, 0) == _lib.MH_E_ARG        # no sinks
+    bad = _attn()
+    bad.wo = _lib.MhWT(_lib.DT_Q8R, 64, 32, 1, 1)
+    assert _rc("mh_attention_dev", C.byref(bad), x, 0) == _lib.MH_E_ARG
+    assert "projection" in _err()
+    assert _rc("mh_sample_dev", None, 10, 0.0, 1.0, C.c_float(0.0), 1) == _lib.MH_E_ARG
+    assert _rc("mh_sample_dev", 1, 0, 0.0, 1.0, C.c_float(0.0), 1) == _lib.MH_E_ARG
+    assert "vocabulary" in _err()
