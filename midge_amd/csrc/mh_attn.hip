@@ -3,7 +3,8 @@
 // decode step beside the MoE layers.
 //
 //   rmsnorm          launch_rmsnorm (k_rmsnorm)
-//   q, k, v          the GEMV engine (launch_gemv), any weight dtype
+//   q, k, v          one launch on the GEMV engine (k_gemv3), any weight
+//                    dtype; three launch_gemv calls where the shapes differ
 //   k_attn_prep      one block per head, one thread per element: biases,
 //                    per-head RMSNorm (the reference's sequential sum), RoPE
 //                    from the given tables, k and v to the f16 cache slot
@@ -12,12 +13,98 @@
 //                    positions, softmax with the optional sink logit in the
 //                    denominator, the weighted sum of the cached v
 //   o                the GEMV engine, then k_attn_residual: + bias, x += o
-#include "mh_internal.h"
+#include "mh_gemv.cuh"
 
 namespace mh {
 namespace {
 
 constexpr int kAttnThreads = 256;
+
+// q, k and v in one launch: the three matrices (same dtype and width) as
+// consecutive block ranges of one grid, each block a k_gemv block over rows
+// of one of them (block-uniform choice), into y[m] = W[m] x.
+struct Gemv3Args {
+    const uint8_t *W[3];
+    const void *S[3];
+    float *Y[3];
+    int rows[3], nb[3];
+    const float *x;
+    int cols, ns, rpb;
+};
+
+template <int DT>
+__global__ void __launch_bounds__(kGemvThreads) k_gemv3(Gemv3Args A) {
+    constexpr int E = gemv_chunk<DT>::E;
+    extern __shared__ float lds[];
+    int b = blockIdx.x, m = 0;
+    if (b >= A.nb[0]) {
+        b -= A.nb[0];
+        m = 1;
+        if (b >= A.nb[1]) {
+            b -= A.nb[1];
+            m = 2;
+        }
+    }
+    const uint8_t *W = m == 0 ? A.W[0] : m == 1 ? A.W[1] : A.W[2];
+    const void *S = m == 0 ? A.S[0] : m == 1 ? A.S[1] : A.S[2];
+    float *Y = m == 0 ? A.Y[0] : m == 1 ? A.Y[1] : A.Y[2];
+    const int rows = m == 0 ? A.rows[0] : m == 1 ? A.rows[1] : A.rows[2];
+    const int C = A.cols / E;
+    float *res = lds, *red = lds + A.rpb;
+    const int r0 = b * A.rpb, nf = min(A.rpb, rows - r0);
+    const uint32_t rowbytes = (uint32_t)C * 16u * gemv_chunk<DT>::W;
+    float xr[E];
+    load_x<DT>(A.x, C, A.ns, xr);
+    const mh_rsrc rd = gemv_rsrc(W + (size_t)r0 * rowbytes, (uint32_t)nf * rowbytes);
+    const mh_rsrc rs = gemv_rsrc((const uint16_t *)S + (size_t)r0 * C, (uint32_t)nf * (uint32_t)C * 2u);
+    block_gemv<DT>(
+        rd, rs, [&](int f) { return RowOff{mul24((uint32_t)f, rowbytes), mul24((uint32_t)f, 2u * C)}; }, nf, C,
+        A.ns, xr, red, res);
+    for (int f = threadIdx.x; f < nf; f += blockDim.x) {
+        float v = res[f];
+        if constexpr (DT == MH_DT_Q8R) v *= ((const float *)S)[r0 + f];
+        Y[r0 + f] = v;
+    }
+}
+
+// One launch for q, k, v when their dtype and layout allow the GEMV
+// engine's chunked kernel; *done = false leaves them to three launch_gemv.
+template <int DT>
+int launch_qkv_t(const DevWT *w, const float *x, float *const *y, hipStream_t s, bool *done) {
+    constexpr int E = gemv_chunk<DT>::E;
+    const int64_t cols = w[0].cols;
+    *done = false;
+    for (int m = 0; m < 3; ++m)
+        if (w[m].dt != DT || w[m].cols != cols || ((uintptr_t)w[m].data % 16) != 0 || w[m].rows > INT32_MAX)
+            return MH_OK;
+    if (cols % E != 0 || cols / E > kGemvThreads || ((uintptr_t)x % 16) != 0) return MH_OK;
+    const int C = (int)(cols / E);
+    int ns, nt;
+    gemv_shape(C, &ns, &nt);
+    const int64_t total = w[0].rows + w[1].rows + w[2].rows, target = (int64_t)device_cus() * 2;
+    int64_t rpb = (total + target - 1) / target;
+    rpb = ((rpb + ns - 1) / ns) * ns;
+    if (rpb < ns) rpb = ns;
+    if (rpb > 4096) rpb = 4096;
+    Gemv3Args A;
+    int nblk = 0;
+    for (int m = 0; m < 3; ++m) {
+        A.W[m] = w[m].data;
+        A.S[m] = w[m].scales;
+        A.Y[m] = y[m];
+        A.rows[m] = (int)w[m].rows;
+        A.nb[m] = (int)((w[m].rows + rpb - 1) / rpb);
+        nblk += A.nb[m];
+    }
+    A.x = x;
+    A.cols = (int)cols;
+    A.ns = ns;
+    A.rpb = (int)rpb;
+    const size_t lds = ((size_t)rpb + gemv_lds_floats(ns, C)) * sizeof(float);
+    MH_LAUNCH("gemv_qkv", k_gemv3<DT>, dim3((unsigned)nblk), dim3(nt), lds, s, A);
+    *done = true;
+    return hip_check(hipGetLastError(), "q/k/v launch");
+}
 constexpr int kHeadThreads = 1024;   // per query head: positions, then head_dim x position groups
 
 // wk_to_f16 (engine/mkern.h:261-273): round to nearest even; below the
@@ -259,9 +346,22 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
     float *att = (float *)(b8 + oa), *ao = (float *)(b8 + oo);
     hipStream_t s = stream();
     MH_TRY(launch_rmsnorm(x, (const float *)an, xb, H, L->norm_eps, 1, s));
-    MH_TRY(launch_gemv(wq, xb, q, 1, s));
-    MH_TRY(launch_gemv(wk, xb, k, 1, s));
-    MH_TRY(launch_gemv(wv, xb, v, 1, s));
+    {
+        const DevWT w3[3] = {wq, wk, wv};
+        float *const y3[3] = {q, k, v};
+        bool done = false;
+        switch (wq.dt) {
+        case MH_DT_F32: MH_TRY(launch_qkv_t<MH_DT_F32>(w3, xb, y3, s, &done)); break;
+        case MH_DT_Q8R: MH_TRY(launch_qkv_t<MH_DT_Q8R>(w3, xb, y3, s, &done)); break;
+        case MH_DT_Q4G32: MH_TRY(launch_qkv_t<MH_DT_Q4G32>(w3, xb, y3, s, &done)); break;
+        case MH_DT_MXFP4: MH_TRY(launch_qkv_t<MH_DT_MXFP4>(w3, xb, y3, s, &done)); break;
+        }
+        if (!done) {
+            MH_TRY(launch_gemv(wq, xb, q, 1, s));
+            MH_TRY(launch_gemv(wk, xb, k, 1, s));
+            MH_TRY(launch_gemv(wv, xb, v, 1, s));
+        }
+    }
     PrepArgs P{q, k, v, (const float *)bq, (const float *)bk, (const float *)bv, (const float *)qn, (const float *)kn,
                (const float *)co + (size_t)pos * (hd / 2), (const float *)si + (size_t)pos * (hd / 2), L->kc, L->vc,
                nh, nkv, hd, pos % cap, L->qk_norm ? 1 : 0, L->norm_eps};
