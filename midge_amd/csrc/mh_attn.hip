@@ -12,7 +12,9 @@
 //   k_attn_heads     one block per query head: scores over the cached
 //                    positions, softmax with the optional sink logit in the
 //                    denominator, the weighted sum of the cached v
-//   o                the GEMV engine, then k_attn_residual: + bias, x += o
+//   o                the GEMV engine with the residual in its epilogue
+//                    (k_gemv_res: + bias, x += o); GEMV + k_attn_residual
+//                    where the shape needs the general kernel
 #include "mh_gemv.cuh"
 
 namespace mh {
@@ -65,6 +67,58 @@ __global__ void __launch_bounds__(kGemvThreads) k_gemv3(Gemv3Args A) {
         if constexpr (DT == MH_DT_Q8R) v *= ((const float *)S)[r0 + f];
         Y[r0 + f] = v;
     }
+}
+
+// The o projection with the residual in its epilogue:
+// x[r] = x[r] + ((Wo ao)[r] + bo[r]) (two roundings, as wk_addbias then
+// the residual loop of attention()).
+template <int DT>
+__global__ void __launch_bounds__(kGemvThreads)
+k_gemv_res(const uint8_t *__restrict__ W, const void *__restrict__ S, const float *__restrict__ ao,
+           const float *__restrict__ bo, float *__restrict__ x, int rows, int cols, int ns, int rpb) {
+#pragma clang fp contract(off)
+    constexpr int E = gemv_chunk<DT>::E;
+    extern __shared__ float lds[];
+    const int C = cols / E;
+    float *res = lds, *red = lds + rpb;
+    const int r0 = blockIdx.x * rpb, nf = min(rpb, rows - r0);
+    const uint32_t rowbytes = (uint32_t)C * 16u * gemv_chunk<DT>::W;
+    float xr[E];
+    load_x<DT>(ao, C, ns, xr);
+    const mh_rsrc rd = gemv_rsrc(W + (size_t)r0 * rowbytes, (uint32_t)nf * rowbytes);
+    const mh_rsrc rs = gemv_rsrc((const uint16_t *)S + (size_t)r0 * C, (uint32_t)nf * (uint32_t)C * 2u);
+    block_gemv<DT>(
+        rd, rs, [&](int f) { return RowOff{mul24((uint32_t)f, rowbytes), mul24((uint32_t)f, 2u * C)}; }, nf, C,
+        ns, xr, red, res);
+    for (int f = threadIdx.x; f < nf; f += blockDim.x) {
+        float v = res[f];
+        if constexpr (DT == MH_DT_Q8R) v *= ((const float *)S)[r0 + f];
+        const float y = v + bo[r0 + f];
+        x[r0 + f] = x[r0 + f] + y;
+    }
+}
+
+template <int DT>
+int launch_o_res_t(const DevWT &w, const float *ao, const float *bo, float *x, hipStream_t s, bool *done) {
+    constexpr int E = gemv_chunk<DT>::E;
+    *done = false;
+    if (w.cols % E != 0 || w.cols / E > kGemvThreads || ((uintptr_t)w.data % 16) != 0 || ((uintptr_t)ao % 16) != 0 ||
+        w.rows > INT32_MAX)
+        return MH_OK;
+    const int C = (int)(w.cols / E);
+    int ns, nt;
+    gemv_shape(C, &ns, &nt);
+    const int64_t target = (int64_t)device_cus() * 2;
+    int64_t rpb = (w.rows + target - 1) / target;
+    rpb = ((rpb + ns - 1) / ns) * ns;
+    if (rpb < ns) rpb = ns;
+    if (rpb > 4096) rpb = 4096;
+    const int64_t nblk = (w.rows + rpb - 1) / rpb;
+    const size_t lds = ((size_t)rpb + gemv_lds_floats(ns, C)) * sizeof(float);
+    MH_LAUNCH("gemv_o_res", k_gemv_res<DT>, dim3((unsigned)nblk), dim3(nt), lds, s, w.data, w.scales, ao, bo, x,
+              (int)w.rows, (int)w.cols, ns, (int)rpb);
+    *done = true;
+    return hip_check(hipGetLastError(), "o projection launch");
 }
 
 // One launch for q, k, v when their dtype and layout allow the GEMV
@@ -370,9 +424,18 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
     HeadArgs A{q, (const float *)sk, L->kc, L->vc, att, ao, hd, nh / nkv, kvd, pos + 1 < cap ? pos + 1 : cap, cap,
                L->sinks ? 1 : 0, kvec, L->attn_scale};
     MH_LAUNCH("attn_heads", k_attn_heads, dim3((unsigned)nh), dim3(kHeadThreads), 0, s, A);
-    MH_TRY(launch_gemv(wo, ao, xb, 1, s));
-    MH_LAUNCH("attn_residual", k_attn_residual, dim3((unsigned)((H + kAttnThreads - 1) / kAttnThreads)),
-              dim3(kAttnThreads), 0, s, x, xb, (const float *)bo, H);
+    bool fused = false;
+    switch (wo.dt) {
+    case MH_DT_F32: MH_TRY(launch_o_res_t<MH_DT_F32>(wo, ao, (const float *)bo, x, s, &fused)); break;
+    case MH_DT_Q8R: MH_TRY(launch_o_res_t<MH_DT_Q8R>(wo, ao, (const float *)bo, x, s, &fused)); break;
+    case MH_DT_Q4G32: MH_TRY(launch_o_res_t<MH_DT_Q4G32>(wo, ao, (const float *)bo, x, s, &fused)); break;
+    case MH_DT_MXFP4: MH_TRY(launch_o_res_t<MH_DT_MXFP4>(wo, ao, (const float *)bo, x, s, &fused)); break;
+    }
+    if (!fused) {
+        MH_TRY(launch_gemv(wo, ao, xb, 1, s));
+        MH_LAUNCH("attn_residual", k_attn_residual, dim3((unsigned)((H + kAttnThreads - 1) / kAttnThreads)),
+                  dim3(kAttnThreads), 0, s, x, xb, (const float *)bo, H);
+    }
     return hip_check(hipGetLastError(), "attention launch");
 }
 
