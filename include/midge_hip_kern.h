@@ -18,8 +18,8 @@
  * Weights live in the engine's read-only mmaps. The first time a tensor is
  * used its data and scales are uploaded (mh_register_region) and stay
  * resident: HBM takes the place of the page cache. A host that registers the
- * whole experts.midge data region up front (one call after model_load, see
- * INTEGRATION.md) uploads it in one piece instead.
+ * whole experts.midge data region up front (one mh_register_region call
+ * after model_load) uploads it in one piece instead.
  *
  * Failures follow the engine's convention: "# <message>" on stderr and exit
  * code 3 (engine/midge.c:136, 195-227).
