@@ -172,13 +172,16 @@ def run_gpu(args, shape):
     midge_amd.sync()
     kern = {}
     # per-layer phase spans of the one-launch step: mean over blocks, and the slowest block
+    # (k_decode_grp's spans, then k_decode_step's; a name the run's kernel does not stamp is absent)
     spans = ("layer", "x_wait", "router", "route", "route0_gather", "route0_rank", "route0_weights",
-             "route0_publish", "gate_up", "gu_issue", "gu_math", "gu_reduce", "gu_epilogue",
-             "barrier_arrive_prefetch", "barrier_wait", "down_combine", "dn_hload", "dn_math", "dn_reduce",
-             "dn_combine", "tail")
+             "route0_publish", "gu_issue", "gu_math", "gu_reduce", "h_publish", "dn_stage", "h_wait", "dn_math",
+             "y_publish", "combine", "gate_up", "gu_epilogue", "barrier_arrive_prefetch", "barrier_wait",
+             "down_combine", "dn_hload", "dn_reduce", "dn_combine", "tail", "gu_first_pair", "gu_mid_pair",
+             "gu_last_pair", "gu_wave7_lag", "gu_barrier")
     phases = tuple(f"decode_step/{n}{m}" for n in spans for m in ("", ".max")) + tuple(
         f"decode_step/crit_{n}" for n in ("logits", "routed", "h", "x")) + tuple(
-        f"decode_step/t{st:02d}.{w}" for st in (0, 15, 1, 16, 17, 18, 2, 9, 10, 11, 3, 4, 5, 12, 13, 14, 6, 7)
+        f"decode_step/t{st:02d}.{w}" for st in (0, 15, 1, 16, 17, 18, 2, 9, 19, 20, 10, 21, 22, 11, 3, 4, 5, 12, 13,
+                                                14, 6, 7)
         for w in ("first", "last"))
     for name in ("decode_step", "expert_gu", "expert_down", "gemv", "topk", "rmsnorm", "combine_decode") + phases:
         tot, n = profile_query(name)
@@ -190,7 +193,7 @@ def run_gpu(args, shape):
         # one launch per step: the timed region's event time per step is the
         # launch's average duration (the profiled launches also write phase
         # stamps and run a few percent slower)
-        dom = {"name": "k_decode_step (all layers of a step in one cooperative launch)",
+        dom = {"name": "k_decode_grp (all layers of a step in one launch)",
                "bytes": step_bytes(shape, args.batch, unique), "avg_us": ms / args.steps * 1e3,
                "profiled_avg_us": kern["decode_step"]["avg_us"]}
         tpath = os.path.join(ROOT, "profiles", "decode_step_120b_b1_traffic.json")

@@ -1,39 +1,50 @@
 // mh_decode.hip — a whole MoE decode step (every layer of a stack, batch 1)
-// in one cooperative launch: the MoE half of forward()'s layer loop
-// (engine/midge.c:557-560) with moe() (engine/midge.c:469-549) per layer.
+// in one launch: the MoE half of forward()'s layer loop (engine/midge.c:
+// 557-560) with moe() (engine/midge.c:469-549) per layer.
 //
-// One block per CU, 512 threads. Per layer:
-//   A  router     every block reads x (the previous layer's output, as
-//                 sequence-tagged words), forms xb = rmsnorm(x) * w in LDS;
-//                 the router's rows are spread over the blocks and each
-//                 logit is published as a tagged word.
-//   route         every block gathers the tagged logits (from one of
-//                 kLR copies, so that few blocks poll each line) and ranks
-//                 them (stable top-k, ties to the lower index) itself: all
-//                 reach the same selection and weights, with no broadcast.
-//   B  gate/up    each block takes an even share of the routed experts'
-//                 (gate, up) row pairs, with the bias + clamped SwiGLU
-//                 epilogue -> h[k][ffn]; then a grid barrier.
-//   C  down       each block owns a slice of output rows for all k experts.
-//                 MXFP4 stacks: the rows are loaded during the barrier,
-//                 staged in LDS and multiplied on the matrix cores (f16 MFMA
-//                 over h split into two f16 terms); otherwise they are
-//                 loaded into registers between the barrier's arrive and wait
-//                 and multiplied on the vector ALUs. Epilogue: y = Wd h + bd,
-//                 moe = sum_i w_i y_i in selection order, x += moe, written
-//                 as tagged words for the next layer (plain floats after the
-//                 last layer).
+// Two kernels share the routing phase (route_layer):
+//
+// k_decode_grp — MXFP4 experts with the clamped SwiGLU (gpt-oss), the
+//   default. The grid is G blocks per routed slot (G * K blocks, at most one
+//   per CU). Block (slot i, index gi) owns gate/up pairs [PB gi, +PB) and
+//   down rows [RB gi, +RB) of slot i's expert, so a block's work touches one
+//   expert and its h comes from its own group of G blocks. Per layer:
+//     A  every block reads x (the previous layer's output, tagged words from
+//        one of kXR copies) and forms xb = rmsnorm(x) * w in LDS; blocks
+//        b < E compute router logit b and publish it in kLR copies;
+//     R  every block's first wave gathers the logits and ranks them itself
+//        (stable top-k, ties to the lower index): all blocks reach the same
+//        selection and weights and nothing is broadcast;
+//     B  the block issues every weight load of its share at once, the
+//        gate/up pairs first and the down rows behind them, so the layer's
+//        weights stream as one transfer; the gate/up math runs as the data
+//        arrives; bias + clamped SwiGLU give h, published as tagged words
+//        (h as two f16 terms) to the slot's group;
+//     C  the down rows are staged in LDS; each wave polls only the part of
+//        h that its matrix-core K steps read and multiplies (f16 MFMA); the
+//        down bias completes y_i for the block's rows, which slots i > 0
+//        publish as tagged words;
+//     D  the slot-0 block of each row slice gathers y_1 .. y_{K-1} of its
+//        rows, forms moe = sum_i w_i y_i in selection order and x += moe
+//        (engine/midge.c:544-548), and publishes x in kXR copies.
+//   There is no grid-wide barrier: every exchange is a tagged word the
+//   consumer polls, and every block's y is waited for once per layer, which
+//   also orders the reuse of the exchange buffers from layer to layer.
+//
+// k_decode_step — the vector-ALU path (q4g32 experts, plain SiLU, down
+//   scales the f16 path cannot hold exactly). One block per CU; a block
+//   takes an even share of all routed (gate, up) pairs and, after one grid
+//   barrier, a slice of output rows for every routed expert.
+//
 // Tagged words carry the producer's sequence number next to the value in one
-// 64-bit store, so a consumer needs no separate barrier: it polls the words
-// it needs until every tag matches. The one full barrier per layer (before
-// the down phase, which needs all of h) is a gather/broadcast over per-block
-// flags (measured faster than every block polling every flag). Every wait is
-// bounded: one that does not complete within ~1 s raises an error flag and
-// every block exits.
+// 64-bit store, so a consumer polls the data itself. Every wait is bounded:
+// one that does not complete within ~1 s raises an error flag and every
+// block exits.
 #include <stdio.h>
 #include <stdlib.h>
 
 #include <algorithm>
+#include <utility>
 #include <vector>
 
 #include "mh_gemv.cuh"
@@ -48,56 +59,89 @@ struct StepLayer {
     const float *norm_w;
 };
 
-struct StepArgs {
+// What the routing phase reads and writes, common to both kernels.
+struct RouteArgs {
     const StepLayer *layers;
-    int n_layers, H, F, E, K;
-    int CH, CF;              // 16-byte chunks per expert row: H / 32, F / 32
-    uint64_t stride;
-    uint64_t off[9];
-    float alpha, limit, eps;
-    int act_plain, router_norm;
-    float *x;                // [H], in place
+    int n_layers, H, E, K;
+    float eps;
+    int router_norm;
+    float *x;                // [H] input at layer 0 (and the last layer's output)
     int32_t *sel;            // [L][K] or null
     float *w;                // [L][K] or null
     uint32_t *usage;         // [L][E] or null
     uint64_t *lw;            // [kLR][lws] tagged logits: kLR copies, lws words apart
     int lws;
+    unsigned *err;
+    unsigned long long *trace;   // [L][kStamps][gridDim.x] per-block phase timestamps, or null
+};
+
+struct StepArgs {            // k_decode_step
+    RouteArgs R;
+    int F;
+    int CH, CF;              // 16-byte chunks per expert row: H / 32, F / 32
+    uint64_t stride;
+    uint64_t off[9];
+    float alpha, limit;
+    int act_plain;
     uint64_t *xw;            // [H] tagged x between layers
-    float *h;                // [K][F] scratch (VALU path)
-    uint16_t *h16;           // [2][K][Fpad] f16 planes of h (MFMA path)
-    int Fpad;                // ffn rounded up to 128
+    float *h;                // [K][F] scratch
     unsigned *flags;         // [gridDim.x] barrier flags
     unsigned *go;            // barrier release word (written by block 0)
     unsigned seq0;           // first sequence number of this launch (3 per layer)
-    unsigned *err;
-    unsigned long long *trace;   // [L][kStamps][gridDim.x] per-block phase timestamps, or null
-    int res_floats;              // LDS floats of the reduced-rows area
-    int red_floats;              // LDS floats of the partial-sum area
+};
+
+struct GrpArgs {             // k_decode_grp
+    RouteArgs R;
+    int F;
+    int CH, CF;              // 16-byte chunks per row: H / 32 (gate/up), F / 32 (down)
+    int G, PB, RB;           // blocks per slot; gate/up pairs and down rows per block
+    uint64_t stride;
+    uint64_t off[9];
+    float alpha, limit;
+    uint64_t *xw;            // [kXR][xws] tagged x
+    int xws;
+    uint64_t *hw;            // [kHR][K][hws] tagged h (payload: hi f16 | lo f16 << 16)
+    int hws;
+    uint64_t *yw;            // [K][H] tagged y of slots 1 .. K-1
+    unsigned *flags;         // [gridDim.x] per-block flags (layers with an unfilled slot)
+    unsigned seq0;           // first sequence number of this launch (4 per layer)
 };
 
 namespace {
 
 constexpr int kThreads = 512;   // 8 waves: 2 per SIMD, up to 256 VGPRs each
 constexpr int kUP = 9;          // gate/up row pairs in flight per thread
-constexpr int kUC = 12;         // down rows in flight per thread
+constexpr int kUC = 12;         // down rows in flight per thread (k_decode_step)
+constexpr int kUD = 9;          // down rows in flight per thread (k_decode_grp)
+static_assert(kUD <= kUP, "k_decode_grp issues one down-row load per gate/up pair");
 constexpr int kNX = 8;          // x elements per thread in the router phase (H <= kNX * kThreads)
 constexpr unsigned kSpinLimit = 1u << 20;
 constexpr int kStamps = 24;     // phase timestamps per layer and block while profiling
 constexpr int kEL = 2;          // logits per lane in the routing wave (E <= 64 * kEL)
 constexpr int kLR = 8;          // copies of the logits (each polled by NB / kLR blocks)
+constexpr int kXR = 8;          // copies of x (k_decode_grp)
+constexpr int kHR = 2;          // copies of h (k_decode_grp: each polled by G / kHR blocks)
 constexpr int kGoCopies = 8;    // copies of the barrier's release word
 constexpr int kGoStride = 64;   // words between them (256 B)
-// static LDS capacities of the one-launch step (plan creation checks a
-// stack against them)
+constexpr int kMaxK = 16;       // engine/midge.c:44 MAX_TOPK
+constexpr int kMaxGrpK = 8;     // top-k of k_decode_grp (its combine polls (k - 1) x kRBMax words)
+// static LDS capacities (plan creation checks a stack against them)
 constexpr int kHMax = 3072;         // hidden size
 constexpr int kResMax = 1024;       // floats of reduced rows
 constexpr int kRedMax = 8192;       // floats of partial sums
+constexpr int kQ = 3;               // 128-column K steps per wave (ffn <= 8 * kQ * 128)
+constexpr int kKPad = 8 * kQ * 128; // largest ffn of k_decode_grp
+constexpr int kRBMax = 48;          // down rows per block of k_decode_grp (3 matrix-core row tiles)
+constexpr int kSDMax = kKPad / 32 + 1;   // LDS row stride (chunks) of the staged down rows
+constexpr int kGrpBig = kRBMax * kSDMax * 16 > kRedMax * 4 ? kRBMax * kSDMax * 16 : kRedMax * 4;
+constexpr int kScW = 8192;          // bytes per staged scale window of k_decode_grp (gate, up, down)
+constexpr int kScLoads = 3;         // 16-byte scale loads per thread (3 windows <= kScLoads * 512 chunks)
 
 // Memory access. Every load goes through a buffer resource (32-bit offsets,
 // out-of-range reads return 0). Weights are streamed with the nontemporal
-// hint. Data that blocks exchange inside the launch (x, logits, h) is
+// hint. Data that blocks exchange inside the launch (x, logits, h, y) is
 // written with device-scope stores and read with device-scope loads, which
-// are coherent across the XCDs' L2 caches: the barriers then need no L2
+// are coherent across the XCDs' L2 caches: the exchanges then need no L2
 // write-back or invalidate, and read-only weights stay cached.
 constexpr int kNT = 2;     // cache-policy bits: nontemporal
 constexpr int kDev = 16;   // cache-policy bits: device scope
@@ -131,6 +175,9 @@ __device__ __forceinline__ mh_u4 ld_dev16(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ void st_dev(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void raise_err(unsigned *err) {
+    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 // An opaque copy of v: values derived from it are recomputed where they are
 // used instead of being hoisted out of the layer loop and held in registers
@@ -139,6 +186,16 @@ __device__ __forceinline__ int opaque(int v) {
     asm volatile("" : "+v"(v));
     return v;
 }
+
+// Per-block phase timestamps (100 MHz wall clock), written by thread 0 of
+// each block while profiling: trace[(layer * kStamps + id) * blocks + block].
+struct Stamper {
+    unsigned long long *tr;
+    int nb;
+    __device__ __forceinline__ void operator()(int l, int id) const {
+        if (tr) tr[(size_t)(l * kStamps + id) * nb] = wall_clock64();
+    }
+};
 
 // Arrive: every wave's stores have completed (device-scope stores complete
 // at the device coherence point), then thread 0 publishes `seq`.
@@ -188,7 +245,7 @@ __device__ __forceinline__ bool bar_wait(const unsigned *flags, unsigned *go, un
         }
         if (lane == 0) {
             *s_ok = ok ? 1 : 0;
-            if (!ok) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (!ok) raise_err(err);
         }
     }
     __syncthreads();
@@ -207,13 +264,15 @@ __device__ __forceinline__ float block_sum(float v, float *part) {
     return s;
 }
 
-// Tagged words: (tag << 32) | value bits in one device-scope 64-bit store.
-__device__ __forceinline__ void st_tag(uint64_t *p, unsigned tag, float v) {
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Tagged words: (tag << 32) | payload in one device-scope 64-bit store.
+__device__ __forceinline__ void st_tag_u(uint64_t *p, unsigned tag, uint32_t v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void st_tag(uint64_t *p, unsigned tag, float v) { st_tag_u(p, tag, __float_as_uint(v)); }
 __device__ __forceinline__ uint64_t ld_tag(uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ bool tag_is(uint64_t w, unsigned tag) { return (unsigned)(w >> 32) == tag; }
 
 // Maximum over the wave (every lane gets it): DPP within rows of 16, then
 // row broadcasts; lanes a DPP step does not write keep their value.
@@ -324,13 +383,13 @@ struct RouterPref {
 };
 
 template <int RDT>
-__device__ __forceinline__ RouterPref prefetch_router(const StepArgs &A, int l) {
+__device__ __forceinline__ RouterPref prefetch_router(const RouteArgs &R, int l) {
     RouterPref p;
-    const StepLayer Lp = A.layers[l];
-    const int b = blockIdx.x, t = threadIdx.x, H = A.H;
-    const int e = b < A.E ? b : 0;
+    const StepLayer Lp = R.layers[l];
+    const int b = blockIdx.x, t = threadIdx.x, H = R.H;
+    const int e = b < R.E ? b : 0;
     constexpr uint32_t wb = RDT == MH_DT_Q8R ? 1u : 4u;   // bytes per router weight
-    const rsrc_t rw = make_rsrc(Lp.router_w, (uint32_t)A.E * (uint32_t)H * wb);
+    const rsrc_t rw = make_rsrc(Lp.router_w, (uint32_t)R.E * (uint32_t)H * wb);
 #pragma unroll
     for (int k = 0; k < kNX; ++k) {   // past H: the next row's weights (or 0), met by x = 0
         const uint32_t o = ((uint32_t)e * (uint32_t)H + (uint32_t)(t + k * kThreads)) * wb;
@@ -338,8 +397,8 @@ __device__ __forceinline__ RouterPref prefetch_router(const StepArgs &A, int l) 
         else p.rw[k] = __builtin_amdgcn_raw_buffer_load_b32(rw, o, 0, 0);
     }
     p.rs = 1.0f;
-    if constexpr (RDT == MH_DT_Q8R) p.rs = ld_f(make_rsrc(Lp.router_s, (uint32_t)A.E * 4u), (uint32_t)e * 4u);
-    p.rb = ld_f(make_rsrc(Lp.router_b, (uint32_t)A.E * 4u), (uint32_t)e * 4u);
+    if constexpr (RDT == MH_DT_Q8R) p.rs = ld_f(make_rsrc(Lp.router_s, (uint32_t)R.E * 4u), (uint32_t)e * 4u);
+    p.rb = ld_f(make_rsrc(Lp.router_b, (uint32_t)R.E * 4u), (uint32_t)e * 4u);
     const rsrc_t rn = make_rsrc(Lp.norm_w, (uint32_t)H * 4u);
 #pragma unroll
     for (int k = 0; k < kNX; ++k) p.nw[k] = ld_f(rn, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
@@ -371,19 +430,189 @@ __device__ __forceinline__ float2 block_sum2(float a, float c, float *part) {
     return make_float2(sa, sc);
 }
 
+// LDS of the routing phase.
+struct RouteLds {
+    float *part;     // [16]
+    int *sel;        // [kMaxK]
+    float *w;        // [kMaxK]
+    float *xs;       // [H] x at layer start
+    float *xbs;      // xb = rmsnorm(x) * w in 32-element groups padded to 33 floats
+};
+
+// Phase A and the routing of layer l, common to both kernels.
+//  - x: from R.x at layer 0, else as tagged words from xsrc (tag xtag); each
+//    thread loads its <= kNX words and re-polls only the late ones.
+//  - One DPP-reduced block sum gives both sum(x^2) and this block's router
+//    dot with x * w (the norm weights): logit b = inv * dot * scale + bias,
+//    with inv = 1 / sqrt(mean(x^2) + eps) factored out of the row's dot
+//    (engine/mkern.h:238-243, then the router matvec). Blocks b < E publish
+//    it in kLR copies; rows beyond the grid are looped over.
+//  - xb = x * inv * w goes to LDS in 32-element groups padded to 33 floats:
+//    a thread reading group c element by element and its wave's 64 lanes
+//    then hit 64 distinct banks.
+//  - Every block's first wave gathers the E logits from copy b % kLR and
+//    ranks them (wave_topk: the reference's insertion order, ties to the
+//    lower index) and computes the weights; block 0 records sel, w and the
+//    usage counts. The block's other waves wait at the closing barrier.
+// Returns false, with the error flag raised, if a wait timed out (every
+// thread of the block returns the same value).
+template <int RDT>
+__device__ __forceinline__ bool route_layer(const RouteArgs &R, const RouterPref &pf, int l, uint64_t *xsrc,
+                                            unsigned xtag, unsigned ltag, const RouteLds &S, const Stamper &stamp) {
+    const int H = R.H, E = R.E, K = R.K;
+    const int NB = gridDim.x, b = blockIdx.x, t = threadIdx.x;
+    const StepLayer Ly = R.layers[l];
+    {
+        float xv[kNX];
+        if (l == 0) {
+            const rsrc_t rx = make_rsrc(R.x, (uint32_t)H * 4u);
+#pragma unroll
+            for (int k = 0; k < kNX; ++k) xv[k] = ld_dev(rx, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
+        } else {
+            uint64_t wv[kNX];
+            const int tt = opaque(t);
+#pragma unroll
+            for (int k = 0; k < kNX; ++k) {
+                const int i = tt + k * kThreads;
+                wv[k] = i < H ? ld_tag(xsrc + i) : (uint64_t)xtag << 32;
+            }
+            bool late = false;
+            for (unsigned spins = 0;; ++spins) {
+                bool ready = true;
+#pragma unroll
+                for (int k = 0; k < kNX; ++k) ready = ready && tag_is(wv[k], xtag);
+                if (ready) break;
+                if (spins > kSpinLimit) {
+                    late = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                for (int k = 0; k < kNX; ++k) {
+                    const int i = tt + k * kThreads;
+                    if (i < H && !tag_is(wv[k], xtag)) wv[k] = ld_tag(xsrc + i);
+                }
+            }
+            if (__syncthreads_or(late)) {
+                if (t == 0) raise_err(R.err);
+                return false;
+            }
+#pragma unroll
+            for (int k = 0; k < kNX; ++k) xv[k] = __uint_as_float((uint32_t)wv[k]);
+        }
+        stamp(l, 15);
+        float ss = 0.f, dp = 0.f;
+#pragma unroll
+        for (int k = 0; k < kNX; ++k) {
+            ss = __builtin_fmaf(xv[k], xv[k], ss);
+            dp = __builtin_fmaf(router_weight<RDT>(pf.rw[k]), xv[k] * pf.nw[k], dp);
+        }
+        const float2 sums = block_sum2(ss, dp, S.part);
+        const float inv = 1.0f / sqrtf(sums.x / (float)H + R.eps);
+        if (b < E && t < kLR) {   // one copy per logit replica
+            float p = sums.y * inv;
+            if constexpr (RDT == MH_DT_Q8R) p *= pf.rs;
+            st_tag(R.lw + (size_t)t * R.lws + b, ltag, p + pf.rb);
+        }
+#pragma unroll
+        for (int k = 0; k < kNX; ++k) {
+            const int i = t + k * kThreads;
+            if (i < H) {
+                S.xs[i] = xv[k];
+                S.xbs[(i >> 5) * 33 + (i & 31)] = xv[k] * inv * pf.nw[k];
+            }
+        }
+    }
+    __syncthreads();
+    // router rows beyond the grid (more experts than blocks): over xb
+    constexpr int RE = mh_chunk<RDT>::E;   // elements per router chunk (16 int8 / 4 f32)
+    const int CR = H / RE;
+    for (int e = b + NB; e < E; e += NB) {
+        float p = 0.f;
+        const rsrc_t rw = make_rsrc(Ly.router_w, (uint32_t)E * (uint32_t)CR * 16u);
+        for (int c = t; c < CR; c += kThreads) {
+            const mh_u4 q = ld_w16(rw, (uint32_t)(e * CR + c) * 16u);
+            const int i0 = c * RE;   // a router chunk lies inside one 32-element group
+            p += mh_dot_chunk<RDT>(q, S.xbs + (i0 >> 5) * 33 + (i0 & 31));
+        }
+        p = block_sum(p, S.part);
+        if (t < kLR) {
+            if constexpr (RDT == MH_DT_Q8R) p *= Ly.router_s[e];
+            st_tag(R.lw + (size_t)t * R.lws + e, ltag, p + Ly.router_b[e]);
+        }
+    }
+    stamp(l, 1);
+    bool late = false;
+    if (t < 64) {
+        const int lane = t;
+        const int tt = opaque(t);
+        uint64_t *lr = R.lw + (size_t)(b % kLR) * R.lws;
+        uint64_t wv[kEL];
+#pragma unroll
+        for (int j = 0; j < kEL; ++j) {
+            const int e = tt + 64 * j;
+            wv[j] = e < E ? ld_tag(lr + e) : (uint64_t)ltag << 32;
+        }
+        for (unsigned spins = 0;; ++spins) {
+            bool ready = true;
+#pragma unroll
+            for (int j = 0; j < kEL; ++j) ready = ready && tag_is(wv[j], ltag);
+            if (__all(ready)) break;
+            if (spins > kSpinLimit) {
+                late = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int j = 0; j < kEL; ++j) {
+                const int e = tt + 64 * j;
+                if (e < E && !tag_is(wv[j], ltag)) wv[j] = ld_tag(lr + e);
+            }
+        }
+        if (b == 0) stamp(l, 16);
+        float v[kEL], v0[kEL];
+#pragma unroll
+        for (int j = 0; j < kEL; ++j) {
+            v[j] = lane + 64 * j < E ? __uint_as_float((uint32_t)wv[j]) : -INFINITY;
+            v0[j] = v[j];
+        }
+        int my_sel;
+        float my_val;
+        wave_topk(v, K, &my_sel, &my_val);
+        if (b == 0) stamp(l, 17);
+        const float my_w = wave_weight(v0, K, R.router_norm, my_val);
+        if (b == 0) stamp(l, 18);
+        if (lane < K) {
+            // (addresses from an opaque lane: recomputed here, not hoisted
+            // out of the layer loop and spilled)
+            const int ln = opaque(lane);
+            S.sel[ln] = my_sel;
+            S.w[ln] = my_w;
+            if (b == 0) {
+                if (R.sel) R.sel[(size_t)l * K + ln] = my_sel;
+                if (R.w) R.w[(size_t)l * K + ln] = my_w;
+                if (R.usage && my_sel >= 0)
+                    __hip_atomic_fetch_add(&R.usage[(size_t)l * E + my_sel], 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+    if (__syncthreads_or(late)) {
+        if (t == 0) raise_err(R.err);
+        return false;
+    }
+    return true;
+}
+
 // ---------------------------------------------------------------- MFMA
-// The down projection of an MXFP4 stack runs on V_MFMA_F32_16X16X32_F16
+// The down projection of k_decode_grp runs on V_MFMA_F32_16X16X32_F16
 // (measured layout on gfx950: lane l holds A row l % 16 and B column l % 16,
 // 8 consecutive K values 8 (l / 16) .. +7 each; output lane l holds column
 // l % 16 of rows 4 (l / 16) + i).
-//   A  16 of the block's down rows (rows of different routed experts may
-//      share a tile), e2m1 converted to f16 with the chunk's power-of-two
-//      scale, which is exact (the plan scans every scale)
-//   B  h split into two f16 terms (hi = h rounded, lo = h - hi rounded:
-//      within 2^-22 |h|), written by the producing block as two planes;
-//      column 2 i + term holds routed slot i's term, so a B operand is one
-//      16-byte load and row rho's dot product is columns 2 i + 0, 2 i + 1 of
-//      its slot i summed
+//   A  16 of the block's down rows, e2m1 converted to f16 with the chunk's
+//      power-of-two scale, which is exact (the plan scans every scale)
+//   B  h as two f16 terms (hi = h rounded, lo = h - hi rounded: within
+//      2^-22 |h|) in columns 0 and 1; the other columns are zero
 // A K step of 128 = 4 lane groups x 32 takes one 16-byte MXFP4 chunk per
 // lane group: lane (m, g) converts dword j of its chunk for the step's j-th
 // MFMA, and B lane (n, g) supplies elements 8 j .. 8 j + 7 of the same chunk.
@@ -393,11 +622,6 @@ __device__ __forceinline__ float2 block_sum2(float a, float c, float *part) {
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-
-constexpr int kQ = 3;                  // 128-column K steps per wave (ffn <= 8 * kQ * 128)
-constexpr int kKPad = 8 * kQ * 128;    // largest padded ffn
-constexpr int kRTC = 3;                // down row tiles (k * rows per block <= 48)
-constexpr int kSD = kKPad / 32 + 1;    // LDS row stride (chunks) of the staged down rows
 
 __device__ __forceinline__ v8h fp4x8_f16(uint32_t w, float s) {
     const v2h a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0);
@@ -415,18 +639,17 @@ template <int K>
 __device__ __forceinline__ float dpp_shl(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + K, 0xF, 0xF, false));
 }
-__device__ __forceinline__ void st_dev16(rsrc_t r, uint32_t off, uint16_t v) {
-    __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kDev);
-}
 
-// The down rows [0, rows) of the block's slice (row rho = i * RC + j: slot i,
-// row j), staged in LDS at a stride of SD chunks, times h's two f16 planes
-// (hb: this lane's B operands, loaded by the caller), NT = ceil(rows / 16)
-// row tiles; row rho's partial (columns 2 i, 2 i + 1 summed) goes to
-// red[w * 48 + rho].
+// One wave's share of the down projection: the K steps q = kQ wave .. +kQ
+// (128 columns each) of the block's down rows [0, rows), staged in LDS at a
+// stride of SD chunks (sw; their f16 scales ss at a stride of CF), times the
+// wave's h terms hp
+// ([2][kQ * 128] f16: hi, lo of columns 128 kQ wave + ...), NT = ceil(rows /
+// 16) row tiles. Row rho's partial (the hi and lo columns summed) goes to
+// out[rho].
 template <int NT>
-__device__ __forceinline__ void dn_mfma_t(const uint8_t *sw, const uint16_t *ss, const v8h (*hb)[4], int SD, int CF,
-                                          int rows, int RC, float *red) {
+__device__ __forceinline__ void dn_mfma_grp(const uint8_t *sw, const uint16_t *ss, const _Float16 *hp, int SD, int CF,
+                                            int rows, float *out) {
     const int tt = opaque(threadIdx.x);
     const int lane = tt & 63, m = lane & 15, g = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(tt >> 6);
@@ -439,19 +662,23 @@ __device__ __forceinline__ void dn_mfma_t(const uint8_t *sw, const uint16_t *ss,
         const int q = kQ * wv + u;
         if (q >= NQC) break;
         const int c = min(4 * q + g, CF - 1);   // past F: B is zero
+        v8h hb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            hb[j] = m < 2 ? *(const v8h *)(hp + m * (kQ * 128) + 128 * u + 32 * g + 8 * j) : v8h{};
         mh_u4 qa[NT];
         float sc[NT];
 #pragma unroll
         for (int rt = 0; rt < NT; ++rt) {
-            const int o = min(16 * rt + m, rows - 1) * SD + c;
-            qa[rt] = *(const mh_u4 *)(sw + (size_t)o * 16);
-            sc[rt] = mh_f16(ss[o]);
+            const int row = min(16 * rt + m, rows - 1);
+            qa[rt] = *(const mh_u4 *)(sw + (size_t)(row * SD + c) * 16);
+            sc[rt] = mh_f16(ss[row * CF + c]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt)
-                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp4x8_f16(dword_of(qa[rt], j), sc[rt]), hb[u][j], acc[rt],
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp4x8_f16(dword_of(qa[rt], j), sc[rt]), hb[j], acc[rt],
                                                                  0, 0, 0);
     }
 #pragma unroll
@@ -461,206 +688,353 @@ __device__ __forceinline__ void dn_mfma_t(const uint8_t *sw, const uint16_t *ss,
             const float v = acc[rt][ii];
             const float v1 = dpp_shl<1>(v);
             const int rho = 16 * rt + 4 * g + ii;
-            if (rho < rows && m == 2 * (rho / RC)) red[wv * 48 + rho] = v + v1;
+            if (rho < rows && m == 0) out[rho] = v + v1;
         }
     }
 }
 
-template <int RDT, int XDT, bool MF>
-__global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
-    constexpr int XE = mh_chunk<XDT>::E;   // elements per expert chunk (32)
-    constexpr int RE = mh_chunk<RDT>::E;   // elements per router chunk (16 int8 / 4 f32)
+// ------------------------------------------------------- k_decode_grp
+
+template <int RDT>
+__global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
     // LDS is static (capacities are checked at plan creation).
     __shared__ float s_part[16];
-    __shared__ int s_sel[16];
-    __shared__ float s_w[16];
-    __shared__ int s_ok;
-    __shared__ __attribute__((aligned(16))) float s_xs[kHMax];       // x at layer start
-    // xb = rmsnorm(x) * w in 32-element groups padded to 33 floats: thread c
-    // reads group c element by element, and the padding puts the 64 lanes of
-    // a wave in 64 distinct LDS banks
+    __shared__ int s_sel[kMaxK];
+    __shared__ float s_w[kMaxK];
+    __shared__ __attribute__((aligned(16))) float s_xs[kHMax];
     __shared__ __attribute__((aligned(16))) float s_xbs[kHMax / 32 * 33];
-    __shared__ __attribute__((aligned(16))) float s_res[kResMax];    // reduced rows / staged logits
-    __shared__ __attribute__((aligned(16))) float s_red[kRedMax];    // partial sums
-    __shared__ __attribute__((aligned(16))) float s_bds[kThreads];   // [K][rows of this block's down slice]
-    // MFMA path: the block's down rows ([16 kRTC rows][kSD chunks]) and scales
-    __shared__ __attribute__((aligned(16))) uint8_t s_dw[MF ? 16 * kRTC * kSD * 16 : 16];
-    __shared__ uint16_t s_ds[MF ? 16 * kRTC * kSD : 2];
-    const int H = A.H, F = A.F, E = A.E, K = A.K;
-    float *xs = s_xs, *xbs = s_xbs, *res = s_res, *red = s_red, *bds = s_bds;
-    const int NB = gridDim.x, b = blockIdx.x, t = threadIdx.x;
-    const int wave = t >> 6;
-
-    // per-block phase timestamps (100 MHz), written by thread 0 while profiling
-    unsigned long long *tr = (A.trace && t == 0) ? A.trace + b : nullptr;
-#define MH_STAMP(ph) \
-    if (tr) tr[(size_t)(l * kStamps + (ph)) * NB] = wall_clock64()
-
-    const rsrc_t rx = make_rsrc(A.x, (uint32_t)H * 4u);
-    const rsrc_t rh = make_rsrc(A.h, (uint32_t)K * (uint32_t)F * 4u);
-    const uint32_t layer_bytes = (uint32_t)((uint64_t)E * A.stride - 1u) + 1u;   // < 4 GiB (plan check)
-    const int CR = H / RE;   // router chunks per row
-    RouterPref pf = prefetch_router<RDT>(A, 0);
-    const rsrc_t rh16 = make_rsrc(A.h16, (uint32_t)(2 * K * A.Fpad) * 2u);
-    for (int l = 0; l < A.n_layers; ++l) {
-        const StepLayer Ly = A.layers[l];
-        // sequence numbers of this layer: logits and routing record, the
-        // barrier before the down phase, x for the next layer
-        const unsigned tagA = A.seq0 + 3u * (unsigned)l, tagB = tagA + 1u, tagC = tagA + 2u;
-        MH_STAMP(0);
-        // ------------------------------------------------ A: router
+    __shared__ __attribute__((aligned(16))) float s_res[kResMax];
+    // the gate/up partial sums, then (once they are reduced) the down rows
+    __shared__ __attribute__((aligned(16))) uint8_t s_big[kGrpBig];
+    // the block's f16 scales: gate rows, up rows, down rows (3 windows)
+    __shared__ __attribute__((aligned(16))) uint8_t s_sc[3 * kScW];
+    __shared__ __attribute__((aligned(16))) _Float16 s_hp[kThreads / 64][2 * kQ * 128];
+    __shared__ float s_dred[kThreads / 64 * kRBMax];
+    __shared__ float s_bd[kRBMax];
+    __shared__ float s_y[kMaxGrpK * kRBMax];   // the combine's y_i rows, then x
+    const RouteArgs &R = A.R;
+    const int H = R.H, F = A.F, K = R.K;
+    const int b = blockIdx.x, t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63;
+    const int slot = b / A.G, gi = b - slot * A.G;
+    const int p0 = A.PB * gi, np = max(0, min(F - p0, A.PB));
+    const int r0 = A.RB * gi, nr = max(0, min(H - r0, A.RB));   // >= 1 (plan check)
+    const Stamper stamp{(R.trace && t == 0) ? R.trace + b : nullptr, (int)gridDim.x};
+    const RouteLds S{s_part, s_sel, s_w, s_xs, s_xbs};
+    const uint32_t layer_bytes = (uint32_t)((uint64_t)R.E * A.stride - 1u) + 1u;   // < 4 GiB (plan check)
+    uint64_t *xsrc = A.xw + (size_t)(b % kXR) * A.xws;
+    uint64_t *hsrc = A.hw + (size_t)((gi % kHR) * K + slot) * A.hws;
+    for (int l = 0; l < R.n_layers; ++l) {
+        const StepLayer Ly = R.layers[l];
+        // sequence numbers of this layer: logits, h, y, and x for the next layer
+        const unsigned tagL = A.seq0 + 4u * (unsigned)l, tagH = tagL + 1u, tagY = tagL + 2u, tagX = tagL + 3u;
+        stamp(l, 0);
         {
-            float xv[kNX];
-            if (l == 0) {
+            // the router row's loads are issued here and land while x is on
+            // its way (held across the layer they would cost 18 registers)
+            const RouterPref pf = prefetch_router<RDT>(R, l);
+            if (!route_layer<RDT>(R, pf, l, xsrc, tagL - 1u, tagL, S, stamp)) return;
+        }
+        stamp(l, 2);
+        const int e = s_sel[slot];   // block-uniform
+        // A slot with nothing routed (fewer than k logits above -1e30) takes
+        // its blocks out of the h exchange, the one wait that otherwise
+        // shows a block has read x; in such a layer every block raises a
+        // flag once it has routed, and x (l + 1) is published after all are
+        // up. (Every block ranks the same logits, so all agree on this.)
+        const bool unfilled = s_sel[K - 1] < 0;
+        if (unfilled && t == 0) __hip_atomic_store(&A.flags[b], tagY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float y = 0.f;               // row t of this slot's y (t < nr)
+        if (e >= 0) {
+            const rsrc_t rex = make_rsrc(Ly.experts, layer_bytes);
+            const uint32_t eo = (uint32_t)e * (uint32_t)A.stride;
+            const int tt = opaque(t);
+            // -------------------------------------- B: every load at once
+            // gate/up: thread (slot gs, chunk c) takes pairs pp = u ns + gs
+            // (whole rows per instruction: a wave reads 1 KB of contiguous
+            // row); past-the-end pairs and idle slots re-read the last pair
+            // and are masked out in the math
+            const int C = A.CH, ns = kThreads / C;
+            const int gs = tt / C, c = tt - gs * C;
+            const bool gact = gs < ns;
+            const int gsl = gact ? gs : ns - 1;
+            const int plast = max(np - 1, 0);
+            float xr[32];
 #pragma unroll
-                for (int k = 0; k < kNX; ++k) xv[k] = ld_dev(rx, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
-            } else {
-                // the previous layer's x, tagged tagA - 1: load all, re-poll the late ones
-                uint64_t wv[kNX];
-                const unsigned want = tagA - 1u;
-                const int tt = opaque(t);
+            for (int j = 0; j < 32; ++j) xr[j] = gact ? s_xbs[c * 33 + j] : 0.f;
+            // the scales first: the block's gate, up and down scale rows are
+            // three contiguous ranges, loaded as 16-byte chunks of their
+            // aligned windows (mis: the range's offset in its window)
+            const int CD = A.CF;
+            const uint32_t sa0 = eo + (uint32_t)A.off[1] + (uint32_t)(p0 * C) * 2u;
+            const uint32_t sa1 = eo + (uint32_t)A.off[4] + (uint32_t)(p0 * C) * 2u;
+            const uint32_t sa2 = eo + (uint32_t)A.off[7] + (uint32_t)(r0 * CD) * 2u;
+            const int mis0 = (int)(sa0 & 15u), mis1 = (int)(sa1 & 15u), mis2 = (int)(sa2 & 15u);
+            const int n0 = (mis0 + np * C * 2 + 15) >> 4, n1 = (mis1 + np * C * 2 + 15) >> 4;
+            const int n2 = (mis2 + nr * CD * 2 + 15) >> 4;
+            mh_u4 qs[kScLoads];
 #pragma unroll
-                for (int k = 0; k < kNX; ++k) {
-                    const int i = tt + k * kThreads;
-                    wv[k] = i < H ? ld_tag(A.xw + i) : (uint64_t)want << 32;
+            for (int k = 0; k < kScLoads; ++k) {
+                const int q = tt + kThreads * k;
+                const uint32_t a = q < n0 ? (sa0 & ~15u) + (uint32_t)q * 16u
+                                 : q < n0 + n1 ? (sa1 & ~15u) + (uint32_t)(q - n0) * 16u
+                                               : (sa2 & ~15u) + (uint32_t)min(q - n0 - n1, n2 - 1) * 16u;
+                qs[k] = ld_w16(rex, a);
+            }
+            mh_u4 qg[kUP], qu[kUP];
+            const uint32_t og = eo + (uint32_t)A.off[0], ou = eo + (uint32_t)A.off[3];
+#pragma unroll
+            for (int u = 0; u < kUP; ++u) {
+                const uint32_t rc = (uint32_t)((p0 + min(u * ns + gsl, plast)) * C + c);
+                qg[u] = ld_w16(rex, og + rc * 16u);
+                qu[u] = ld_w16(rex, ou + rc * 16u);
+            }
+            const uint32_t pb4 = (uint32_t)(p0 + min(t, plast)) * 4u;
+            const float bg = ld_f(rex, eo + (uint32_t)A.off[2] + pb4);
+            const float bu = ld_f(rex, eo + (uint32_t)A.off[5] + pb4);
+            __builtin_amdgcn_sched_barrier(0);
+            stamp(l, 9);
+            // the scale windows into LDS (their loads were issued first, so
+            // they complete first)
+#pragma unroll
+            for (int k = 0; k < kScLoads; ++k) {
+                const int q = tt + kThreads * k;
+                const int o = q < n0 ? q * 16 : q < n0 + n1 ? kScW + (q - n0) * 16 : 2 * kScW + (q - n0 - n1) * 16;
+                if (q < n0 + n1 + n2) *(mh_u4 *)(s_sc + o) = qs[k];
+            }
+            __syncthreads();
+            const uint16_t *scg = (const uint16_t *)(s_sc + mis0), *scu = (const uint16_t *)(s_sc + kScW + mis1);
+            // gate/up math as the data arrives (loads complete in issue
+            // order), each pair's math followed by one down-row load: a load
+            // whose issue waits for room in the memory pipeline then holds up
+            // no gate/up math whose data is in; the down rows are needed only
+            // after the h exchange. Down row j = u nsd + ds is thread (slot
+            // ds, chunk dc)'s (whole rows per instruction).
+            const int nsd = kThreads / CD;
+            const int ds = tt / CD, dc = tt - ds * CD;
+            const bool dact = ds < nsd;
+            const int dsl = dact ? ds : nsd - 1;
+            const uint32_t od = eo + (uint32_t)A.off[6];
+            mh_u4 qd[kUD];
+            float *red = (float *)s_big;
+#pragma unroll
+            for (int u = 0; u < kUP; ++u) {
+                const int pp = u * ns + gs;
+                const bool inr = gact && pp < np;
+                const int so = min(pp, plast) * C + c;
+                const float gv = mh_dot_mxfp4(qg[u], xr) * (inr ? mh_f16(scg[so]) : 0.f);
+                const float uv = mh_dot_mxfp4(qu[u], xr) * (inr ? mh_f16(scu[so]) : 0.f);
+                if (inr) {
+                    red[(2 * pp) * C + c] = gv;
+                    red[(2 * pp + 1) * C + c] = uv;
                 }
-                bool late = false;
-                for (unsigned spins = 0;; ++spins) {
-                    bool ready = true;
+                if (u < kUD) {
+                    const uint32_t rc = (uint32_t)((r0 + min(u * nsd + dsl, nr - 1)) * CD + dc);
+                    qd[u] = ld_w16(rex, od + rc * 16u);
+                }
+                if (u == 0) stamp(l, 19);
+                if (u == kUP / 2) stamp(l, 20);
+                __builtin_amdgcn_sched_barrier(0);   // one pair's math at a time
+            }
+            const float bdv = ld_f(rex, eo + (uint32_t)A.off[8] + (uint32_t)(r0 + min(t, nr - 1)) * 4u);
+            stamp(l, 10);
+            if (R.trace && t == kThreads - 64) R.trace[(size_t)(l * kStamps + 21) * gridDim.x + b] = wall_clock64();
+            __syncthreads();
+            stamp(l, 22);
+            block_reduce_rows(red, C, 2 * np, kThreads / 64, s_res, [](int) { return true; });
+            __syncthreads();
+            stamp(l, 11);
+            // epilogue (np <= 64: one pair per lane of wave 0): bias, clamped
+            // SwiGLU (engine/midge.c:531-538), h as two f16 terms, published
+            // in kHR copies for the slot's group
+            if (t < np) {
+                const float hv = act_fn(s_res[2 * t] + bg, s_res[2 * t + 1] + bu, A.alpha, A.limit, 0);
+                const _Float16 hi = (_Float16)hv;
+                const _Float16 lo = (_Float16)(hv - (float)hi);
+                const uint32_t pay = (uint32_t)__builtin_bit_cast(uint16_t, hi) |
+                                     ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
 #pragma unroll
-                    for (int k = 0; k < kNX; ++k) ready = ready && (unsigned)(wv[k] >> 32) == want;
-                    if (ready) break;
+                for (int cp = 0; cp < kHR; ++cp)
+                    st_tag_u(A.hw + (size_t)(cp * K + slot) * A.hws + p0 + t, tagH, pay);
+            }
+            stamp(l, 3);
+            // -------------------------------------- C: down
+            // this wave's part of h: its K steps read columns [kb, kb + 128 kQ)
+            const int kb = kQ * 128 * wave;
+            uint64_t hv[2 * kQ];
+#pragma unroll
+            for (int m2 = 0; m2 < 2 * kQ; ++m2) {
+                const int k = kb + lane + 64 * m2;
+                hv[m2] = k < F ? ld_tag(hsrc + k) : (uint64_t)tagH << 32;
+            }
+            // stage the down rows while h is on its way: row j of the slice at
+            // a stride of SD chunks (odd: the matrix-core lanes' 16 rows fall
+            // in distinct banks); s_big's partial sums are reduced already
+            const int SD = CD | 1;
+            if (dact) {
+#pragma unroll
+                for (int u = 0; u < kUD; ++u) {
+                    const int j = u * nsd + ds;
+                    if (j < nr) *(mh_u4 *)(s_big + (size_t)(j * SD + dc) * 16) = qd[u];
+                }
+            }
+            if (t < nr) s_bd[t] = bdv;
+            stamp(l, 4);
+            __syncthreads();   // the staged rows are visible to every wave
+            bool late = false;
+            for (unsigned spins = 0;; ++spins) {
+                bool ready = true;
+#pragma unroll
+                for (int m2 = 0; m2 < 2 * kQ; ++m2) ready = ready && tag_is(hv[m2], tagH);
+                if (ready) break;
+                if (spins > kSpinLimit) {
+                    late = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                for (int m2 = 0; m2 < 2 * kQ; ++m2) {
+                    const int k = kb + lane + 64 * m2;
+                    if (k < F && !tag_is(hv[m2], tagH)) hv[m2] = ld_tag(hsrc + k);
+                }
+            }
+            // the wave's h terms into its LDS planes (zeros past F); a wave's
+            // LDS accesses are performed in order, so its lanes read these
+            // after the writes without a block barrier
+            _Float16 *hp = s_hp[wave];
+#pragma unroll
+            for (int m2 = 0; m2 < 2 * kQ; ++m2) {
+                const uint32_t pv = (uint32_t)hv[m2];
+                hp[lane + 64 * m2] = __builtin_bit_cast(_Float16, (uint16_t)(pv & 0xFFFFu));
+                hp[kQ * 128 + lane + 64 * m2] = __builtin_bit_cast(_Float16, (uint16_t)(pv >> 16));
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (wave == 0) stamp(l, 5);
+            if (!late) {
+                const uint16_t *scd = (const uint16_t *)(s_sc + 2 * kScW + mis2);
+                switch ((nr + 15) >> 4) {   // block-uniform (plan check: nr <= 16 * 3)
+                case 1: dn_mfma_grp<1>(s_big, scd, hp, SD, CD, nr, s_dred + wave * kRBMax); break;
+                case 2: dn_mfma_grp<2>(s_big, scd, hp, SD, CD, nr, s_dred + wave * kRBMax); break;
+                case 3: dn_mfma_grp<3>(s_big, scd, hp, SD, CD, nr, s_dred + wave * kRBMax); break;
+                default: break;
+                }
+            }
+            if (wave == 0) stamp(l, 13);
+            if (__syncthreads_or(late)) {
+                if (t == 0) raise_err(R.err);
+                return;
+            }
+            if (t < nr) {
+                float sum = 0.f;
+#pragma unroll
+                for (int w = 0; w < kThreads / 64; ++w) sum += s_dred[w * kRBMax + t];
+                y = sum + s_bd[t];   // the matvec, then wk_addbias (engine/midge.c:539-541)
+            }
+        }
+        // y of slots 1.. goes to the slot-0 block of the same rows (a slot
+        // with nothing routed publishes 0, so that its rows are marked done)
+        if (slot > 0 && t < nr) st_tag(A.yw + (size_t)slot * H + r0 + t, tagY, y);
+        stamp(l, 14);
+        // -------------------------------------- D: combine (slot 0)
+        if (slot == 0) {
+            // thread (slot i >= 1, row j) polls y_i[j]; the values meet in LDS
+            bool late = false;
+            const int tq = opaque(t);
+            const int iq = 1 + tq / kRBMax, jq = tq - (iq - 1) * kRBMax;
+            if (iq < K && jq < nr) {
+                uint64_t *yp = A.yw + (size_t)iq * H + r0 + jq;
+                uint64_t yw = ld_tag(yp);
+                for (unsigned spins = 0; !tag_is(yw, tagY); ++spins) {
                     if (spins > kSpinLimit) {
                         late = true;
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-                    for (int k = 0; k < kNX; ++k) {
-                        const int i = tt + k * kThreads;
-                        if (i < H && (unsigned)(wv[k] >> 32) != want) wv[k] = ld_tag(A.xw + i);
+                    yw = ld_tag(yp);
+                }
+                s_y[iq * kRBMax + jq] = __uint_as_float((uint32_t)yw);
+            }
+            if (t < nr) s_y[t] = y;
+            if (__syncthreads_or(late)) {
+                if (t == 0) raise_err(R.err);
+                return;
+            }
+            // moe = sum_i w_i y_i in selection order, then x += moe, each
+            // product and sum rounded on its own (engine/midge.c:544-548)
+            if (t < nr) {
+#pragma clang fp contract(off)
+                float moe = 0.f;
+                for (int i = 0; i < K; ++i) {
+                    if (s_sel[i] < 0) continue;
+                    moe = moe + s_w[i] * s_y[i * kRBMax + t];
+                }
+                const float xn = s_xs[r0 + t] + moe;
+                if (l + 1 < R.n_layers) s_y[t] = xn;   // (slot 0's y is consumed)
+                else st_dev(R.x + r0 + t, xn);
+            }
+            if (unfilled && l + 1 < R.n_layers) {
+                if (t < 64) {
+                    for (unsigned spins = 0;; ++spins) {
+                        bool up = true;
+                        for (int i = t; i < (int)gridDim.x; i += 64)
+                            up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tagY;
+                        if (__all(up)) break;
+                        if (spins > kSpinLimit) {
+                            late = true;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
                     }
                 }
                 if (__syncthreads_or(late)) {
-                    if (t == 0) __hip_atomic_store(A.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    if (t == 0) raise_err(R.err);
                     return;
                 }
-#pragma unroll
-                for (int k = 0; k < kNX; ++k) xv[k] = __uint_as_float((uint32_t)wv[k]);
             }
-            MH_STAMP(15);
-            // the sum of squares and this block's logit in one pass: the
-            // row's dot with xb = x * inv * w is inv * (row . (x * w))
-            float ss = 0.f, dp = 0.f;
-#pragma unroll
-            for (int k = 0; k < kNX; ++k) {
-                ss = __builtin_fmaf(xv[k], xv[k], ss);
-                dp = __builtin_fmaf(router_weight<RDT>(pf.rw[k]), xv[k] * pf.nw[k], dp);
-            }
-            const float2 sums = block_sum2(ss, dp, s_part);
-            const float inv = 1.0f / sqrtf(sums.x / (float)H + A.eps);
-            if (b < E && t < kLR) {   // one copy per logit replica
-                float p = sums.y * inv;
-                if constexpr (RDT == MH_DT_Q8R) p *= pf.rs;
-                st_tag(A.lw + (size_t)t * A.lws + b, tagA, p + pf.rb);
-            }
-#pragma unroll
-            for (int k = 0; k < kNX; ++k) {
-                const int i = t + k * kThreads;
-                if (i < H) {
-                    xs[i] = xv[k];
-                    xbs[(i >> 5) * 33 + (i & 31)] = xv[k] * inv * pf.nw[k];
-                }
+            if (l + 1 < R.n_layers) {
+                __syncthreads();
+                // thread (copy cp, row j) publishes x[r0 + j] in copy cp
+                const int cp = tq / kRBMax, j = tq - cp * kRBMax;
+                if (cp < kXR && j < nr) st_tag(A.xw + (size_t)cp * A.xws + r0 + j, tagX, s_y[j]);
             }
         }
-        __syncthreads();
-        // router rows beyond the grid (more experts than blocks): over xb
-        for (int e = b + NB; e < E; e += NB) {
-            float p = 0.f;
-            const rsrc_t rw = make_rsrc(Ly.router_w, (uint32_t)E * (uint32_t)CR * 16u);
-            for (int c = t; c < CR; c += kThreads) {
-                const mh_u4 q = ld_w16(rw, (uint32_t)(e * CR + c) * 16u);
-                const int i0 = c * RE;   // a router chunk lies inside one 32-element group
-                p += mh_dot_chunk<RDT>(q, xbs + (i0 >> 5) * 33 + (i0 & 31));
-            }
-            p = block_sum(p, s_part);
-            if (t < kLR) {
-                if constexpr (RDT == MH_DT_Q8R) p *= Ly.router_s[e];
-                st_tag(A.lw + (size_t)t * A.lws + e, tagA, p + Ly.router_b[e]);
-            }
-        }
-        MH_STAMP(1);
+        stamp(l, 6);
+        stamp(l, 7);
+    }
+}
 
-        // ------------------------------------------------ route
-        {
-            // Every block routes: its first wave gathers the logits from
-            // replica b % kLR (kEL per lane: element lane + 64 j) and selects
-            // the stable top-k and the weights, so no routing record has to
-            // be broadcast; all blocks reach the same selection from the same
-            // words. (One copy polled by every block congests its lines: 32
-            // pollers per copy do not.) The block's other waves wait at the
-            // barrier below.
-            bool late = false;
-            if (wave == 0) {
-                const int lane = t;
-                const int tt = opaque(t);
-                uint64_t *lr = A.lw + (size_t)(b % kLR) * A.lws;
-                uint64_t wv[kEL];
-#pragma unroll
-                for (int j = 0; j < kEL; ++j) {
-                    const int e = tt + 64 * j;
-                    wv[j] = e < E ? ld_tag(lr + e) : (uint64_t)tagA << 32;
-                }
-                for (unsigned spins = 0;; ++spins) {
-                    bool ready = true;
-#pragma unroll
-                    for (int j = 0; j < kEL; ++j) ready = ready && (unsigned)(wv[j] >> 32) == tagA;
-                    if (__all(ready)) break;
-                    if (spins > kSpinLimit) {
-                        late = true;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-                    for (int j = 0; j < kEL; ++j) {
-                        const int e = tt + 64 * j;
-                        if (e < E && (unsigned)(wv[j] >> 32) != tagA) wv[j] = ld_tag(lr + e);
-                    }
-                }
-                MH_STAMP(16);
-                float v[kEL], v0[kEL];
-#pragma unroll
-                for (int j = 0; j < kEL; ++j) {
-                    v[j] = lane + 64 * j < E ? __uint_as_float((uint32_t)wv[j]) : -INFINITY;
-                    v0[j] = v[j];
-                }
-                int my_sel;
-                float my_val;
-                wave_topk(v, K, &my_sel, &my_val);
-                MH_STAMP(17);
-                const float my_w = wave_weight(v0, K, A.router_norm, my_val);
-                MH_STAMP(18);
-                if (lane < K) {
-                    // (addresses from an opaque lane: recomputed here, not
-                    // hoisted out of the layer loop and spilled)
-                    const int ln = opaque(lane);
-                    s_sel[ln] = my_sel;
-                    s_w[ln] = my_w;
-                    if (b == 0) {
-                        if (A.sel) A.sel[(size_t)l * K + ln] = my_sel;
-                        if (A.w) A.w[(size_t)l * K + ln] = my_w;
-                        if (A.usage && my_sel >= 0)
-                            __hip_atomic_fetch_add(&A.usage[(size_t)l * E + my_sel], 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
-            }
-            if (__syncthreads_or(late)) {
-                if (t == 0) __hip_atomic_store(A.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                return;
-            }
-        }
-        MH_STAMP(2);
+// ------------------------------------------------------ k_decode_step
+
+template <int RDT, int XDT>
+__global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
+    constexpr int XE = mh_chunk<XDT>::E;   // elements per expert chunk (32)
+    // LDS is static (capacities are checked at plan creation).
+    __shared__ float s_part[16];
+    __shared__ int s_sel[kMaxK];
+    __shared__ float s_w[kMaxK];
+    __shared__ int s_ok;
+    __shared__ __attribute__((aligned(16))) float s_xs[kHMax];
+    __shared__ __attribute__((aligned(16))) float s_xbs[kHMax / 32 * 33];
+    __shared__ __attribute__((aligned(16))) float s_res[kResMax];    // reduced rows
+    __shared__ __attribute__((aligned(16))) float s_red[kRedMax];    // partial sums
+    __shared__ __attribute__((aligned(16))) float s_bds[kThreads];   // [K][rows of this block's down slice]
+    const RouteArgs &R = A.R;
+    const int H = R.H, F = A.F, K = R.K;
+    float *res = s_res, *red = s_red, *bds = s_bds;
+    const int NB = gridDim.x, b = blockIdx.x, t = threadIdx.x;
+    const Stamper stamp{(R.trace && t == 0) ? R.trace + b : nullptr, NB};
+    const RouteLds S{s_part, s_sel, s_w, s_xs, s_xbs};
+    const rsrc_t rh = make_rsrc(A.h, (uint32_t)K * (uint32_t)F * 4u);
+    const uint32_t layer_bytes = (uint32_t)((uint64_t)R.E * A.stride - 1u) + 1u;   // < 4 GiB (plan check)
+    RouterPref pf = prefetch_router<RDT>(R, 0);
+    for (int l = 0; l < R.n_layers; ++l) {
+        const StepLayer Ly = R.layers[l];
+        // sequence numbers of this layer: logits, the barrier before the down
+        // phase, x for the next layer
+        const unsigned tagA = A.seq0 + 3u * (unsigned)l, tagB = tagA + 1u, tagC = tagA + 2u;
+        stamp(l, 0);
+        if (!route_layer<RDT>(R, pf, l, A.xw, tagA - 1u, tagA, S, stamp)) return;
+        stamp(l, 2);
 
         // ------------------------------------------------ B: gate/up
         const rsrc_t rex = make_rsrc(Ly.experts, layer_bytes);
@@ -688,7 +1062,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             const uint32_t os0 = (uint32_t)A.off[1], os1 = (uint32_t)A.off[4];
             float xr[XE];
 #pragma unroll
-            for (int j = 0; j < XE; ++j) xr[j] = active ? xbs[c * 33 + j] : 0.f;
+            for (int j = 0; j < XE; ++j) xr[j] = active ? s_xbs[c * 33 + j] : 0.f;
             // One pass (plan check: np <= ns * kUP). Branch-free loads: a
             // past-the-end pair or an idle slot re-reads the block's last pair
             // and is masked out in the math; scale bits stay raw until every
@@ -719,7 +1093,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 bu_pref = ld_f(rex, eo + (uint32_t)A.off[5] + r4);
             }
             __builtin_amdgcn_sched_barrier(0);   // all loads issued before any math
-            MH_STAMP(9);
+            stamp(l, 9);
 #pragma unroll
             for (int u = 0; u < kUP; ++u) {
                 const int pp = u * ns + slot;
@@ -733,8 +1107,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 }
                 __builtin_amdgcn_sched_barrier(0);   // one pair's math at a time
             }
-            MH_STAMP(10);
-            if constexpr (!MF) {
+            stamp(l, 10);
+            {
                 // the gate/up weight registers are free: start the down slice
                 // now, so it streams in during the reduction, the epilogue and
                 // the barrier (branch-free: out-of-range rows re-read row 0 of
@@ -768,146 +1142,22 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             __syncthreads();
             block_reduce_rows(red, C, 2 * np, kThreads / 64, res, [](int) { return true; });
             __syncthreads();
-            MH_STAMP(11);
-            if constexpr (MF) {
-                if (wave == 0) {
-                    // epilogue (np <= 64: one pair per lane): h as two f16
-                    // planes, hi = h rounded, lo = (h - hi) rounded; then
-                    // arrive as soon as this wave's stores are complete
-                    if (t < np) {
-#pragma clang fp contract(off)
-                        const int pr = rb + t;
-                        const bool second = pr >= F;
-                        const int e = second ? e_b : e_a;
-                        float hv = 0.f;
-                        if (e >= 0)
-                            hv = act_fn(res[2 * t] + bg_pref, res[2 * t + 1] + bu_pref, A.alpha, A.limit, A.act_plain);
-                        const _Float16 hi = (_Float16)hv;
-                        const _Float16 lo = (_Float16)(hv - (float)hi);
-                        const uint32_t o = (uint32_t)((second ? ia + 1 : ia) * A.Fpad + (second ? pr - F : pr));
-                        st_dev16(rh16, o * 2u, __builtin_bit_cast(uint16_t, hi));
-                        st_dev16(rh16, ((uint32_t)(K * A.Fpad) + o) * 2u, __builtin_bit_cast(uint16_t, lo));
-                    }
-                    __builtin_amdgcn_s_waitcnt(0);
-                    if (t == 0)
-                        __hip_atomic_store(&A.flags[b], tagB, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else {
-                    // waves 1.. load the block's down rows (whole rows per
-                    // instruction: thread (slot, chunk)) while the barrier
-                    // completes, then stage them in LDS as row rho = i * RC + j
-                    // at a stride of SD chunks (odd: the MFMA lanes' 16 rows
-                    // fall in distinct banks)
-                    const int CD = A.CF, SD = CD | 1, nsC = (kThreads - 64) / CD, spe = nsC / K;
-                    const int RC = (H + NB - 1) / NB, r_begin = b * RC;
-                    const int nr = max(0, min(H, r_begin + RC) - r_begin);
-                    if (nr > 0) {
-                        const int td = opaque(t) - 64;
-                        const int dslot = td / CD, dc = td - dslot * CD;
-                        const int di = dslot / spe, dsub = dslot - di * spe;
-                        const int de = di < K ? s_sel[di] : -1;
-                        const int ea = de >= 0 ? de : max(s_sel[0], 0);
-                        const uint32_t eo = (uint32_t)ea * (uint32_t)A.stride;
-#pragma unroll
-                        for (int u = 0; u < kUC; ++u) {
-                            const uint32_t rc = (uint32_t)((r_begin + min(dsub + spe * u, nr - 1)) * CD + dc);
-                            qd[u] = ld_w16(rex, eo + (uint32_t)A.off[6] + rc * 16u);
-                            sd[u] = ld_w2(rex, eo + (uint32_t)A.off[7] + rc * 2u);
-                        }
-                        // the down biases: (expert ib, row jb) -> thread 64 + ib * nr + jb
-                        const int tb = min(td, K * nr - 1);
-                        const int ib = tb / nr, jb = tb - ib * nr;
-                        const int eb = s_sel[ib];
-                        const float bdv = ld_f(rex, (uint32_t)max(eb, 0) * (uint32_t)A.stride + (uint32_t)A.off[8] +
-                                                        (uint32_t)(r_begin + jb) * 4u);
-                        if (di < K) {
-#pragma unroll
-                            for (int u = 0; u < kUC; ++u) {
-                                const int j = dsub + spe * u;
-                                if (j < nr) {
-                                    const int o = (di * RC + j) * SD + dc;
-                                    *(mh_u4 *)(s_dw + (size_t)o * 16) = qd[u];
-                                    s_ds[o] = (uint16_t)sd[u];
-                                }
-                            }
-                        }
-                        if (td < K * nr) bds[td] = eb >= 0 ? bdv : 0.f;
-                    }
-                }
-            } else {
-                // epilogue: pair t -> h (np <= F <= kThreads pairs: one per thread)
-                if (t < np) {
-                    const int pr = rb + t;
-                    const bool second = pr >= F;
-                    const int e = second ? e_b : e_a;
-                    float hv = 0.f;
-                    if (e >= 0) hv = act_fn(res[2 * t] + bg_pref, res[2 * t + 1] + bu_pref, A.alpha, A.limit, A.act_plain);
-                    st_dev(A.h + (size_t)(second ? ia + 1 : ia) * F + (second ? pr - F : pr), hv);
-                }
+            stamp(l, 11);
+            // epilogue: pair t -> h (np <= F <= kThreads pairs: one per thread)
+            if (t < np) {
+                const int pr = rb + t;
+                const bool second = pr >= F;
+                const int e = second ? e_b : e_a;
+                float hv = 0.f;
+                if (e >= 0) hv = act_fn(res[2 * t] + bg_pref, res[2 * t + 1] + bu_pref, A.alpha, A.limit, A.act_plain);
+                st_dev(A.h + (size_t)(second ? ia + 1 : ia) * F + (second ? pr - F : pr), hv);
             }
         }
-        MH_STAMP(3);
-        if constexpr (!MF) bar_arrive(A.flags, tagB);
+        stamp(l, 3);
+        bar_arrive(A.flags, tagB);
 
         // ------------------------------------------------ C: down + combine
-        if constexpr (MF) {
-            const int CF = A.CF, NQC = (CF + 3) >> 2;
-            const int RC = (H + NB - 1) / NB, r_begin = b * RC;
-            const int nr = max(0, min(H, r_begin + RC) - r_begin);
-            const int rowsC = K * RC;
-            // a block without output rows reads no h (the next layer's
-            // producers may overwrite it as soon as every x row is in)
-            if (nr > 0 || b == 0) {
-                MH_STAMP(4);
-                if (!bar_wait(A.flags, A.go, tagB, A.err, &s_ok)) return;
-                MH_STAMP(5);
-                const int tt = opaque(t);
-                const int lane = tt & 63, m = lane & 15, g = lane >> 4;
-                const int wv = __builtin_amdgcn_readfirstlane(tt >> 6);
-                // B: column m = 2 i + term reads 8 values of plane (m & 1),
-                // slot i = m / 2
-                // (lanes of unused columns and K steps past the end read
-                // past the buffer, which returns zeros: no branch)
-                v8h hb[kQ][4];
-#pragma unroll
-                for (int u = 0; u < kQ; ++u) {
-                    const int q = kQ * wv + u;
-                    const bool use = q < NQC && m < 2 * K;
-                    const uint32_t e16 = (uint32_t)(((m & 1) * K + (m >> 1)) * A.Fpad + 128 * q + 32 * g);
-                    const uint32_t o = use ? e16 * 2u : 0x80000000u;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) hb[u][j] = __builtin_bit_cast(v8h, ld_dev16(rh16, o + 16u * j));
-                }
-                MH_STAMP(12);
-                switch ((rowsC + 15) >> 4) {   // block-uniform (plan check: rows <= 16 kRTC)
-                case 1: dn_mfma_t<1>(s_dw, s_ds, hb, CF | 1, CF, rowsC, RC, red); break;
-                case 2: dn_mfma_t<2>(s_dw, s_ds, hb, CF | 1, CF, rowsC, RC, red); break;
-                case 3: dn_mfma_t<3>(s_dw, s_ds, hb, CF | 1, CF, rowsC, RC, red); break;
-                default: break;
-                }
-                MH_STAMP(13);
-                __syncthreads();
-                if (t < rowsC) {
-                    float sum = 0.f;
-#pragma unroll
-                    for (int w = 0; w < kThreads / 64; ++w) sum += red[w * 48 + t];
-                    res[t] = sum;
-                }
-                __syncthreads();
-                MH_STAMP(14);
-                for (int j = t; j < nr; j += kThreads) {
-#pragma clang fp contract(off)
-                    const int r = r_begin + j;
-                    float moe = 0.f;
-                    for (int ii = 0; ii < K; ++ii) {
-                        if (s_sel[ii] < 0) continue;
-                        const float y = res[ii * RC + j] + bds[ii * nr + j];
-                        moe = moe + s_w[ii] * y;
-                    }
-                    if (l + 1 < A.n_layers) st_tag(A.xw + r, tagC, xs[r] + moe);
-                    else st_dev(A.x + r, xs[r] + moe);
-                }
-            }
-        } else {
+        {
             // one pass (plan check): slot -> (expert i, row phase sub), rows
             // j = sub + spe * u of this block's slice
             const int C = A.CF;
@@ -922,9 +1172,9 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
             const bool act = i < K;
             const int e = act ? s_sel[i] : -1;
             __builtin_amdgcn_sched_barrier(0);
-            MH_STAMP(4);
-            if (!bar_wait(A.flags, A.go, tagB, A.err, &s_ok)) return;
-            MH_STAMP(5);
+            stamp(l, 4);
+            if (!bar_wait(A.flags, A.go, tagB, R.err, &s_ok)) return;
+            stamp(l, 5);
             float xr[XE];
             {
                 const uint32_t hb = (uint32_t)((act ? i : 0) * F + c * XE) * 4u;
@@ -937,7 +1187,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                     xr[4 * jj + 3] = act ? __uint_as_float(v.w) : 0.f;
                 }
             }
-            MH_STAMP(12);
+            stamp(l, 12);
 #pragma unroll
             for (int u = 0; u < kUC; ++u) {
                 const int j = sub + spe * u;
@@ -947,11 +1197,11 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (t < K * nr) bds[t] = bd_pref;
-            MH_STAMP(13);
+            stamp(l, 13);
             __syncthreads();
             block_reduce_rows(red, C, K * RC, kThreads / 64, res, [&](int it) { return it % RC < nr; });
             __syncthreads();
-            MH_STAMP(14);
+            stamp(l, 14);
             // combine in selection order: moe = sum_i w_i (dot_i + bd_i); x += moe
             for (int j = t; j < nr; j += kThreads) {
 #pragma clang fp contract(off)
@@ -962,15 +1212,14 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
                     const float y = res[ii * RC + j] + bds[ii * nr + j];
                     moe = moe + s_w[ii] * y;
                 }
-                if (l + 1 < A.n_layers) st_tag(A.xw + r, tagC, xs[r] + moe);
-                else st_dev(A.x + r, xs[r] + moe);
+                if (l + 1 < R.n_layers) st_tag(A.xw + r, tagC, s_xs[r] + moe);
+                else st_dev(R.x + r, s_xs[r] + moe);
             }
         }
-        MH_STAMP(6);
-        if (l + 1 < A.n_layers) pf = prefetch_router<RDT>(A, l + 1);
-        MH_STAMP(7);
+        stamp(l, 6);
+        if (l + 1 < R.n_layers) pf = prefetch_router<RDT>(R, l + 1);
+        stamp(l, 7);
     }
-#undef MH_STAMP
 }
 
 __global__ void k_fill_u32(unsigned *p, int n, unsigned v) {
@@ -990,40 +1239,47 @@ __global__ void k_scan_scales(const uint8_t *experts, uint64_t stride, uint64_t 
     if (!ok) atomicOr(bad, 1u);
 }
 
-template <int RDT, int XDT, bool MF>
-int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
-    auto k = k_decode_step<RDT, XDT, MF>;
-    // the LDS attribute and the occupancy query once per device and
-    // instantiation (both cost host time comparable to a small step)
-    static int ready_dev = -1, per_cu = 0;
-    static size_t ready_lds = 0;
+// Launch of a one-launch step: nb blocks of kThreads. Every block must be
+// resident at once (the blocks wait on each other): the plan sizes the grid
+// to at most one block per CU, and the occupancy is checked here (the query
+// once per device and kernel: it costs host time comparable to a small
+// step). A plain launch is the default; MIDGE_HIP_COOP=1 makes it a
+// cooperative launch, whose runtime check of co-residency costs ~18 us of
+// device time per call. A block that were not resident would make the grid's
+// bounded waits time out and report an error through mh_sync, never hang.
+template <class Args>
+int launch_step(const void *k, const Args &A, int nb, hipStream_t s, int *ready_dev, int *per_cu) {
     int dev = 0;
     MH_HIP(hipGetDevice(&dev));
-    if (dev != ready_dev || lds != ready_lds) {
-        MH_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        MH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, lds));
-        ready_dev = dev;
-        ready_lds = lds;
+    if (dev != *ready_dev) {
+        MH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k, kThreads, 0));
+        *ready_dev = dev;
     }
-    if (per_cu < 1) return fail(MH_E_UNSUPPORTED, "decode step: a %d-thread block with %zu B LDS does not fit a CU", kThreads, lds);
-    StepArgs a = A;
+    if (*per_cu < 1) return fail(MH_E_UNSUPPORTED, "decode step: a %d-thread block does not fit a CU", kThreads);
+    Args a = A;
     void *args[] = {&a};
     const bool prof = profiling();
     if (prof) prof_begin("decode_step", s);
-    // One block per CU with the occupancy checked above: every block is
-    // resident at once. The cooperative launch makes the runtime verify that
-    // too; MIDGE_HIP_COOP=0 selects a plain launch of the same grid (for
-    // tools that do not handle cooperative dispatches). A block that were
-    // not resident would make the grid's bounded waits time out and report
-    // an error through mh_sync, never hang.
     const char *coop = getenv("MIDGE_HIP_COOP");
     hipError_t e;
-    if (coop && coop[0] == '0')
-        e = hipLaunchKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s);
+    if (coop && coop[0] == '1')
+        e = hipLaunchCooperativeKernel(k, dim3(nb), dim3(kThreads), args, 0u, s);
     else
-        e = hipLaunchCooperativeKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s);
+        e = hipLaunchKernel(k, dim3(nb), dim3(kThreads), args, 0u, s);
     if (prof) prof_end(s);
-    return hip_check(e, "decode step cooperative launch");
+    return hip_check(e, "decode step launch");
+}
+
+template <int RDT>
+int launch_grp(const GrpArgs &A, int nb, hipStream_t s) {
+    static int ready_dev = -1, per_cu = 0;
+    return launch_step((const void *)k_decode_grp<RDT>, A, nb, s, &ready_dev, &per_cu);
+}
+
+template <int RDT, int XDT>
+int launch_flat(const StepArgs &A, int nb, hipStream_t s) {
+    static int ready_dev = -1, per_cu = 0;
+    return launch_step((const void *)k_decode_step<RDT, XDT>, A, nb, s, &ready_dev, &per_cu);
 }
 
 }  // namespace
@@ -1032,26 +1288,92 @@ int launch_t(const StepArgs &A, int nb, size_t lds, hipStream_t s) {
 // words kGoStride apart.
 static int go_offset(int nb) { return (nb + 63) / 32 * 32; }
 static int flag_words(int nb) { return go_offset(nb) + kGoCopies * kGoStride; }
+// Words between copies of an exchanged vector of n words: rounded up to 16
+// words, plus 32 (copies start 256 B past a line boundary apart).
+static int copy_stride(int n) { return (n + 15) / 16 * 16 + 32; }
 
-// Scratch and tables a stack keeps for the one-launch path.
+// Scratch and tables a stack keeps for the one-launch paths.
 struct StepPlan {
     StepLayer *layers = nullptr;   // device [L]
     unsigned *flags = nullptr;     // device [flag_words(nb)]: flags, then the release word's copies
-    uint64_t *tagged = nullptr;    // device: logit copies [kLR][lws] | x [H], tagged words
+    uint64_t *tagged = nullptr;    // device: exchanged words (tag_layout)
     size_t tagged_words = 0;
-    unsigned long long *trace = nullptr;   // device [L][16][nb] (filled while profiling)
+    unsigned long long *trace = nullptr;   // device [L][kStamps][nb] (filled while profiling)
     int n_layers = 0;
-    unsigned *err = nullptr;       // host-mapped pinned [1]: set by a timed-out barrier
+    unsigned *err = nullptr;       // host-mapped pinned [1]: set by a timed-out wait
     unsigned *err_dev = nullptr;   // its device address
-    float *h = nullptr;            // device [K][F]
-    uint16_t *h16 = nullptr;       // device [2][K][Fpad]
-    int Fpad = 0;
-    int mf = 0;                    // 1 = the MFMA path may run the expert GEMVs
-    unsigned seq = 0;              // next barrier sequence number
-    int nb = 0;
-    int ok = 0;                    // 1 = eligible, 0 = not (reason recorded)
+    float *h = nullptr;            // device [K][F] (k_decode_step)
+    unsigned seq = 0;              // next sequence number
+    int nb = 0;                    // CUs: k_decode_step's grid
+    int flat = 0;                  // 1 = k_decode_step can run the stack
+    int grp = 0;                   // 1 = k_decode_grp can run the stack
+    int G = 0, PB = 0, RB = 0;     // k_decode_grp's shape (grid G * K)
+    int ok = 0;                    // 1 = one of the kernels is eligible
     char why[160] = {0};
+    std::vector<std::pair<void *, uint64_t>> mem;   // device allocations (counted)
 };
+
+template <class T>
+static int plan_alloc(StepPlan *p, T **out, uint64_t bytes, const char *what) {
+    void *v = nullptr;
+    MH_TRY(dev_alloc(&v, bytes, what));
+    p->mem.push_back({v, bytes});
+    *out = (T *)v;
+    return MH_OK;
+}
+
+// Frees a plan's device and pinned memory; the plan stays ineligible. Called
+// by step_plan_destroy, and by mh_shutdown for plans still alive.
+static void plan_release(void *key) {
+    StepPlan *p = (StepPlan *)key;
+    for (auto &m : p->mem) dev_release(m.first, m.second);
+    p->mem.clear();
+    p->layers = nullptr;
+    p->flags = nullptr;
+    p->trace = nullptr;
+    p->tagged = nullptr;
+    p->h = nullptr;
+    if (p->err) {
+        unwatch_async_error(p->err);
+        (void)hipHostFree(p->err);
+    }
+    p->err = p->err_dev = nullptr;
+    p->flat = p->grp = p->ok = 0;
+}
+
+// Exchange-word layout in StepPlan::tagged: the logits' kLR copies, x's kXR
+// copies, h's kHR x K planes, y's K rows (offsets in words).
+struct TagLayout {
+    int lws, xws, hws;
+    size_t lw, xw, hw, yw, total;
+};
+static TagLayout tag_layout(const DevLayer &L0) {
+    TagLayout t;
+    t.lws = copy_stride(L0.n_experts);
+    t.xws = copy_stride((int)L0.hidden);
+    t.hws = copy_stride((int)L0.ffn);
+    t.lw = 0;
+    t.xw = t.lw + (size_t)kLR * t.lws;
+    t.hw = t.xw + (size_t)kXR * t.xws;
+    t.yw = t.hw + (size_t)kHR * L0.top_k * t.hws;
+    t.total = t.yw + (size_t)L0.top_k * L0.hidden;
+    return t;
+}
+
+// k_decode_grp's grid for a shape: the largest G <= cus / K for which every
+// block of a group owns at least one gate/up pair and one down row.
+static bool grp_shape(int cus, int H, int F, int K, int *G, int *PB, int *RB) {
+    for (int g = cus / K; g >= 1; --g) {
+        const int pb = (F + g - 1) / g, rb = (H + g - 1) / g;
+        if ((g - 1) * pb < F && (g - 1) * rb < H) {
+            *G = g;
+            *PB = pb;
+            *RB = rb;
+            return true;
+        }
+    }
+    return false;
+}
 
 int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     StepPlan *p = new StepPlan();
@@ -1065,7 +1387,7 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     if (L0.expert_dt != MH_DT_MXFP4 && L0.expert_dt != MH_DT_Q4G32) return reject("experts are not 4-bit g32");
     if (L0.hidden % 32 || L0.ffn % 32 || L0.hidden / 32 > kThreads || L0.ffn / 32 > kThreads)
         return reject("hidden/ffn not multiples of 32 or too wide");
-    if (L0.n_experts > 64 * kEL || L0.top_k > 16) return reject("too many experts");
+    if (L0.n_experts > 64 * kEL || L0.top_k > kMaxK) return reject("too many experts");
     if (L0.expert_stride * (uint64_t)L0.n_experts >= (1ull << 32)) return reject("a layer's experts exceed 4 GiB");
     for (int l = 0; l < n_layers; l++) {
         const DevLayer &L = layers[l];
@@ -1079,56 +1401,66 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     const int re = L0.router.dt == MH_DT_Q8R ? 16 : 4;
     if (L0.hidden % re) return reject("router width not a chunk multiple");
     const int nb = device_cus();
+    const int H = (int)L0.hidden, F = (int)L0.ffn, K = L0.top_k;
+    if (H > kNX * kThreads || H > kHMax) return reject("hidden exceeds the router phase's per-thread share");
     {
-        const int H = (int)L0.hidden, F = (int)L0.ffn, K = L0.top_k;
-        if (H > kNX * kThreads) return reject("hidden exceeds the router phase's per-thread share");
-        // gate/up: a block's pairs span at most two experts and the epilogue
-        // has one pair per thread
+        // k_decode_step: a block's gate/up pairs span at most two experts and
+        // the epilogue has one pair per thread; the down phase is one pass in
+        // which every routed expert gets slots, each slot's rows of the
+        // block's slice fit kUC iterations, one bias per thread
         const int PB = (K * F + nb - 1) / nb;
-        if (PB > F || PB > kThreads) return reject("a block's gate/up pairs span more than two experts");
-        if (PB > (kThreads / (H / 32)) * kUP) return reject("gate/up does not fit one pass");
-        // down: one pass, every routed expert gets slots, each slot's rows of
-        // the block's slice fit kUC iterations, one bias per thread
         const int nsC = kThreads / (F / 32);
         const int spe = K > 0 ? nsC / K : 0;
         const int RC = (H + nb - 1) / nb;
-        if (spe < 1 || RC > spe * kUC || K * RC > kThreads) return reject("down phase does not fit one pass");
+        const int res = std::max(64 * kEL, std::max(2 * PB, K * RC)) + 64;
+        const int red = std::max(2 * (kThreads / (H / 32)) * kUP * (H / 32), K * RC * (F / 32));
+        p->flat = PB <= F && PB <= kThreads && PB <= (kThreads / (H / 32)) * kUP && spe >= 1 && RC <= spe * kUC &&
+                  K * RC <= kThreads && res <= kResMax && red <= kRedMax;
     }
-    // MFMA down path: MXFP4 experts, the clamped SwiGLU (|h| <= limit (limit +
-    // 1) fits f16), shapes within the tiles, exact f16 scales (scanned below)
     {
-        const int H = (int)L0.hidden, F = (int)L0.ffn, K = L0.top_k;
-        const int RC = (H + nb - 1) / nb, PB = (K * F + nb - 1) / nb;
-        const int spe = K > 0 ? (kThreads - 64) / (F / 32) / K : 0;   // down rows in flight: waves 1..
+        // k_decode_grp: MXFP4 experts, the clamped SwiGLU (|h| <= limit (limit
+        // + 1) fits f16), every block's pairs in one pass and its rows in the
+        // matrix-core tiles, exact f16 down scales (scanned below)
         const float lim = L0.limit;
-        p->mf = L0.expert_dt == MH_DT_MXFP4 && !L0.act_plain && lim >= 0.f && lim * (lim + 1.f) < 60000.f &&
-                F <= kKPad && K * RC <= 16 * kRTC && 2 * K <= 16 && PB <= 64 && spe >= 1 && RC <= spe * kUC &&
-                K * RC <= kThreads - 64;
+        int G = 0, PB = 0, RB = 0;
+        bool ok = L0.expert_dt == MH_DT_MXFP4 && !L0.act_plain && lim >= 0.f && lim * (lim + 1.f) < 60000.f &&
+                  F <= kKPad && K <= kMaxGrpK && grp_shape(nb, H, F, K, &G, &PB, &RB);
+        if (ok) {
+            const int CH = H / 32, CF = F / 32;
+            ok = PB <= (kThreads / CH) * kUP && PB <= 64 && 2 * PB <= kResMax - 64 && 2 * PB * CH <= kRedMax &&
+                 RB <= (kThreads / CF) * kUD && RB <= kRBMax && RB * (CF | 1) <= kRBMax * kSDMax &&
+                 PB * CH * 2 + 16 <= kScW && RB * CF * 2 + 16 <= kScW &&
+                 2 * ((PB * CH * 2 + 30) / 16) + (RB * CF * 2 + 30) / 16 <= kScLoads * kThreads;
+        }
+        p->grp = ok ? 1 : 0;
+        p->G = G;
+        p->PB = PB;
+        p->RB = RB;
     }
+    if (!p->flat && !p->grp) return reject("no one-launch kernel fits the shape");
     std::vector<StepLayer> host((size_t)n_layers);
     for (int l = 0; l < n_layers; l++) {
         const DevLayer &L = layers[l];
         host[(size_t)l] = StepLayer{L.experts, L.router.data, (const float *)L.router.scales, L.router_b, L.mlp_norm};
     }
-    MH_HIP(hipMalloc(&p->layers, sizeof(StepLayer) * (size_t)n_layers));
+    register_owner(p, plan_release);
+    MH_TRY(plan_alloc(p, &p->layers, sizeof(StepLayer) * (size_t)n_layers, "decode plan layers"));
     MH_HIP(hipMemcpy(p->layers, host.data(), sizeof(StepLayer) * (size_t)n_layers, hipMemcpyHostToDevice));
-    MH_HIP(hipMalloc(&p->flags, sizeof(unsigned) * (size_t)flag_words(nb)));
-    MH_HIP(hipMalloc(&p->trace, sizeof(unsigned long long) * kStamps * (size_t)n_layers * (size_t)nb));
+    MH_TRY(plan_alloc(p, &p->flags, sizeof(unsigned) * (size_t)flag_words(nb), "decode plan flags"));
+    MH_TRY(plan_alloc(p, &p->trace, sizeof(unsigned long long) * kStamps * (size_t)n_layers * (size_t)nb,
+                      "decode plan stamps"));
     p->n_layers = n_layers;
     MH_HIP(hipHostMalloc((void **)&p->err, sizeof(unsigned), hipHostMallocMapped));
     *p->err = 0;
     MH_HIP(hipHostGetDevicePointer((void **)&p->err_dev, p->err, 0));
-    watch_async_error(p->err, "decode step: a grid barrier timed out (blocks not co-resident)");
-    p->tagged_words = (size_t)kLR * ((L0.n_experts + 15) / 16 * 16 + 32) + (size_t)L0.hidden;
-    MH_HIP(hipMalloc(&p->tagged, sizeof(uint64_t) * p->tagged_words));
+    watch_async_error(p->err, "decode step: an exchange timed out (blocks not co-resident)");
+    p->tagged_words = tag_layout(L0).total;
+    MH_TRY(plan_alloc(p, &p->tagged, sizeof(uint64_t) * p->tagged_words, "decode plan exchange words"));
     MH_HIP(hipMemset(p->tagged, 0, sizeof(uint64_t) * p->tagged_words));
-    MH_HIP(hipMalloc(&p->h, sizeof(float) * (size_t)L0.top_k * (size_t)L0.ffn));
-    p->Fpad = (int)((L0.ffn + 127) / 128 * 128);
-    MH_HIP(hipMalloc(&p->h16, sizeof(uint16_t) * 2 * (size_t)L0.top_k * (size_t)p->Fpad));
-    MH_HIP(hipMemset(p->h16, 0, sizeof(uint16_t) * 2 * (size_t)L0.top_k * (size_t)p->Fpad));   // the padding stays 0
-    if (p->mf) {
+    MH_TRY(plan_alloc(p, &p->h, sizeof(float) * (size_t)L0.top_k * (size_t)L0.ffn, "decode plan h"));
+    if (p->grp) {
         unsigned *bad = nullptr;
-        MH_HIP(hipMalloc(&bad, sizeof(unsigned)));
+        MH_TRY(dev_alloc((void **)&bad, sizeof(unsigned), "decode plan scale scan"));
         MH_HIP(hipMemset(bad, 0, sizeof(unsigned)));
         const int n_dn = (int)(L0.hidden * (L0.ffn / 32));
         for (int l = 0; l < n_layers; l++) {
@@ -1137,117 +1469,68 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
                                L.expert_stride, L.off[7], n_dn, bad);
         }
         unsigned hb = 0;
-        MH_HIP(hipGetLastError());
-        MH_HIP(hipMemcpy(&hb, bad, sizeof(unsigned), hipMemcpyDeviceToHost));
-        (void)hipFree(bad);
-        if (hb) p->mf = 0;   // the VALU path handles any f16 scale
+        const hipError_t le = hipGetLastError();
+        const hipError_t ce = le != hipSuccess ? le : hipMemcpy(&hb, bad, sizeof(unsigned), hipMemcpyDeviceToHost);
+        dev_release(bad, sizeof(unsigned));
+        MH_HIP(ce);
+        if (hb) p->grp = 0;   // the vector-ALU kernel handles any f16 scale
     }
     MH_HIP(hipMemset(p->flags, 0, sizeof(unsigned) * (size_t)flag_words(nb)));
     MH_HIP(hipDeviceSynchronize());
     p->seq = 1;
     p->nb = nb;
-    p->ok = 1;
+    p->ok = p->flat || p->grp;
+    if (!p->ok) snprintf(p->why, sizeof(p->why), "down scales not exact in f16 and the vector-ALU kernel does not fit");
     return MH_OK;
 }
 
 void step_plan_destroy(StepPlan *p) {
     if (!p) return;
-    (void)hipFree(p->layers);
-    (void)hipFree(p->flags);
-    (void)hipFree(p->trace);
-    unwatch_async_error(p->err);
-    (void)hipHostFree(p->err);
-    (void)hipFree(p->tagged);
-    (void)hipFree(p->h);
-    (void)hipFree(p->h16);
+    unregister_owner(p);
+    plan_release(p);
     delete p;
 }
 
 bool step_plan_ok(const StepPlan *p) { return p && p->ok; }
 
-int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_t *sel, float *w,
-             uint32_t *usage, hipStream_t s) {
-    const DevLayer &L0 = layers[0];
-    StepArgs A;
-    A.layers = p->layers;
-    A.n_layers = n_layers;
-    A.H = (int)L0.hidden;
-    A.F = (int)L0.ffn;
-    A.E = L0.n_experts;
-    A.K = L0.top_k;
-    A.CH = A.H / 32;
-    A.CF = A.F / 32;
-    A.stride = L0.expert_stride;
-    for (int i = 0; i < 9; i++) A.off[i] = L0.off[i];
-    A.alpha = L0.alpha;
-    A.limit = L0.limit;
-    A.eps = L0.norm_eps;
-    A.act_plain = L0.act_plain;
-    A.router_norm = L0.router_norm;
-    A.x = x;
-    A.sel = sel;
-    A.w = w;
-    A.usage = usage;
-    A.lws = (A.E + 15) / 16 * 16 + 32;   // copies 256 B past a line boundary apart
-    A.lw = p->tagged;
-    A.xw = p->tagged + (size_t)kLR * A.lws;
-    A.go = p->flags + go_offset(p->nb);
-    A.h = p->h;
-    A.h16 = p->h16;
-    A.Fpad = p->Fpad;
-    A.flags = p->flags;
-    A.trace = profiling() ? p->trace : nullptr;
-    A.err = p->err_dev;
-    const unsigned nbar = 3u * (unsigned)n_layers;
-    if (p->seq > 0xF0000000u) {   // wrap: restart the sequence from a clean slate
-        MH_LAUNCH("fill", k_fill_u32, dim3(1), dim3(256), 0, s, p->flags, flag_words(p->nb), 0u);
-        MH_LAUNCH("fill", k_fill_u32, dim3(8), dim3(256), 0, s, (unsigned *)p->tagged, (int)(2 * p->tagged_words), 0u);
-        p->seq = 1;
-    }
-    A.seq0 = p->seq;
-    p->seq += nbar;
-    const int nb = p->nb;
-    const int PB = (A.K * A.F + nb - 1) / nb, RC = (A.H + nb - 1) / nb;
-    A.res_floats = std::max(64 * kEL, std::max(2 * PB, A.K * RC)) + 64;
-    const int nsB = kThreads / A.CH;
-    A.red_floats = std::max(2 * nsB * kUP * A.CH, A.K * RC * A.CF);
-    const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two paths
-    const bool mf = p->mf && !(nm && nm[0] && nm[0] != '0');
-    if (A.H > kHMax || A.res_floats > kResMax || A.red_floats > kRedMax)
-        return fail(MH_E_UNSUPPORTED, "decode step: shape exceeds the kernel's LDS capacities");
-    const size_t lds = 0;
-    if (A.trace)   // stamps a block does not reach (a skipped phase) stay 0
-        MH_LAUNCH("fill", k_fill_u32, dim3(64), dim3(256), 0, s, (unsigned *)p->trace,
-                  (int)(2 * (size_t)kStamps * n_layers * p->nb), 0u);
-    int rc;
-    if (L0.router.dt == MH_DT_Q8R) {
-        if (L0.expert_dt == MH_DT_MXFP4)
-            rc = mf ? launch_t<MH_DT_Q8R, MH_DT_MXFP4, true>(A, nb, lds, s)
-                    : launch_t<MH_DT_Q8R, MH_DT_MXFP4, false>(A, nb, lds, s);
-        else
-            rc = launch_t<MH_DT_Q8R, MH_DT_Q4G32, false>(A, nb, lds, s);
-    } else {
-        if (L0.expert_dt == MH_DT_MXFP4)
-            rc = mf ? launch_t<MH_DT_F32, MH_DT_MXFP4, true>(A, nb, lds, s)
-                    : launch_t<MH_DT_F32, MH_DT_MXFP4, false>(A, nb, lds, s);
-        else
-            rc = launch_t<MH_DT_F32, MH_DT_Q4G32, false>(A, nb, lds, s);
-    }
-    if (rc || !A.trace) return rc;
-    // profiling: fold the per-block phase timestamps (100 MHz clock) into
-    // the profile: the mean over blocks and the slowest block of each span
+namespace {
+
+// A span between two phase stamps: mean over blocks (or block 0 only).
+struct Span {
+    const char *name;
+    int a, b;
+    bool b0;
+};
+const Span kGrpSpans[] = {
+    {"x_wait", 0, 15, false},        {"router", 15, 1, false},       {"route", 1, 2, false},
+    {"route0_gather", 1, 16, true},  {"route0_rank", 16, 17, true},  {"route0_weights", 17, 18, true},
+    {"route0_publish", 18, 2, true}, {"gu_issue", 2, 9, false},      {"gu_math", 9, 10, false},
+    {"gu_reduce", 10, 11, false},    {"h_publish", 11, 3, false},    {"dn_stage", 3, 4, false},
+    {"h_wait", 4, 5, false},         {"dn_math", 5, 13, false},      {"y_publish", 13, 14, false},
+    {"combine", 14, 6, false},       {"tail", 6, 7, false},          {"layer", 0, 7, false},
+    {"gu_first_pair", 9, 19, false}, {"gu_mid_pair", 19, 20, false}, {"gu_last_pair", 20, 10, false},
+    {"gu_wave7_lag", 10, 21, false}, {"gu_barrier", 10, 22, false}};
+const int kGrpOrder[] = {0, 15, 1, 16, 17, 18, 2, 9, 19, 20, 10, 21, 22, 11, 3, 4, 5, 13, 14, 6, 7};
+const Span kFlatSpans[] = {
+    {"x_wait", 0, 15, false},        {"router", 15, 1, false},       {"route", 1, 2, false},
+    {"route0_gather", 1, 16, true},  {"route0_rank", 16, 17, true},  {"route0_weights", 17, 18, true},
+    {"route0_publish", 18, 2, true}, {"gate_up", 2, 3, false},       {"gu_issue", 2, 9, false},
+    {"gu_math", 9, 10, false},       {"gu_reduce", 10, 11, false},   {"gu_epilogue", 11, 3, false},
+    {"barrier_arrive_prefetch", 3, 4, false}, {"barrier_wait", 4, 5, false}, {"down_combine", 5, 6, false},
+    {"dn_hload", 5, 12, false},      {"dn_math", 12, 13, false},     {"dn_reduce", 13, 14, false},
+    {"dn_combine", 14, 6, false},    {"tail", 6, 7, false},          {"layer", 0, 7, false}};
+const int kFlatOrder[] = {0, 15, 1, 16, 17, 18, 2, 9, 10, 11, 3, 4, 5, 12, 13, 14, 6, 7};
+
+// Folds the per-block phase stamps (100 MHz clock) of a profiled launch into
+// the profile: per span the mean over blocks and the slowest block; per
+// stamp the earliest and latest block from the layer's first start; the
+// critical path to the last logit, routing, h and x.
+template <size_t NS, size_t NO>
+int fold_stamps(const StepPlan *p, int n_layers, int nb, const Span (&spans)[NS], const int (&order)[NO],
+                hipStream_t s) {
     std::vector<unsigned long long> tr((size_t)kStamps * n_layers * nb);
     MH_HIP(hipMemcpyAsync(tr.data(), p->trace, tr.size() * 8, hipMemcpyDeviceToHost, s));
     MH_HIP(hipStreamSynchronize(s));
-    // (name, from, to, only block 0)
-    static const struct { const char *name; int a, b; bool b0; } spans[] = {
-        {"x_wait", 0, 15, false},   {"router", 15, 1, false},     {"route", 1, 2, false},
-        {"route0_gather", 1, 16, true}, {"route0_rank", 16, 17, true}, {"route0_weights", 17, 18, true},
-        {"route0_publish", 18, 2, true}, {"gate_up", 2, 3, false}, {"gu_issue", 2, 9, false},
-        {"gu_math", 9, 10, false},  {"gu_reduce", 10, 11, false}, {"gu_epilogue", 11, 3, false},
-        {"barrier_arrive_prefetch", 3, 4, false}, {"barrier_wait", 4, 5, false}, {"down_combine", 5, 6, false},
-        {"dn_hload", 5, 12, false}, {"dn_math", 12, 13, false},  {"dn_reduce", 13, 14, false},
-        {"dn_combine", 14, 6, false}, {"tail", 6, 7, false},     {"layer", 0, 7, false}};
     char name[96];
     auto at = [&](int l, int st, int b) { return (double)tr[((size_t)l * kStamps + st) * nb + b]; };
     for (int l = 0; l < n_layers; l++) {
@@ -1267,8 +1550,6 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
             snprintf(name, sizeof(name), "decode_step/%s.max", sp.name);
             prof_add(name, mx * 1e-5);
         }
-        // the critical path: from the first block's layer start to the last
-        // block's logit, the last block's routing record and the last arrival
         double t0 = 1e300, lastA = 0, lastR = 0, lastB = 0, lastC = 0;
         for (int b = 0; b < nb; b++) {
             t0 = std::min(t0, at(l, 0, b));
@@ -1277,8 +1558,6 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
             lastB = std::max(lastB, at(l, 3, b));
             lastC = std::max(lastC, at(l, 6, b));
         }
-        // every stamp's earliest and latest block, from the layer's first start
-        static const int order[] = {0, 15, 1, 16, 17, 18, 2, 9, 10, 11, 3, 4, 5, 12, 13, 14, 6, 7};
         for (int st : order) {
             double lo = 1e300, hi = 0;
             for (int b = 0; b < nb; b++) {
@@ -1289,7 +1568,7 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
                 hi = std::max(hi, v);
             }
             snprintf(name, sizeof(name), "decode_step/t%02d.first", st);
-            prof_add(name, lo * 1e-5);
+            prof_add(name, lo < 1e299 ? lo * 1e-5 : 0.0);
             snprintf(name, sizeof(name), "decode_step/t%02d.last", st);
             prof_add(name, hi * 1e-5);
         }
@@ -1299,6 +1578,93 @@ int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_
         prof_add("decode_step/crit_x", (lastC - t0) * 1e-5);
     }
     return MH_OK;
+}
+
+}  // namespace
+
+int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_t *sel, float *w,
+             uint32_t *usage, hipStream_t s) {
+    if (!p || !p->ok) return fail(MH_E_UNSUPPORTED, "decode step: no one-launch kernel for this stack");
+    const DevLayer &L0 = layers[0];
+    const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two kernels
+    const bool grp = p->grp && !(nm && nm[0] && nm[0] != '0');
+    if (!grp && !p->flat) return fail(MH_E_UNSUPPORTED, "decode step: the vector-ALU kernel does not fit this stack");
+    const TagLayout tl = tag_layout(L0);
+    RouteArgs R;
+    R.layers = p->layers;
+    R.n_layers = n_layers;
+    R.H = (int)L0.hidden;
+    R.E = L0.n_experts;
+    R.K = L0.top_k;
+    R.eps = L0.norm_eps;
+    R.router_norm = L0.router_norm;
+    R.x = x;
+    R.sel = sel;
+    R.w = w;
+    R.usage = usage;
+    R.lw = p->tagged + tl.lw;
+    R.lws = tl.lws;
+    R.err = p->err_dev;
+    R.trace = profiling() ? p->trace : nullptr;
+    const unsigned per_layer = grp ? 4u : 3u;
+    if (p->seq > 0xF0000000u) {   // wrap: restart the sequence from a clean slate
+        MH_LAUNCH("fill", k_fill_u32, dim3(1), dim3(256), 0, s, p->flags, flag_words(p->nb), 0u);
+        MH_LAUNCH("fill", k_fill_u32, dim3(64), dim3(256), 0, s, (unsigned *)p->tagged, (int)(2 * p->tagged_words), 0u);
+        p->seq = 1;
+    }
+    const unsigned seq0 = p->seq;
+    p->seq += per_layer * (unsigned)n_layers;
+    const int nb = grp ? p->G * R.K : p->nb;
+    if (R.trace)   // stamps a block does not reach (a skipped phase) stay 0
+        MH_LAUNCH("fill", k_fill_u32, dim3(64), dim3(256), 0, s, (unsigned *)p->trace,
+                  (int)(2 * (size_t)kStamps * n_layers * nb), 0u);
+    const bool q8 = L0.router.dt == MH_DT_Q8R;
+    int rc;
+    if (grp) {
+        GrpArgs A;
+        A.R = R;
+        A.F = (int)L0.ffn;
+        A.CH = R.H / 32;
+        A.CF = A.F / 32;
+        A.G = p->G;
+        A.PB = p->PB;
+        A.RB = p->RB;
+        A.stride = L0.expert_stride;
+        for (int i = 0; i < 9; i++) A.off[i] = L0.off[i];
+        A.alpha = L0.alpha;
+        A.limit = L0.limit;
+        A.xw = p->tagged + tl.xw;
+        A.xws = tl.xws;
+        A.hw = p->tagged + tl.hw;
+        A.hws = tl.hws;
+        A.yw = p->tagged + tl.yw;
+        A.flags = p->flags;
+        A.seq0 = seq0;
+        rc = q8 ? launch_grp<MH_DT_Q8R>(A, nb, s) : launch_grp<MH_DT_F32>(A, nb, s);
+    } else {
+        StepArgs A;
+        A.R = R;
+        A.F = (int)L0.ffn;
+        A.CH = R.H / 32;
+        A.CF = A.F / 32;
+        A.stride = L0.expert_stride;
+        for (int i = 0; i < 9; i++) A.off[i] = L0.off[i];
+        A.alpha = L0.alpha;
+        A.limit = L0.limit;
+        A.act_plain = L0.act_plain;
+        A.xw = p->tagged + tl.xw;
+        A.h = p->h;
+        A.flags = p->flags;
+        A.go = p->flags + go_offset(p->nb);
+        A.seq0 = seq0;
+        if (L0.expert_dt == MH_DT_MXFP4)
+            rc = q8 ? launch_flat<MH_DT_Q8R, MH_DT_MXFP4>(A, nb, s) : launch_flat<MH_DT_F32, MH_DT_MXFP4>(A, nb, s);
+        else
+            rc = q8 ? launch_flat<MH_DT_Q8R, MH_DT_Q4G32>(A, nb, s) : launch_flat<MH_DT_F32, MH_DT_Q4G32>(A, nb, s);
+    }
+    if (rc || !R.trace) return rc;
+    return grp ? fold_stamps(p, n_layers, nb, kGrpSpans, kGrpOrder, s)
+               : fold_stamps(p, n_layers, nb, kFlatSpans, kFlatOrder, s);
 }
 
 }  // namespace mh

@@ -40,6 +40,15 @@ int device_cus();   // compute units on the current device
 int resolve_weight(const void *p, uint64_t bytes, const void **dev, const char *what);
 int resolve_dev(const void *p, uint64_t bytes, const char *what);
 
+// Device memory counted against MIDGE_HIP_MAX_BYTES (MH_E_NOMEM beyond it);
+// dev_release frees it and returns the bytes to the count.
+int dev_alloc(void **p, uint64_t bytes, const char *what);
+void dev_release(void *p, uint64_t bytes);
+// Objects that hold device memory of their own (decode plans) register a
+// release callback; mh_shutdown calls it for every object still alive.
+void register_owner(void *key, void (*release)(void *));
+void unregister_owner(void *key);
+
 // Library-owned device scratch that grows on demand (slot = purpose id).
 // Contents are not preserved across growth.
 enum Scratch { S_X = 0, S_Y, S_XB, S_H, S_YE, S_RL, S_SEL, S_W, S_PLAN, S_MISC, S_LIST, S_Q, S_XQ, S_ORD, S_SAMPLE, S_ATTN, S_COUNT };

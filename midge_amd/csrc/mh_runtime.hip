@@ -22,14 +22,25 @@ struct Region {
     uint8_t *dev;
 };
 
+// Live objects holding device memory outside the tables below (decode
+// plans): mh_shutdown releases their memory through the callback.
+struct Owner {
+    void *key;
+    void (*release)(void *);
+};
+
 struct State {
     bool inited = false;
     int device = -1;
     int cus = 0;
     hipStream_t own = nullptr;
     hipStream_t cur = nullptr;
-    std::vector<Region> regions;
+    // registered regions, keyed by host base and by device base (lookups
+    // are O(log n): a lazily registered model holds tens of thousands)
+    std::map<uintptr_t, Region> regions;
+    std::map<uintptr_t, uint64_t> region_dev;   // device base -> bytes
     std::map<uintptr_t, uint64_t> allocs;   // device base -> bytes (mh_alloc)
+    std::vector<Owner> owners;
     uint64_t allocated = 0;
     uint64_t cap = 0;                       // 0 = no cap
     void *scratch[S_COUNT] = {};
@@ -82,6 +93,24 @@ int fail(int code, const char *fmt, ...) {
 }
 
 void clear_error() { g_err[0] = 0; }
+
+int dev_alloc(void **p, uint64_t bytes, const char *what) { return dev_malloc(p, bytes, what); }
+
+void dev_release(void *p, uint64_t bytes) {
+    if (!p) return;
+    (void)hipFree(p);
+    g.allocated = g.allocated >= bytes ? g.allocated - bytes : 0;
+}
+
+void register_owner(void *key, void (*release)(void *)) { g.owners.push_back(Owner{key, release}); }
+
+void unregister_owner(void *key) {
+    for (size_t i = 0; i < g.owners.size(); i++)
+        if (g.owners[i].key == key) {
+            g.owners.erase(g.owners.begin() + (long)i);
+            return;
+        }
+}
 
 void watch_async_error(unsigned *flag, const char *msg) { g_async.push_back({flag, msg}); }
 
@@ -161,28 +190,33 @@ int wt_bytes(int dt, int64_t rows, int64_t cols, uint64_t *db, uint64_t *sb) {
     return fail(MH_E_DTYPE, "unknown dtype %d", dt);
 }
 
+static uint64_t span_of(uint64_t bytes) { return bytes; }
+static uint64_t span_of(const Region &r) { return r.bytes; }
+
+// The entry of a base -> bytes map whose range holds address a, or end().
+template <class M>
+static typename M::const_iterator containing(const M &m, uintptr_t a) {
+    auto it = m.upper_bound(a);
+    if (it == m.begin()) return m.end();
+    --it;
+    return a < it->first + span_of(it->second) ? it : m.end();
+}
+
 // Device allocation containing [p, p+bytes), via our own tables first and
 // the HIP runtime otherwise.
 static int check_device_range(const void *p, uint64_t bytes, const char *what) {
     uintptr_t a = (uintptr_t)p;
-    auto it = g.allocs.upper_bound(a);
-    if (it != g.allocs.begin()) {
-        --it;
-        if (a >= it->first && a < it->first + it->second) {
-            if (a + bytes > it->first + it->second)
-                return fail(MH_E_RANGE, "%s: %llu bytes at %p overrun its allocation", what,
-                            (unsigned long long)bytes, p);
-            return MH_OK;
-        }
+    auto it = containing(g.allocs, a);
+    if (it != g.allocs.end()) {
+        if (a + bytes > it->first + it->second)
+            return fail(MH_E_RANGE, "%s: %llu bytes at %p overrun its allocation", what, (unsigned long long)bytes, p);
+        return MH_OK;
     }
-    for (const Region &r : g.regions) {
-        uintptr_t d = (uintptr_t)r.dev;
-        if (a >= d && a < d + r.bytes) {
-            if (a + bytes > d + r.bytes)
-                return fail(MH_E_RANGE, "%s: %llu bytes at %p overrun the region", what,
-                            (unsigned long long)bytes, p);
-            return MH_OK;
-        }
+    auto rd = containing(g.region_dev, a);
+    if (rd != g.region_dev.end()) {
+        if (a + bytes > rd->first + rd->second)
+            return fail(MH_E_RANGE, "%s: %llu bytes at %p overrun the region", what, (unsigned long long)bytes, p);
+        return MH_OK;
     }
     hipPointerAttribute_t attr;
     hipError_t e = hipPointerGetAttributes(&attr, p);
@@ -207,15 +241,14 @@ static int check_device_range(const void *p, uint64_t bytes, const char *what) {
 int resolve_weight(const void *p, uint64_t bytes, const void **dev, const char *what) {
     if (!p) return fail(MH_E_ARG, "%s: NULL pointer", what);
     uintptr_t a = (uintptr_t)p;
-    for (const Region &r : g.regions) {
-        uintptr_t h = (uintptr_t)r.host;
-        if (a >= h && a < h + r.bytes) {
-            if (a + bytes > h + r.bytes)
-                return fail(MH_E_RANGE, "%s: %llu bytes at %p run past the registered region", what,
-                            (unsigned long long)bytes, p);
-            *dev = r.dev + (a - h);
-            return MH_OK;
-        }
+    auto it = containing(g.regions, a);
+    if (it != g.regions.end()) {
+        const Region &r = it->second;
+        if (a + bytes > it->first + r.bytes)
+            return fail(MH_E_RANGE, "%s: %llu bytes at %p run past the registered region", what,
+                        (unsigned long long)bytes, p);
+        *dev = r.dev + (a - it->first);
+        return MH_OK;
     }
     MH_TRY(check_device_range(p, bytes, what));
     *dev = p;
@@ -224,12 +257,8 @@ int resolve_weight(const void *p, uint64_t bytes, const void **dev, const char *
 
 int resolve_dev(const void *p, uint64_t bytes, const char *what) {
     if (!p) return fail(MH_E_ARG, "%s: NULL pointer", what);
-    uintptr_t a = (uintptr_t)p;
-    for (const Region &r : g.regions) {
-        uintptr_t h = (uintptr_t)r.host;
-        if (a >= h && a < h + r.bytes)
-            return fail(MH_E_ARG, "%s: %p is a registered host pointer; _dev calls need device memory", what, p);
-    }
+    if (containing(g.regions, (uintptr_t)p) != g.regions.end())
+        return fail(MH_E_ARG, "%s: %p is a registered host pointer; _dev calls need device memory", what, p);
     return check_device_range(p, bytes, what);
 }
 
@@ -309,8 +338,16 @@ int mh_shutdown(void) {
     clear_error();
     if (!g.inited) return MH_OK;
     (void)hipStreamSynchronize(g.cur);
-    for (Region &r : g.regions) (void)hipFree(r.dev);
+    // live plans first (their release callbacks unregister them)
+    while (!g.owners.empty()) {
+        const Owner o = g.owners.back();
+        g.owners.pop_back();
+        o.release(o.key);
+    }
+    g_async.clear();
+    for (auto &r : g.regions) (void)hipFree(r.second.dev);
     g.regions.clear();
+    g.region_dev.clear();
     for (auto &a : g.allocs) (void)hipFree((void *)a.first);
     g.allocs.clear();
     for (int i = 0; i < S_COUNT; i++) {
@@ -376,9 +413,17 @@ int mh_register_region(const void *host_base, uint64_t bytes, void **dev_base) {
     MH_TRY(require_init());
     if (!host_base || !bytes || !dev_base) return fail(MH_E_ARG, "register_region: NULL base/out or zero size");
     uintptr_t a = (uintptr_t)host_base;
-    for (const Region &r : g.regions) {
-        uintptr_t h = (uintptr_t)r.host;
-        if (a < h + r.bytes && h < a + bytes)
+    if (bytes > UINTPTR_MAX - a) return fail(MH_E_ARG, "register_region: [%p, +%llu) wraps the address space", host_base,
+                                             (unsigned long long)bytes);
+    {
+        // the nearest region at or below a, and the first one above it
+        auto hi = g.regions.upper_bound(a);
+        bool overlap = hi != g.regions.end() && hi->first < a + bytes;
+        if (hi != g.regions.begin()) {
+            auto lo = std::prev(hi);
+            overlap = overlap || a < lo->first + lo->second.bytes;
+        }
+        if (overlap)
             return fail(MH_E_ARG, "register_region: [%p, +%llu) overlaps a registered region", host_base,
                         (unsigned long long)bytes);
     }
@@ -390,7 +435,8 @@ int mh_register_region(const void *host_base, uint64_t bytes, void **dev_base) {
         g.allocated -= bytes;
         return hip_check(e, "register_region upload");
     }
-    g.regions.push_back(Region{(const uint8_t *)host_base, bytes, (uint8_t *)d});
+    g.regions[a] = Region{(const uint8_t *)host_base, bytes, (uint8_t *)d};
+    g.region_dev[(uintptr_t)d] = bytes;
     *dev_base = d;
     return MH_OK;
 }
@@ -398,16 +444,14 @@ int mh_register_region(const void *host_base, uint64_t bytes, void **dev_base) {
 int mh_unregister_region(const void *host_base) {
     clear_error();
     MH_TRY(require_init());
-    for (size_t i = 0; i < g.regions.size(); i++) {
-        if (g.regions[i].host == host_base) {
-            MH_HIP(hipStreamSynchronize(g.cur));
-            MH_HIP(hipFree(g.regions[i].dev));
-            g.allocated -= g.regions[i].bytes;
-            g.regions.erase(g.regions.begin() + (long)i);
-            return MH_OK;
-        }
-    }
-    return fail(MH_E_ARG, "unregister_region: %p is not a registered base", host_base);
+    auto it = g.regions.find((uintptr_t)host_base);
+    if (it == g.regions.end()) return fail(MH_E_ARG, "unregister_region: %p is not a registered base", host_base);
+    MH_HIP(hipStreamSynchronize(g.cur));
+    MH_HIP(hipFree(it->second.dev));
+    g.allocated -= it->second.bytes;
+    g.region_dev.erase((uintptr_t)it->second.dev);
+    g.regions.erase(it);
+    return MH_OK;
 }
 
 int mh_alloc(uint64_t bytes, void **dev) {
