@@ -113,7 +113,8 @@ constexpr int kThreads = 512;   // 8 waves: 2 per SIMD, up to 256 VGPRs each
 constexpr int kUP = 9;          // gate/up row pairs in flight per thread
 constexpr int kUC = 12;         // down rows in flight per thread (k_decode_step)
 constexpr int kUD = 9;          // down rows in flight per thread (k_decode_grp)
-static_assert(kUD <= kUP, "k_decode_grp issues one down-row load per gate/up pair");
+constexpr int kPD = 4;          // gate/up pairs in flight per thread (k_decode_grp)
+static_assert(kPD <= kUP, "k_decode_grp's gate/up pipeline depth");
 constexpr int kNX = 8;          // x elements per thread in the router phase (H <= kNX * kThreads)
 constexpr unsigned kSpinLimit = 1u << 20;
 constexpr int kStamps = 24;     // phase timestamps per layer and block while profiling
@@ -781,14 +782,20 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                                                : (sa2 & ~15u) + (uint32_t)min(q - n0 - n1, n2 - 1) * 16u;
                 qs[k] = ld_w16(rex, a);
             }
+            // gate/up pairs in flight: kPD per thread, pair u + kPD issued
+            // after pair u's math (loads complete in issue order, and a
+            // wave's first loads complete only when its last do if all of
+            // the layer's loads are in flight at once: the depth lets the
+            // math run as the stream arrives)
             mh_u4 qg[kUP], qu[kUP];
             const uint32_t og = eo + (uint32_t)A.off[0], ou = eo + (uint32_t)A.off[3];
-#pragma unroll
-            for (int u = 0; u < kUP; ++u) {
+            auto issue_gu = [&](int u) __attribute__((always_inline)) {
                 const uint32_t rc = (uint32_t)((p0 + min(u * ns + gsl, plast)) * C + c);
                 qg[u] = ld_w16(rex, og + rc * 16u);
                 qu[u] = ld_w16(rex, ou + rc * 16u);
-            }
+            };
+#pragma unroll
+            for (int u = 0; u < kPD; ++u) issue_gu(u);
             const uint32_t pb4 = (uint32_t)(p0 + min(t, plast)) * 4u;
             const float bg = ld_f(rex, eo + (uint32_t)A.off[2] + pb4);
             const float bu = ld_f(rex, eo + (uint32_t)A.off[5] + pb4);
@@ -804,11 +811,11 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
             }
             __syncthreads();
             const uint16_t *scg = (const uint16_t *)(s_sc + mis0), *scu = (const uint16_t *)(s_sc + kScW + mis1);
-            // gate/up math as the data arrives (loads complete in issue
-            // order), each pair's math followed by one down-row load: a load
-            // whose issue waits for room in the memory pipeline then holds up
-            // no gate/up math whose data is in; the down rows are needed only
-            // after the h exchange. Down row j = u nsd + ds is thread (slot
+            // gate/up math as the data arrives, each pair's math followed by
+            // the next pair's loads and, once those are all issued, by the
+            // down rows (needed only after the h exchange), so that a load
+            // whose issue waits for room in the memory pipeline holds up no
+            // math whose data is in. Down row j = u nsd + ds is thread (slot
             // ds, chunk dc)'s (whole rows per instruction).
             const int nsd = kThreads / CD;
             const int ds = tt / CD, dc = tt - ds * CD;
@@ -828,9 +835,14 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                     red[(2 * pp) * C + c] = gv;
                     red[(2 * pp + 1) * C + c] = uv;
                 }
-                if (u < kUD) {
-                    const uint32_t rc = (uint32_t)((r0 + min(u * nsd + dsl, nr - 1)) * CD + dc);
-                    qd[u] = ld_w16(rex, od + rc * 16u);
+                if (u + kPD < kUP) issue_gu(u + kPD);
+                if (u >= kUP - kPD) {
+                    const int i = u - (kUP - kPD);
+#pragma unroll
+                    for (int d = i * kUD / kPD; d < (i + 1) * kUD / kPD; ++d) {
+                        const uint32_t rc = (uint32_t)((r0 + min(d * nsd + dsl, nr - 1)) * CD + dc);
+                        qd[d] = ld_w16(rex, od + rc * 16u);
+                    }
                 }
                 if (u == 0) stamp(l, 19);
                 if (u == kUP / 2) stamp(l, 20);
