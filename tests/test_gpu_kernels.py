@@ -358,6 +358,46 @@ def test_sample_dev_vs_oracle(mh, V):
     out.free()
 
 
+@pytest.mark.parametrize("shape", ["peaked", "flat", "equal", "steps", "cap_edge"])
+def test_sample_dev_nucleus_paths(mh, shape):
+    # The nucleus selection's two ways (a sort of the candidates in LDS, or
+    # the exact radix select over the whole vocabulary when the candidates
+    # are too many or the nucleus reaches past them): peaked logits (a few
+    # candidates), flat ones (the nucleus is most of the vocabulary), all
+    # logits equal (one group of V equal p: ties by token id), a staircase
+    # of equal-p groups, and a nucleus of about the candidate capacity.
+    from midge_amd.moe import sample_dev
+    say(f"sample_dev nucleus {shape}")
+    rng = np.random.default_rng(hash(shape) % 2**32)
+    V = 201088
+    if shape == "peaked":
+        lg = (rng.standard_normal(V) * 6).astype(np.float32)
+    elif shape == "flat":
+        lg = (rng.standard_normal(V) * 0.2).astype(np.float32)
+    elif shape == "equal":
+        lg = np.full(V, 0.25, np.float32)
+    elif shape == "steps":
+        lg = np.floor(rng.random(V) * 12).astype(np.float32)
+    else:
+        lg = np.full(V, -30.0, np.float32)
+        lg[rng.choice(V, 9000, replace=False)] = rng.random(9000).astype(np.float32)
+    ld, out = DevBuf.from_array(lg), DevBuf(4)
+    st = 0x853C49E6748FEA9B ^ len(shape)
+    for temp in (0.7, 1.0):
+        for topp in (0.3, 0.9, 0.999, 1.0):
+            for _ in range(3):
+                u, st = po.rng_f(st)
+                sample_dev(ld, V, temp, topp, u, out)
+                got = int(out.download(np.int32, (1,))[0])
+                want = po.sample(lg, temp, topp, u)
+                assert got == want, (shape, temp, topp, u, got, want)
+    for u in (0.0, 0.999999):   # the first token of the order; the nucleus's last
+        sample_dev(ld, V, 1.0, 0.9, u, out)
+        assert int(out.download(np.int32, (1,))[0]) == po.sample(lg, 1.0, 0.9, u), (shape, u)
+    ld.free()
+    out.free()
+
+
 @pytest.mark.parametrize("name", ["small_sliding_sinks", "small_full_qknorm", "gpt_oss"])
 def test_attention_dev_vs_oracle(mh, name):
     # attention() for a run of decode positions (past the sliding window, so
