@@ -177,6 +177,17 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos);
  * for equal keys under glibc's qsort). */
 int mh_sample_dev(const float *logits, int64_t V, float temp, float topp, float u, int32_t *out);
 
+/* mh_sample_dev on a fixed workspace that the library holds on each GPU
+ * from mh_init() until the process ends (about 1.05 MB): the call allocates
+ * nothing (no hipMalloc, hipFree or event), for callers that cannot
+ * allocate: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation. No counterpart in the reference. V is limited to
+ * 1..262144 (MH_E_ARG beyond). Every call on a GPU shares that GPU's
+ * workspace: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialised by the caller. Same results as
+ * mh_sample_dev. */
+int mh_sample_dev_static(const float *logits, int64_t V, float temp, float topp, float u, int32_t *out);
+
 /* ------------------------------------------------------- layer level */
 
 /* Decode MoE layer for one token, in place on host x[hidden]: rmsnorm,

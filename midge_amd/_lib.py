@@ -93,6 +93,7 @@ _SIGS = {
     "mh_moe_prefill_dev": [C.POINTER(MhMoeLayer), _I, _P, _P, _P],
     "mh_topk_dev": [_P, _I, _I, _I, _I, _P, _P],
     "mh_sample_dev": [_P, _I64, _F, _F, _F, _P],
+    "mh_sample_dev_static": [_P, _I64, _F, _F, _F, _P],
     "mh_attention_dev": [C.POINTER(MhAttnLayer), _P, _I],
     "mh_expert_major_dev": [C.POINTER(MhMoeLayer), _I, _P, _P, _P, _P],
     "mh_stack_create": [C.POINTER(MhMoeLayer), _I, _I, C.POINTER(_P)],

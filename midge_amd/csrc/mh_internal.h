@@ -33,6 +33,10 @@ bool initialised();
 int require_init();
 hipStream_t stream();
 int device_cus();   // compute units on the current device
+int current_device();   // the device mh_init() opened
+// Looks up the sampling path's fixed workspace on `device` (current) and
+// clears its counters; mh_init() calls it (mh_sample.hip).
+int sample_static_setup(int device);
 
 // Pointer resolution. Weights: a host pointer inside a registered region
 // (translated) or device memory. Activations (_dev calls): device memory

@@ -174,6 +174,7 @@ int require_init() {
 
 hipStream_t stream() { return g.cur; }
 int device_cus() { return g.cus; }
+int current_device() { return g.device; }
 
 int wt_bytes(int dt, int64_t rows, int64_t cols, uint64_t *db, uint64_t *sb) {
     if (rows < 0 || cols < 0) return fail(MH_E_ARG, "negative shape %lld x %lld", (long long)rows, (long long)cols);
@@ -331,6 +332,12 @@ int mh_init(int device) {
     g.cus = prop.multiProcessorCount;
     g.cap = env_cap();
     g.inited = true;
+    const int rc = sample_static_setup(device);
+    if (rc) {
+        (void)hipStreamDestroy(g.own);
+        g = State();
+        return rc;
+    }
     return MH_OK;
 }
 

@@ -670,18 +670,50 @@ uint64_t sample_ws_bytes(int64_t V) { return kWsHead + (uint64_t)V * 4; }
 
 // The sampling launches on workspace ws (device, sample_ws_bytes(V) bytes;
 // its last-block counters must be zero, as a fill to zero leaves them and
-// every call leaves them).
+// every call leaves them). `prof` lets profiling bracket the launches with
+// events (the allocation-free entry point passes false: event creation is
+// not for it).
 int sample_launch(const float *logits, int V, float temp, float topp, float u, void *ws_dev, int32_t *out,
-                  hipStream_t s) {
+                  hipStream_t s, bool prof) {
     SampWs *ws = (SampWs *)ws_dev;
     const bool greedy = temp <= 0.f;
-    MH_LAUNCH("sample_max", k_samp_max, dim3(kSampBlocks), dim3(kSampThreads), 0, s, logits, V, ws,
-              greedy ? out : nullptr);
+#define SAMP_LAUNCH(name, kernel, grid, block, ...)                                  \
+    do {                                                                             \
+        if (prof) MH_LAUNCH(name, kernel, grid, block, 0, s, __VA_ARGS__);           \
+        else hipLaunchKernelGGL(kernel, grid, block, 0, s, __VA_ARGS__);             \
+    } while (0)
+    SAMP_LAUNCH("sample_max", k_samp_max, dim3(kSampBlocks), dim3(kSampThreads), logits, V, ws,
+                greedy ? out : nullptr);
     if (greedy) return hip_check(hipGetLastError(), "sample launch");
-    MH_LAUNCH("sample_exp", k_samp_exp, dim3(kSampBlocks), dim3(kSampThreads), 0, s, logits, V, temp, topp, ws);
-    MH_LAUNCH("sample_select", k_samp_select, dim3(kSelBlocks), dim3(kSelThreads), 0, s, logits, V, temp, topp, u,
-              ws, out);
+    SAMP_LAUNCH("sample_exp", k_samp_exp, dim3(kSampBlocks), dim3(kSampThreads), logits, V, temp, topp, ws);
+    SAMP_LAUNCH("sample_select", k_samp_select, dim3(kSelBlocks), dim3(kSelThreads), logits, V, temp, topp, u, ws,
+                out);
+#undef SAMP_LAUNCH
     return hip_check(hipGetLastError(), "sample launch");
+}
+
+// ------------------------------------------ the fixed, allocation-free workspace
+
+// Vocabularies up to 2^18 tokens (gpt-oss: 201088) fit the fixed workspace:
+// about 1.05 MB of device memory per GPU, held until the process ends.
+constexpr int64_t kStaticMaxV = 1 << 18;
+static __device__ __align__(256) uint8_t samp_static_ws[kWsHead + kStaticMaxV * 4];
+
+// The array's device address on each GPU (its host-side name is no device
+// address), looked up once per device at initialisation.
+constexpr int kMaxDevices = 64;
+static void *g_static_ws[kMaxDevices];
+
+int sample_static_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return fail(MH_E_ARG, "device %d beyond the static workspace table", device);
+    void *p = nullptr;
+    MH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(samp_static_ws)));
+    if (!p) return fail(MH_E_HIP, "hipGetSymbolAddress gave no address for the sampling workspace");
+    // counters and histogram start at zero (a fill kernel: no memset node)
+    hipLaunchKernelGGL(k_samp_clear, dim3(8), dim3(256), 0, stream(), (uint32_t *)p, (int)(kWsHead / 4));
+    MH_HIP(hipGetLastError());
+    g_static_ws[device] = p;
+    return MH_OK;
 }
 
 }  // namespace mh
@@ -699,7 +731,22 @@ int mh_sample_dev(const float *logits, int64_t V, float temp, float topp, float 
     MH_TRY(resolve_dev(out, 4, "mh_sample_dev out"));
     void *ws;
     MH_TRY(sample_scratch(sample_ws_bytes(V), &ws));
-    return sample_launch(logits, (int)V, temp, topp, u, ws, out, stream());
+    return sample_launch(logits, (int)V, temp, topp, u, ws, out, stream(), true);
+}
+
+int mh_sample_dev_static(const float *logits, int64_t V, float temp, float topp, float u, int32_t *out) {
+    clear_error();
+    if (!logits || !out) return fail(MH_E_ARG, "mh_sample_dev_static: NULL logits or out");
+    if (V < 1 || V > kStaticMaxV)
+        return fail(MH_E_ARG, "mh_sample_dev_static: vocabulary %lld outside 1..%lld (the fixed workspace's limit)",
+                    (long long)V, (long long)kStaticMaxV);
+    MH_TRY(require_init());
+    MH_TRY(resolve_dev(logits, (uint64_t)V * 4, "mh_sample_dev_static logits"));
+    MH_TRY(resolve_dev(out, 4, "mh_sample_dev_static out"));
+    const int dev = current_device();
+    void *ws = dev >= 0 && dev < kMaxDevices ? g_static_ws[dev] : nullptr;
+    if (!ws) return fail(MH_E_NOINIT, "mh_sample_dev_static: no workspace address for device %d", dev);
+    return sample_launch(logits, (int)V, temp, topp, u, ws, out, stream(), false);
 }
 
 }  // extern "C"

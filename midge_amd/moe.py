@@ -123,6 +123,13 @@ def sample_dev(logits, vocab: int, temp: float, topp: float, u: float, out) -> N
     _lib.call("mh_sample_dev", int(logits), int(vocab), float(temp), float(topp), float(u), int(out))
 
 
+def sample_dev_static(logits, vocab: int, temp: float, topp: float, u: float, out) -> None:
+    """sample_dev on the library's fixed workspace: allocates nothing
+    (vocab <= 262144; overlapping calls on one GPU share the workspace and
+    race)."""
+    _lib.call("mh_sample_dev_static", int(logits), int(vocab), float(temp), float(topp), float(u), int(out))
+
+
 def topk_dev(logits, n: int, n_experts: int, k: int, router_norm: int, sel, w) -> None:
     _lib.call("mh_topk_dev", int(logits), int(n), int(n_experts), int(k), int(router_norm), int(sel), int(w))
 

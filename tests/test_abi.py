@@ -135,3 +135,7 @@ def test_attention_and_sample_validation_before_device():
     assert _rc("mh_sample_dev", None, 10, 0.0, 1.0, C.c_float(0.0), 1) == _lib.MH_E_ARG
     assert _rc("mh_sample_dev", 1, 0, 0.0, 1.0, C.c_float(0.0), 1) == _lib.MH_E_ARG
     assert "vocabulary" in _err()
+    # the fixed-workspace variant: vocabularies beyond its 2^18 tokens are refused up front
+    assert _rc("mh_sample_dev_static", 1, 262145, 0.0, 1.0, C.c_float(0.0), 1) == _lib.MH_E_ARG
+    assert "fixed workspace" in _err()
+    assert _rc("mh_sample_dev_static", None, 10, 0.0, 1.0, C.c_float(0.0), 1) == _lib.MH_E_ARG
