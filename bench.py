@@ -573,9 +573,11 @@ def prefill_probe(ev, s, seed: int, n: int = 512, reps: int = 10) -> dict:
     return out
 
 
-def run_cpu(shape, seed: int, seconds: float):
+def run_cpu(shape, seed: int, seconds: float, threads: int) -> dict:
     """The reference engine's moe() (AVX2+OpenMP, built from its sources) over
-    one resident gpt-oss-120b layer (128 experts, 1.8 GB host RAM)."""
+    one resident gpt-oss-120b layer (128 experts, 1.8 GB host RAM), in this
+    process (a child of the bench: its OpenMP team is set up from the
+    environment the parent gives it)."""
     from midge_amd import synth
     from oracle import pyoracle as po
 
@@ -605,10 +607,49 @@ def run_cpu(shape, seed: int, seconds: float):
         run(xs[n % 64])
         n += 1
     dt = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)) if kind == "reference" else 1
-    return {"value": n / dt / shape.n_layers, "unit": "tok/s", "cores": threads, "kind": kind,
+    layer_b = step_bytes(shape, 1, shape.top_k) / shape.n_layers   # the bytes one moe() call reads
+    return {"value": n / dt / shape.n_layers, "unit": "tok/s", "cores": threads if kind == "reference" else 1,
+            "kind": kind, "GBps": n / dt * layer_b / 1e9,
             "sample": f"{n} moe() calls on one resident 128-expert gpt-oss-120b layer (batch 1, {dt:.1f}s), "
                       f"tok/s = calls/s / 36 layers"}
+
+
+def physical_cores() -> int | None:
+    """Physical cores of the host (distinct (core, socket) pairs of lscpu)."""
+    import subprocess
+    try:
+        r = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, timeout=20)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    pairs = {ln.strip() for ln in r.stdout.splitlines() if ln.strip() and not ln.startswith("#")}
+    return len(pairs) or None
+
+
+def cpu_baseline(shape, seed: int, seconds: float) -> dict:
+    """The CPU baseline in two child processes: one OpenMP thread (beside the
+    reference's published per-core figure, 3.98 GB/s on AVX2, README.md:84-86)
+    and the threads this process may use (its affinity mask, at most
+    OMP_NUM_THREADS), each pinned to its own physical core (OMP_PROC_BIND=close,
+    OMP_PLACES=cores)."""
+    import subprocess
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    team = max(1, min(avail, int(os.environ.get("OMP_NUM_THREADS", avail))))
+    rows = {}
+    for threads, secs in ((1, seconds / 2), (team, seconds)):
+        env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="close", OMP_PLACES="cores")
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-child", str(threads),
+                            "--cpu-seconds", str(secs), "--seed", str(seed)],
+                           env=env, capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError(f"cpu baseline child ({threads} threads) failed: {r.stderr[-500:]}")
+        rows[threads] = json.loads(r.stdout.strip().splitlines()[-1])
+    out = dict(rows[team])
+    one = rows[1]
+    out.update({"physical_cores": physical_cores(), "affinity_cpus": avail,
+                "binding": "OMP_PROC_BIND=close OMP_PLACES=cores",
+                "one_thread": {"value": one["value"], "unit": "tok/s", "GBps": one["GBps"],
+                               "published_GBps_per_core": 3.98, "sample": one["sample"]}})
+    return out
 
 
 def main() -> int:
@@ -627,15 +668,20 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the expert-major prefill measurement")
     ap.add_argument("--no-refbench", action="store_true", help="skip the reference's run_bench figure")
     ap.add_argument("--no-configs", action="store_true", help="skip the configuration 0-2 measurements")
+    ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device twice (byte-counter calibration)")
     args = ap.parse_args()
+    from midge_amd.synth import MoEShape
+    if args.cpu_child:   # the CPU baseline's child process: no GPU
+        shape = MoEShape(hidden=2880, ffn=2880, n_experts=args.experts, top_k=4, n_layers=args.layers)
+        print(json.dumps(run_cpu(shape, args.seed, args.cpu_seconds, args.cpu_child)), flush=True)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the expert stack "
               "fits one MI355X); run with --gpus 1", file=sys.stderr)
         return 2
 
-    from midge_amd.synth import MoEShape
     shape = MoEShape(hidden=2880, ffn=2880, n_experts=args.experts, top_k=4, n_layers=args.layers)
     ms, unique, kern, dom, extra = run_gpu(args, shape)
     ms_step = ms / args.steps
@@ -644,7 +690,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
-        cpu = run_cpu(shape, args.seed, args.cpu_seconds)
+        cpu = cpu_baseline(shape, args.seed, args.cpu_seconds)
     out = {
         "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",

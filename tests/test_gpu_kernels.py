@@ -404,9 +404,9 @@ def test_attention_dev_vs_oracle(mh, name):
     # the ring wraps): the device x and f16 caches against the oracle's
     # (bit-exact with the reference's scalar attention on the CPU)
     import ctypes
-    from test_oracle_kernels import ATTN_SHAPES, GPT_OSS_ROPE, AttnHost
+    from test_oracle_kernels import ATTN_DIV_FIXTURE, ATTN_SHAPES, GPT_OSS_ATTN, GPT_OSS_ROPE, AttnHost
     from midge_amd import _lib
-    cfgs = dict(ATTN_SHAPES, gpt_oss=dict(hidden=2880, nh=64, nkv=8, hd=64, ctx=160, window=128, qk_norm=0, sinks=1))
+    cfgs = dict(ATTN_SHAPES, gpt_oss=GPT_OSS_ATTN)
     cfg = cfgs[name]
     say(f"attention_dev {name}")
     host = AttnHost(**cfg, seed=13, rope=GPT_OSS_ROPE if name == "gpt_oss" else None)
@@ -442,6 +442,20 @@ def test_attention_dev_vs_oracle(mh, name):
     rng = np.random.default_rng(14)
     xd = DevBuf(H * 4)
     bufs.append(xd)
+    # The bar per position: the reference's own divergence between its AVX2
+    # and scalar builds on this path, at these shapes and seeds. At the small
+    # shapes that stays below 3e-5 (1e-4 here). At the gpt-oss shape it is
+    # the committed per-position table (up to 1.29e-3, at position 64: a
+    # projection's last-bit change can flip a value's f16 rounding in the
+    # cache, 8 query heads share each cached value and the peaked softmax
+    # amplifies score differences); each position is held to max(1e-3,
+    # twice the reference's divergence there), the mean to twice its mean.
+    if name == "gpt_oss":
+        div = np.load(ATTN_DIV_FIXTURE)["div"]
+        assert len(div) == cfg["ctx"] - 1
+        bars, mean_bar = np.maximum(1e-3, 2.0 * div), 2.0 * float(div.mean())
+    else:
+        bars, mean_bar = np.full(cfg["ctx"] - 1, 1e-4), 2e-5
     errs = []
     for pos in range(cfg["ctx"] - 1):
         x = rng.standard_normal(H).astype(np.float32)
@@ -449,16 +463,12 @@ def test_attention_dev_vs_oracle(mh, name):
         xd.upload(x)
         _lib.call("mh_attention_dev", ctypes.byref(D), xd.ptr, pos)
         got = xd.download(np.float32, (H,))
-        # The bar is the reference's own divergence between its AVX2 and
-        # scalar builds on this path: up to 3e-5 at the small shapes; at the
-        # gpt-oss shape mean 1e-4 and up to 1.29e-3 (at position 64) over
-        # these 159 positions, where a projection's last-bit change can flip
-        # a value's f16 rounding in the cache, 8 query heads share each cached
-        # value and the peaked softmax amplifies score differences.
         err = rel_l2(got - x, want - x)
         errs.append(err)
-        assert err < (3e-3 if name == "gpt_oss" else 1e-4), pos
-    assert np.mean(errs) < (3e-4 if name == "gpt_oss" else 2e-5)
+        assert err < bars[pos], (pos, err, bars[pos])
+    errs = np.array(errs)
+    say(f"attention_dev {name}: worst {errs.max():.3g} at {int(errs.argmax())}, mean {errs.mean():.3g}")
+    assert errs.mean() < mean_bar, (errs.mean(), mean_bar)
     kcg = kc_d.download(np.uint16, host.kc.shape)
     vcg = vc_d.download(np.uint16, host.vc.shape)
     # f16 caches: equal but for the rare value on a rounding boundary of the

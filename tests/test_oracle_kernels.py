@@ -8,6 +8,8 @@ scalar path, within f32 rounding on its AVX2+FMA path).
 """
 import ctypes as C
 
+import os
+
 import numpy as np
 import pytest
 
@@ -346,6 +348,45 @@ ATTN_SHAPES = {
     "small_sliding_sinks": dict(hidden=256, nh=8, nkv=2, hd=32, ctx=48, window=16, qk_norm=0, sinks=1),
     "small_full_qknorm": dict(hidden=256, nh=4, nkv=4, hd=32, ctx=40, window=0, qk_norm=1, sinks=0),
 }
+
+
+GPT_OSS_ATTN = dict(hidden=2880, nh=64, nkv=8, hd=64, ctx=160, window=128, qk_norm=0, sinks=1)
+ATTN_DIV_FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "attn_divergence.npz")
+
+
+def attn_divergence_gptoss() -> np.ndarray:
+    """The reference's own divergence on attention() at the gpt-oss shape:
+    per decode position (159 of them, past the 128-token sliding window),
+    rel L2 of the attention output (x_out - x_in) of its AVX2 build against
+    its scalar build, each on its own f16 cache, with the seeds the GPU test
+    uses (weights 13, inputs 14). Also checks that the oracle equals the
+    scalar build bit for bit at every position (outputs and caches)."""
+    cfg = GPT_OSS_ATTN
+    a_sc, a_rf, a_or = (AttnHost(**cfg, seed=13, rope=GPT_OSS_ROPE) for _ in range(3))
+    rng = np.random.default_rng(14)
+    div = np.empty(cfg["ctx"] - 1)
+    for pos in range(cfg["ctx"] - 1):
+        x = rng.standard_normal(cfg["hidden"]).astype(np.float32)
+        xs = a_sc.run(po.ref(scalar=True).ref_attention, x, pos)
+        xr = a_rf.run(po.ref().ref_attention, x, pos)
+        xo = a_or.run(po.oracle().mo_attention, x, pos)
+        assert (xo.view(np.uint32) == xs.view(np.uint32)).all(), pos
+        assert (a_or.kc == a_sc.kc).all() and (a_or.vc == a_sc.vc).all(), pos
+        d = (xs - x).astype(np.float64)
+        div[pos] = np.linalg.norm((xr - x).astype(np.float64) - d) / np.linalg.norm(d)
+    return div
+
+
+def test_attention_divergence_fixture():
+    # the per-position AVX2-vs-scalar divergence the GPU attention test's bar
+    # is built from: recomputed from the compiled reference, equal to the
+    # committed fixture (which the GPU box reads)
+    if not po.have_ref():
+        pytest.skip("reference engine not built (oracle/_ref)")
+    div = attn_divergence_gptoss()
+    want = np.load(ATTN_DIV_FIXTURE)["div"]
+    assert div.shape == want.shape
+    assert np.allclose(div, want, rtol=1e-9, atol=0.0)
 
 
 def test_to_f16_vs_reference():
