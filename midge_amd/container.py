@@ -71,11 +71,13 @@ class DenseFile:
                 f.write(p)
 
 
-def write_experts(path: str, dt: int, table: np.ndarray) -> None:
-    """experts.midge with `table` (all layers, wt_expert_layout order) as its data."""
+def write_experts(path: str, dt: int, layers) -> None:
+    """experts.midge whose data is the concatenation of `layers` (byte arrays,
+    e.g. one per layer, in wt_expert_layout order), written as they come."""
     with open(path, "wb") as f:
         f.write(header_bytes({"midge": 1, "kind": "experts", "dt": DT_STR[dt]}))
-        f.write(np.ascontiguousarray(table, np.uint8).tobytes())
+        for t in layers:
+            f.write(memoryview(np.ascontiguousarray(t, np.uint8)))
 
 
 def read_header(path: str) -> tuple[dict, int]:

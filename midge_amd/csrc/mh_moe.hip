@@ -450,9 +450,18 @@ int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uin
     return hip_check(hipGetLastError(), "combine launch");
 }
 
+// The scaled-MFMA grouped GEMM takes a chunk once its experts average at
+// least this many assignments: its 32-token tiles are then at least a
+// quarter full. Below that the per-assignment GEMVs do no more work, and
+// they keep f32 activations (the GEMM carries them as three fp8 terms, ~12
+// significant bits each, which a small, sharply peaked model can amplify
+// to a few 1e-4 of relative error in its logits).
+constexpr int kMfmaMinPerExpert = 8;
+
 int run_expert_major(const DevLayer &L, int n, const float *xb, const int32_t *sel, const float *w, float *x,
                      const LayerBufs &b, hipStream_t s) {
-    if (prefill_mfma_ok(L)) MH_TRY(run_expert_major_mfma(L, n, xb, sel, b.ye, s));
+    if (prefill_mfma_ok(L) && (int64_t)n * L.top_k >= (int64_t)kMfmaMinPerExpert * L.n_experts)
+        MH_TRY(run_expert_major_mfma(L, n, xb, sel, b.ye, s));
     else MH_TRY(launch_experts(L, n * L.top_k, sel, nullptr, xb, b.h, b.ye, s));
     MH_LAUNCH("combine_prefill", k_combine_prefill, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s,
                        x, b.ye, sel, w, L.hidden, L.top_k, L.n_experts);
