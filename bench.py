@@ -215,6 +215,7 @@ def run_gpu(args, shape):
     if not args.no_configs:
         extra["lm_head_sample"] = lm_head_sample_probe(ev, s)
         extra["attention"] = attention_probe(ev, s)
+        extra["full_token"] = full_token_probe(ev, s, st, shape)
     for b in bufs:
         b.free()
     st.destroy()
@@ -372,6 +373,96 @@ def attention_probe(ev, s, fill: int = 1024, reps: int = 20) -> dict:
     for d in keep:
         d.free()
     return res
+
+
+def full_token_probe(ev, s, st, shape, fill: int = 256, reps: int = 10) -> dict:
+    """A whole decode token on the device at the gpt-oss-120b shape
+    (mh_forward_dev, forward() of engine/midge.c:552-565): the embedding row,
+    36 x (attention, then the MoE layer as its one-launch kernel), the final
+    rmsnorm, the int8 lm_head (201088 x 2880) and the greedy pick. Layers
+    alternate sliding (window 128) and full attention, each with its own
+    synthetic int8 q/k/v/o and f16 cache; the MoE layers are the bench's
+    resident expert stack. The caches are filled by running `fill` tokens
+    first; then `reps` tokens are HIP-event timed back to back."""
+    import ctypes as C
+
+    import midge_amd
+    from midge_amd import DT_Q8R, DevBuf, _lib, synth
+    H, V, nh, nkv, hd, NL = 2880, 201088, 64, 8, 64, shape.n_layers
+    ctx = fill + reps + 8
+    qd, kvd = nh * hd, nkv * hd
+    keep = []
+
+    def buf(n, kind, key, a=0.0, b=1.0):
+        d = DevBuf(n * 4 if kind != "i8" else n)
+        if kind == "i8":
+            _lib.call("mh_synth_i8_dev", d.ptr, n, key)
+        elif kind == "u":
+            _lib.call("mh_synth_uniform_dev", d.ptr, n, key, a, float(synth.uniform_c(a, b)))
+        else:
+            _lib.call("mh_synth_normal_dev", d.ptr, n, key, float(synth.normal_c(b)))
+        keep.append(d)
+        return d.ptr
+
+    def wt(rows, cols, key, lo=1e-4, hi=4e-4):
+        return _lib.MhWT(DT_Q8R, rows, cols, buf(rows * cols, "i8", key), buf(rows, "u", key + 1, lo, hi))
+
+    co, si = buf(ctx * hd // 2, "u", 1936, -1.0, 1.0), buf(ctx * hd // 2, "u", 1937, -1.0, 1.0)
+    layers = []
+    for l in range(NL):
+        k0 = 2000 + 40 * l
+        L = _lib.MhAttnLayer()
+        window = 128 if l % 2 == 0 else 0
+        L.hidden, L.n_heads, L.n_kv_heads, L.head_dim, L.ctx, L.window = H, nh, nkv, hd, ctx, window
+        L.qk_norm, L.sinks, L.norm_eps, L.attn_scale = 0, 1, 1e-5, 0.125
+        L.wq, L.wk, L.wv, L.wo = wt(qd, H, k0), wt(kvd, H, k0 + 2), wt(kvd, H, k0 + 4), wt(H, qd, k0 + 6)
+        L.bq, L.bk, L.bv, L.bo = (buf(qd, "n", k0 + 8, b=0.02), buf(kvd, "n", k0 + 9, b=0.02),
+                                  buf(kvd, "n", k0 + 10, b=0.02), buf(H, "n", k0 + 11, b=0.02))
+        L.attn_norm = buf(H, "u", k0 + 12, 0.5, 1.5)
+        L.sink = buf(nh, "n", k0 + 13)
+        L.rope_cos, L.rope_sin = co, si
+        cap = window if 0 < window < ctx else ctx
+        kc, vc = DevBuf(cap * kvd * 2), DevBuf(cap * kvd * 2)
+        keep += [kc, vc]
+        L.kc, L.vc = kc.ptr, vc.ptr
+        layers.append(L)
+    attn = (_lib.MhAttnLayer * NL)(*layers)
+    d = _lib.MhModelDesc()
+    d.hidden, d.vocab, d.n_layers, d.norm_eps = H, V, NL, 1e-5
+    d.embed = wt(V, H, 1900, 2e-3, 8e-3)
+    d.lm_head = wt(V, H, 1902, 1e-3, 1e-2)
+    d.final_norm = buf(H, "u", 1904, 0.5, 1.5)
+    d.attn, d.moe = attn, st._cl
+    model = C.c_void_p()
+    _lib.call("mh_model_create", C.byref(d), C.byref(model))
+    x, lg, tok = DevBuf(H * 4), DevBuf(V * 4), DevBuf(4)
+    keep += [x, lg, tok]
+    toks = np.random.default_rng(77).integers(0, V, fill + reps)
+
+    def token(i):
+        _lib.call("mh_forward_dev", model, int(toks[i]), i, x.ptr, lg.ptr, None, None)
+        _lib.call("mh_sample_dev", lg.ptr, V, 0.0, 1.0, 0.0, tok.ptr)
+
+    for i in range(fill):
+        token(i)
+    midge_amd.sync()
+    a, b = ev.event(), ev.event()
+    t0 = time.perf_counter()
+    ev.record(a, s)
+    for i in range(fill, fill + reps):
+        token(i)
+    ev.record(b, s)
+    host = (time.perf_counter() - t0) / reps * 1e3
+    ms = ev.elapsed_ms(a, b) / reps
+    midge_amd.sync()
+    _lib.call("mh_model_destroy", model)
+    for dd in keep:
+        dd.free()
+    log(f"full decode token (36 x attention + MoE, lm_head, greedy): {ms:.3f} ms")
+    return {"workload": "one decode token on the device, gpt-oss-120b shape: embedding, 36 x (attention "
+                        "(alternately sliding 128 / full) + MoE (128 MXFP4 experts, top-4)), final norm, int8 "
+                        "lm_head 201088x2880, greedy pick",
+            "ms_per_token": ms, "tok_per_s": 1e3 / ms, "host_enqueue_ms": host, "cached_positions": fill + reps}
 
 
 def reference_bench(ev, s, seconds: float = 1.0) -> dict:

@@ -236,6 +236,37 @@ int mh_stack_create(const mh_moe_layer *layers, int n_layers, int max_batch, mh_
 int mh_stack_decode(mh_stack *s, float *x, int batch, int32_t *sel, float *w, uint32_t *usage);
 int mh_stack_destroy(mh_stack *s);
 
+/* ----------------------------------------------------- decode token */
+
+/* forward() (engine/midge.c:552-565) with every tensor and activation on the
+ * device: a whole decode token. The model descriptor names the engine's
+ * tensors (Model, engine/midge.c:65-87): the embedding and lm_head matrices,
+ * the final norm, and per layer the attention layer (its f16 k/v cache and
+ * rope tables included, as mh_attention_dev takes them) and the MoE layer.
+ * Every layer's MoE must share hidden, ffn, experts and top-k. */
+typedef struct {
+    int64_t hidden, vocab;
+    int32_t n_layers;
+    float norm_eps;
+    mh_wt embed;                        /* [vocab][hidden], any dtype (wk_row) */
+    mh_wt lm_head;                      /* [vocab][hidden] */
+    const float *final_norm;            /* [hidden] */
+    const mh_attn_layer *attn;          /* [n_layers] */
+    const mh_moe_layer *moe;            /* [n_layers] */
+} mh_model_desc;
+
+typedef struct mh_model mh_model;
+/* Resolves and checks the descriptor (the arrays it points to are copied),
+ * and plans the MoE layers' one-launch kernel. */
+int mh_model_create(const mh_model_desc *d, mh_model **out);
+/* One token at position pos (its k/v go to each layer's cache slot pos %
+ * cap): x[hidden] (device) <- embedding row `token`, then per layer
+ * attention() and moe(); if logits (device [vocab]) is not NULL, the final
+ * rmsnorm and the lm_head GEMV. sel / w (device [n_layers][top_k]) get each
+ * layer's routing, or NULL. Asynchronous on the library stream. */
+int mh_forward_dev(mh_model *m, int32_t token, int32_t pos, float *x, float *logits, int32_t *sel, float *w);
+int mh_model_destroy(mh_model *m);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,13 @@ class MhAttnLayer(C.Structure):
                 ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("kc", C.c_void_p), ("vc", C.c_void_p)]
 
 
+class MhModelDesc(C.Structure):
+    """mh_model_desc: the tensors forward() reads (engine/midge.c:552-565)."""
+    _fields_ = [("hidden", C.c_int64), ("vocab", C.c_int64), ("n_layers", C.c_int32), ("norm_eps", C.c_float),
+                ("embed", MhWT), ("lm_head", MhWT), ("final_norm", C.c_void_p),
+                ("attn", C.POINTER(MhAttnLayer)), ("moe", C.POINTER(MhMoeLayer))]
+
+
 _P = C.c_void_p
 _I = C.c_int
 _I64 = C.c_int64
@@ -99,6 +106,9 @@ _SIGS = {
     "mh_stack_create": [C.POINTER(MhMoeLayer), _I, _I, C.POINTER(_P)],
     "mh_stack_decode": [_P, _P, _I, _P, _P, _P],
     "mh_stack_destroy": [_P],
+    "mh_model_create": [C.POINTER(MhModelDesc), C.POINTER(_P)],
+    "mh_forward_dev": [_P, _I, _I, _P, _P, _P, _P],
+    "mh_model_destroy": [_P],
     "mh_synth_bytes_dev": [_P, _U64, _U64],
     "mh_synth_scales_dev": [_P, _U64, _U64, _I, _I],
     "mh_synth_i8_dev": [_P, _U64, _U64],

@@ -1594,16 +1594,18 @@ int fold_stamps(const StepPlan *p, int n_layers, int nb, const Span (&spans)[NS]
 
 }  // namespace
 
-int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_t *sel, float *w,
+int step_run(StepPlan *p, const DevLayer *layers, int first, int n_layers, float *x, int32_t *sel, float *w,
              uint32_t *usage, hipStream_t s) {
     if (!p || !p->ok) return fail(MH_E_UNSUPPORTED, "decode step: no one-launch kernel for this stack");
-    const DevLayer &L0 = layers[0];
+    if (first < 0 || n_layers < 1 || first + n_layers > p->n_layers)
+        return fail(MH_E_ARG, "decode step: layers [%d, %d) outside the plan's %d", first, first + n_layers, p->n_layers);
+    const DevLayer &L0 = layers[first];
     const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two kernels
     const bool grp = p->grp && !(nm && nm[0] && nm[0] != '0');
     if (!grp && !p->flat) return fail(MH_E_UNSUPPORTED, "decode step: the vector-ALU kernel does not fit this stack");
     const TagLayout tl = tag_layout(L0);
     RouteArgs R;
-    R.layers = p->layers;
+    R.layers = p->layers + first;
     R.n_layers = n_layers;
     R.H = (int)L0.hidden;
     R.E = L0.n_experts;

@@ -116,7 +116,9 @@ struct StepPlan;
 int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out);
 void step_plan_destroy(StepPlan *p);
 bool step_plan_ok(const StepPlan *p);
-int step_run(StepPlan *p, const DevLayer *layers, int n_layers, float *x, int32_t *sel, float *w,
+// Runs layers [first, first + n_layers) of a plan in one launch; sel, w and
+// usage are indexed from layer `first`.
+int step_run(StepPlan *p, const DevLayer *layers, int first, int n_layers, float *x, int32_t *sel, float *w,
              uint32_t *usage, hipStream_t s);
 
 // Kernel timing (mh_profile_*): while enabled, every launch made through

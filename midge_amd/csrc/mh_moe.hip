@@ -549,6 +549,29 @@ struct mh_stack {
     mh::StepPlan *plan = nullptr;   // one-launch batch-1 path (null/ineligible -> per-layer launches)
 };
 
+namespace mh {
+
+// Layer l of a stack for one token on device x (the one-launch kernel when
+// the plan holds, else the per-layer launches); sel, w (device [k]) and
+// usage (device [E]) are this layer's rows, or null.
+int stack_decode_layer(mh_stack *st, int l, float *x, int32_t *sel, float *w, uint32_t *usage) {
+    hipStream_t s = stream();
+    const char *nf = getenv("MIDGE_HIP_NO_FUSED");
+    if (!(nf && *nf && *nf != '0') && step_plan_ok(st->plan)) {
+        int rc = step_run(st->plan, st->layers.data(), l, 1, x, sel, w, usage, s);
+        if (rc != MH_E_UNSUPPORTED) return rc;
+        clear_error();
+    }
+    const DevLayer &L = st->layers[(size_t)l];
+    LayerBufs b;
+    MH_TRY(layer_bufs(L, 1, &b));
+    if (sel) b.sel = sel;
+    if (w) b.w = w;
+    return run_decode_layer(L, x, 1, b, usage, s);
+}
+
+}  // namespace mh
+
 using namespace mh;
 
 extern "C" {
@@ -712,7 +735,7 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
     hipStream_t s = stream();
     const char *nf = getenv("MIDGE_HIP_NO_FUSED");   // per call, so callers can A/B the two paths
     if (batch == 1 && !(nf && *nf && *nf != '0') && step_plan_ok(st->plan)) {
-        int rc = step_run(st->plan, st->layers.data(), nl, x, sel, w, usage, s);
+        int rc = step_run(st->plan, st->layers.data(), 0, nl, x, sel, w, usage, s);
         if (rc != MH_E_UNSUPPORTED) return rc;
         clear_error();   // shape this device cannot run in one launch: per-layer launches below
     }

@@ -303,13 +303,13 @@ class AttnHost:
     """One attention layer on host arrays (q8r projections) with its f16
     caches, as the oracle and the compiled reference take it."""
 
-    def __init__(self, hidden, nh, nkv, hd, ctx, window, qk_norm, sinks, seed, rope=None):
+    def __init__(self, hidden, nh, nkv, hd, ctx, window, qk_norm, sinks, seed, rope=None, wscale=(5e-4, 2.5e-3)):
         rng = np.random.default_rng(seed)
         self.keep = []
 
-        def q8(rows, cols):
+        def q8(rows, cols):   # row scales uniform in wscale
             w = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
-            s = (rng.random(rows) * 2e-3 + 5e-4).astype(np.float32)
+            s = (rng.random(rows) * (wscale[1] - wscale[0]) + wscale[0]).astype(np.float32)
             self.keep += [w, s]
             return po.MhWT(DT_Q8R, rows, cols, w.ctypes.data, s.ctypes.data)
 
