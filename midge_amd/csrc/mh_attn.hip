@@ -161,24 +161,15 @@ int launch_qkv_t(const DevWT *w, const float *x, float *const *y, hipStream_t s,
 }
 constexpr int kHeadThreads = 1024;   // per query head: positions, then head_dim x position groups
 
-// wk_to_f16 (engine/mkern.h:261-273): round to nearest even; below the
-// normal range a signed zero; at or past the top (inf, NaN) a signed inf.
+// The cache's f16 as wk_to_f16 (engine/mkern.h:261-273) makes it: the
+// hardware's round-to-nearest-even conversion (which already overflows to
+// inf from 65520 up), except that magnitudes below the f16 normal range
+// become a signed zero and NaN becomes a signed inf.
 __device__ __forceinline__ uint16_t to_f16_ref(float f) {
-    const uint32_t x = __float_as_uint(f);
-    const uint32_t sign = (x >> 16) & 0x8000u;
-    int e = (int)((x >> 23) & 0xff) - 112;
-    const uint32_t man = x & 0x7fffffu;
-    if (e <= 0) return (uint16_t)sign;
-    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
-    uint32_t m = man >> 13;
-    const uint32_t rem = man & 0x1fffu;
-    if (rem > 0x1000u || (rem == 0x1000u && (m & 1u))) {
-        if (++m == 0x400u) {
-            m = 0;
-            if (++e >= 31) return (uint16_t)(sign | 0x7c00u);
-        }
-    }
-    return (uint16_t)(sign | ((uint32_t)e << 10) | m);
+    const float a = fabsf(f);
+    const uint16_t sign = (uint16_t)((__float_as_uint(f) >> 16) & 0x8000u);
+    if (!(a >= 0x1p-14f)) return a != a ? (uint16_t)(sign | 0x7c00u) : sign;
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
 struct PrepArgs {

@@ -400,6 +400,26 @@ def test_to_f16_vs_reference():
         assert po.oracle().mo_to_f16(float(v)) == po.ref().ref_to_f16_attn(float(v)), v
 
 
+def test_device_f16_rule_equals_the_cache_conversion():
+    # the attention kernel stores the f16 cache as: IEEE round-to-nearest-even
+    # (the hardware conversion), except |f| < 2^-14 -> signed zero and NaN ->
+    # signed inf; that rule equals the oracle's wk_to_f16 everywhere
+    rng = np.random.default_rng(81)
+    vals = np.concatenate([rng.standard_normal(40000) * 10.0 ** rng.integers(-12, 7, 40000),
+                           np.frombuffer(rng.bytes(4 * 40000), np.float32),
+                           [0.0, -0.0, 65504.0, 65519.99, 65520.0, -65520.0, 2.0 ** -14, -(2.0 ** -14),
+                            np.nextafter(np.float32(2.0 ** -14), np.float32(0)), 5.96e-8, np.inf, -np.inf, np.nan,
+                            1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11]]).astype(np.float32)
+    a = np.abs(vals)
+    with np.errstate(over="ignore", invalid="ignore"):
+        rule = vals.astype(np.float16).view(np.uint16).copy()
+    sign = ((vals.view(np.uint32) >> 16) & 0x8000).astype(np.uint16)
+    small = ~(a >= np.float32(2.0 ** -14))
+    rule[small] = np.where(np.isnan(vals[small]), sign[small] | 0x7C00, sign[small])
+    want = np.array([po.oracle().mo_to_f16(float(v)) for v in vals], np.uint16)
+    assert (rule == want).all(), vals[rule != want][:8]
+
+
 @pytest.mark.parametrize("rope", [dict(), GPT_OSS_ROPE, dict(GPT_OSS_ROPE, truncate=1)])
 def test_rope_tables_vs_reference(rope):
     if not po.have_ref():
