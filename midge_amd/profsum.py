@@ -5,6 +5,11 @@ traffic), so the figures quoted by bench.py can be traced to a profiler run.
     python -m midge_amd.profsum traffic <fetch counter_collection.csv> <write counter_collection.csv>
                                         --kernel REGEX --copy-bytes N [--json OUT]
 
+    python -m midge_amd.profsum counters <counter_collection.csv> --kernel REGEX
+
+`counters` averages every counter of the file per dispatch over the
+dispatches whose kernel name matches REGEX (one line per kernel name).
+
 `traffic` averages FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the
 dispatches whose kernel name matches REGEX, and scales each by the ratio the
 same counter shows for the runtime's device-to-device copy kernel of N bytes
@@ -73,6 +78,20 @@ def traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int) -> dic
     return res
 
 
+def counters(path: str, kernel: str) -> str:
+    acc: dict[tuple[str, str], list[float]] = defaultdict(list)
+    for r in _rows(path):
+        k = _col(r, "Kernel_Name", "KERNEL_NAME")
+        if re.search(kernel, k):
+            acc[(k, _col(r, "Counter_Name", "COUNTER_NAME"))].append(float(_col(r, "Counter_Value", "COUNTER_VALUE")))
+    if not acc:
+        raise SystemExit(f"no dispatch of /{kernel}/ in {path}")
+    out = ["| kernel | counter | dispatches | mean per dispatch |", "|---|---|---|---|"]
+    for (k, c), vs in sorted(acc.items()):
+        out.append(f"| {k.replace('|', chr(92) + '|')[:70]} | {c} | {len(vs)} | {sum(vs) / len(vs):.6g} |")
+    return "\n".join(out)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -85,9 +104,14 @@ def main() -> int:
     b.add_argument("--kernel", required=True)
     b.add_argument("--copy-bytes", type=int, required=True)
     b.add_argument("--json")
+    c = sub.add_parser("counters")
+    c.add_argument("csv")
+    c.add_argument("--kernel", required=True)
     args = ap.parse_args()
     if args.cmd == "stats":
         print(stats(args.csv, args.top))
+    elif args.cmd == "counters":
+        print(counters(args.csv, args.kernel))
     else:
         r = traffic(args.fetch_csv, args.write_csv, args.kernel, args.copy_bytes)
         if args.json:
