@@ -222,7 +222,54 @@ def run_gpu(args, shape):
     return ms, unique, kern, dom, extra
 
 
-def gemv_probe(ev, s, rows: int = 524288, cols: int = 2880, reps: int = 8, sustain: int = 30) -> dict:
+class DeviceSampler:
+    """Samples the GPU's power, clock level and temperatures from sysfs
+    (amdgpu hwmon and pp_dpm_sclk of the first card that has them) on a
+    background thread, every `period` seconds, with host timestamps."""
+
+    def __init__(self, period: float = 0.002):
+        import glob
+        import threading
+        self.period, self.samples, self.stop_ev = period, [], threading.Event()
+        self.dev = next((d for d in sorted(glob.glob("/sys/class/drm/card*/device"))
+                         if glob.glob(d + "/hwmon/hwmon*/power1_input")), None)
+        self.hw = glob.glob(self.dev + "/hwmon/hwmon*")[0] if self.dev else None
+        self.th = threading.Thread(target=self._run, daemon=True)
+
+    def _read(self, path: str) -> str | None:
+        try:
+            with open(path) as f:
+                return f.read()
+        except OSError:
+            return None
+
+    def _run(self) -> None:
+        while not self.stop_ev.is_set():
+            t = time.perf_counter()
+            p = self._read(self.hw + "/power1_input")
+            t2, t3 = self._read(self.hw + "/temp2_input"), self._read(self.hw + "/temp3_input")
+            sclk = None
+            txt = self._read(self.dev + "/pp_dpm_sclk") or ""
+            for ln in txt.splitlines():
+                if ln.strip().endswith("*"):
+                    sclk = float(ln.split(":")[1].strip().rstrip("*").strip().lower().rstrip("mhz"))
+            self.samples.append((t, float(p) / 1e6 if p else None, sclk, float(t2) / 1e3 if t2 else None,
+                                 float(t3) / 1e3 if t3 else None))
+            self.stop_ev.wait(self.period)
+
+    def __enter__(self):
+        if self.hw:
+            self.th.start()
+        return self
+
+    def __exit__(self, *a):
+        self.stop_ev.set()
+        if self.hw:
+            self.th.join()
+
+
+def gemv_probe(ev, s, rows: int = 524288, cols: int = 2880, reps: int = 8, sustain: int = 30,
+               sustain_s: float = 0.8) -> dict:
     """The MXFP4 GEMV engine alone: y = W x over a 524288 x 2880 matrix
     (849 MB of nibbles + f16 scales, over three times the 256 MB Infinity
     Cache).
@@ -230,38 +277,86 @@ def gemv_probe(ev, s, rows: int = 524288, cols: int = 2880, reps: int = 8, susta
     `avg_us` is per launch over `reps` back-to-back launches (~1.2 ms)
     between one pair of HIP events, the few microseconds between launches
     included. A longer back-to-back run (`sustain` launches, ~4.5 ms of
-    streaming) is reported beside it, timed in groups of 5: under sustained
-    streaming at this rate the device slows down after ~2 ms (by ~20% in
-    kernel traces), so its first and last groups are given separately."""
+    streaming) is reported beside it, timed in groups of 5, first and last
+    group. `sustained_1s` streams for `sustain_s` seconds, timed in groups of
+    10, with the device's power, clock level and temperatures sampled from
+    sysfs meanwhile, in windows of 5 ms (the first 50 ms) and 50 ms;
+    `control_2x` does the same over a
+    matrix twice as large (1.7 GB), so that no cache holds a useful part of
+    either."""
     import midge_amd
     from midge_amd import DT_MXFP4, DevBuf, _lib, synth
     from midge_amd.kern import WT, matvec_dev
-    data, sc = DevBuf(rows * cols // 2), DevBuf(rows * cols // 32 * 2)
-    x, y = DevBuf(cols * 4), DevBuf(rows * 4)
-    _lib.call("mh_synth_bytes_dev", data.ptr, rows * cols // 2, 11)
-    _lib.call("mh_synth_scales_dev", sc.ptr, rows * cols // 32, 12, -8, -4)
+
+    def make(r: int):
+        data, sc = DevBuf(r * cols // 2), DevBuf(r * cols // 32 * 2)
+        y = DevBuf(r * 4)
+        _lib.call("mh_synth_bytes_dev", data.ptr, r * cols // 2, 11)
+        _lib.call("mh_synth_scales_dev", sc.ptr, r * cols // 32, 12, -8, -4)
+        return WT(DT_MXFP4, r, cols, data.ptr, sc.ptr), [data, sc, y], y
+
+    x = DevBuf(cols * 4)
     _lib.call("mh_synth_normal_dev", x.ptr, cols, 13, float(synth.normal_c(1.0)))
-    t = WT(DT_MXFP4, rows, cols, data.ptr, sc.ptr)
+    t, bufs, y = make(rows)
     for _ in range(3):
         matvec_dev(t, x, y)
     midge_amd.sync()
 
-    def launches(n: int, group: int) -> list:
+    def launches(tt, yy, n: int, group: int) -> list:
         """Per-launch us of each group of `group` back-to-back launches."""
         evs = [ev.event() for _ in range(n // group + 1)]
         ev.record(evs[0], s)
         for i in range(n // group):
             for _ in range(group):
-                matvec_dev(t, x, y)
+                matvec_dev(tt, x, yy)
             ev.record(evs[i + 1], s)
         midge_amd.sync()
         return [1e3 * ev.elapsed_ms(evs[i], evs[i + 1]) / group for i in range(n // group)]
 
-    avg = launches(reps, reps)[0]
+    def nbytes_of(r: int) -> int:
+        return r * cols // 2 + r * cols // 32 * 2 + cols * 4 + r * 4
+
+    def sustained(tt, yy, r: int) -> dict:
+        """`sustain_s` seconds of back-to-back launches with device samples,
+        folded into 50 ms windows of GPU time."""
+        group = 10
+        n = max(group, int(sustain_s / (nbytes_of(r) / 5.5e12)) // group * group)
+        time.sleep(0.3)   # idle first
+        with DeviceSampler() as smp:
+            time.sleep(0.02)
+            t0 = time.perf_counter()
+            per = launches(tt, yy, n, group)
+            time.sleep(0.02)
+        out, acc, w0, gt = [], 0.0, 0, 0.0
+        for i, us in enumerate(per):
+            acc += us * group
+            if acc >= (5e3 if gt < 50e3 else 50e3) or i == len(per) - 1:   # 5 ms windows for the first 50 ms
+                gt += acc
+                g0 = sum(per[:w0]) * group * 1e-6   # window start, s of GPU time
+                g1 = g0 + acc * 1e-6
+                sm = [q for q in smp.samples if t0 + g0 <= q[0] < t0 + g1]
+
+                def mean(k):
+                    v = [q[k] for q in sm if q[k] is not None]
+                    return round(sum(v) / len(v), 1) if v else None
+
+                out.append({"t_ms": round(g0 * 1e3, 1), "GBps": round(nbytes_of(r) * (i + 1 - w0) * group /
+                                                                      (acc * 1e-6) / 1e9, 1),
+                            "power_W": mean(1), "sclk_MHz": mean(2), "temp2_C": mean(3), "temp3_C": mean(4),
+                            "samples": len(sm)})
+                acc, w0 = 0.0, i + 1
+        return {"launches": n, "bytes_per_launch": nbytes_of(r), "windows": out}
+
+    avg = launches(t, y, reps, reps)[0]
     time.sleep(0.2)
-    long = launches(sustain, 5)
-    nbytes = rows * cols // 2 + rows * cols // 32 * 2 + cols * 4 + rows * 4
-    for d in (data, sc, x, y):
+    long = launches(t, y, sustain, 5)
+    nbytes = nbytes_of(rows)
+    sus = sustained(t, y, rows)
+    for d in bufs:
+        d.free()
+    t2, bufs2, y2 = make(2 * rows)
+    ctl = sustained(t2, y2, 2 * rows)
+    for d in bufs2 + [x]:
         d.free()
     gbs = nbytes / (avg * 1e-6) / 1e9
     first, last = long[0], long[-1]
@@ -269,7 +364,8 @@ def gemv_probe(ev, s, rows: int = 524288, cols: int = 2880, reps: int = 8, susta
             "GBps": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS,
             "sustained": {"launches": sustain, "first5_us": first, "last5_us": last,
                           "first5_frac_of_peak": nbytes / (first * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                          "last5_frac_of_peak": nbytes / (last * 1e-6) / 1e9 / HBM_PEAK_GBS}}
+                          "last5_frac_of_peak": nbytes / (last * 1e-6) / 1e9 / HBM_PEAK_GBS},
+            "sustained_1s": sus, "control_2x": ctl}
 
 
 def lm_head_sample_probe(ev, s, reps: int = 20) -> dict:
