@@ -321,6 +321,125 @@ k_gemm_q8r(const int8_t *__restrict__ W, const float *__restrict__ S, const uint
     }
 }
 
+// Long int8 matrices (the lm_head) at batch 2+: a wave owns tiles of 16 MT
+// rows, an equal contiguous share of them. Per K super-step of 1024 columns
+// it loads each of its rows' next kilobyte with one 64-lane instruction
+// (whole rows per instruction: the fastest HBM pattern; the matrix-core
+// operand layout, 16 rows x 64 bytes per instruction, streams ~25% slower),
+// writes them to its private LDS buffer at a row stride of 1040 bytes (the
+// operand lanes' 16 rows then fall in distinct banks), issues the next
+// super-step's loads, and runs the step's matrix instructions from LDS.
+// Digits as in k_gemm_q8r (L2 hits), DB chunks ahead. (lm_head 201088 x
+// 2880 at batch 32: 252 us with the operand-layout loads, 226 us with this
+// kernel at MT = 1, 214 at MT = 2, 208 with the digits four chunks ahead.)
+constexpr int kQ8SS = 1024;        // bytes of a row per super-step (16 chunks of 64)
+constexpr int kQ8RowLds = 1040;    // LDS row stride
+constexpr int kQ8RowWaves = 4;     // waves per block (each with its own buffer)
+
+template <int NT, int MT>
+__global__ void __launch_bounds__(64 * kQ8RowWaves, MT == 1 ? 2 : 1)
+k_gemm_q8r_rows(const int8_t *__restrict__ W, const float *__restrict__ S, const uint8_t *__restrict__ xq,
+                const int *__restrict__ shift, const float *__restrict__ X, float *__restrict__ Y, int R, int K,
+                int batch) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kQ8RowWaves][16 * MT * kQ8RowLds];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = blockIdx.y, KC = K >> 6, NSS = (K + kQ8SS - 1) / kQ8SS;
+    const int i = lane & 15, g = lane >> 4;
+    const int64_t T = (R + 16 * MT - 1) / (16 * MT), nw = (int64_t)gridDim.x * kQ8RowWaves, gw = (int64_t)blockIdx.x * kQ8RowWaves + wave;
+    const int tbeg = (int)(gw * T / nw), tend = (int)((gw + 1) * T / nw);
+    uint8_t *buf = lds[wave];
+    const mh_gbytes bp = mh_global(xq + ((size_t)grp * KC * 3 * NT * 64 + lane) * 16);
+    constexpr int DB = 4;   // digit chunks in flight (their L2 latency exceeds a chunk's math)
+    mh_u4 st[16 * MT];   // one super-step of the 16 MT rows: row j's bytes 16 lane .. +15
+    mh_u4 b[DB][3 * NT];
+    auto load_b = [&](int set, int kc) {
+#pragma unroll
+        for (int j = 0; j < 3 * NT; ++j)
+            b[set][j] = *(const mh_u4 __attribute__((address_space(1))) *)(bp + ((size_t)kc * 3 * NT + j) * 1024);
+    };
+    for (int tile = tbeg; tile < tend; ++tile) {
+        const int r0 = tile * 16 * MT;
+        auto load_ss = [&](int ss) {
+            const int o = ss * kQ8SS + 16 * lane;
+#pragma unroll
+            for (int j = 0; j < 16 * MT; ++j) {
+                const int r = min(r0 + j, R - 1);
+                st[j] = o < K ? mh_load16(mh_global(W + (size_t)r * K + o)) : mh_u4{0u, 0u, 0u, 0u};
+            }
+        };
+        mh_i4 acc[MT][NT][3];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+                for (int d = 0; d < 3; ++d) acc[m][n][d] = mh_i4{0, 0, 0, 0};
+#pragma unroll
+        for (int d = 0; d + 1 < DB; ++d) load_b(d, min(d, KC - 1));
+        load_ss(0);
+        for (int ss = 0; ss < NSS; ++ss) {
+            // this super-step's rows into LDS (the wave's own LDS accesses
+            // complete in order: the last step's reads are done), then the
+            // next super-step's loads
+#pragma unroll
+            for (int j = 0; j < 16 * MT; ++j) *(mh_u4 *)(buf + j * kQ8RowLds + 16 * lane) = st[j];
+            if (ss + 1 < NSS) load_ss(ss + 1);
+            const int nc = min(16, KC - 16 * ss);
+            const uint8_t *ab = buf + i * kQ8RowLds + 16 * g;
+            for (int c = 0; c < nc; c += DB) {
+#pragma unroll
+                for (int h = 0; h < DB; ++h) {
+                    if (c + h >= nc) break;
+                    const int kc = 16 * ss + c + h;   // its digits are in set kc % DB = h
+                    load_b((h + DB - 1) % DB, min(kc + DB - 1, KC - 1));
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const mh_u4 a = *(const mh_u4 *)(ab + 16 * m * kQ8RowLds + 64 * (c + h));
+#pragma unroll
+                        for (int n = 0; n < NT; ++n)
+#pragma unroll
+                            for (int d = 0; d < 3; ++d)
+                                acc[m][n][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                    (mh_i4)a, (mh_i4)b[h][d * NT + n], acc[m][n][d], 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const int col = grp * kQ8Cols + 16 * n + i;
+            if (col >= batch) continue;
+            const int sh = shift[col];
+            float *yc = Y + (size_t)col * R;
+            if (sh == kQ8NonFinite) {
+                // a column holding inf or nan: the plain f32 sum, so the
+                // pattern of infinities and nans is that of mv_q8r
+                const float *xc = X + (size_t)col * K;
+#pragma unroll 1
+                for (int q = 0; q < 4 * MT; ++q) {
+                    const int row = r0 + 16 * (q >> 2) + 4 * g + (q & 3);
+                    if (row >= R) continue;
+                    const int8_t *wr = W + (size_t)row * K;
+                    float t = 0.f;
+                    for (int k = 0; k < K; ++k) t = __builtin_fmaf((float)wr[k], xc[k], t);
+                    yc[row] = t * S[row];
+                }
+                continue;
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int row = r0 + 16 * m + 4 * g + q;
+                    if (row >= R) continue;
+                    const float t = (float)acc[m][n][0][q] * 65536.f +
+                                    ((float)acc[m][n][1][q] * 256.f + (float)acc[m][n][2][q]);
+                    yc[row] = ldexpf(t, sh) * S[row];
+                }
+        }
+    }
+}
+
 // ------------------------------------------------------------ dequant
 
 // out[i][c] = W[r0+i][c] dequantized, bit-exact with wk_row.
@@ -433,7 +552,17 @@ int launch_gemm_q8r(const DevWT &w, const float *x, float *y, int batch, hipStre
         MH_LAUNCH("gemm_q8r", kern, dim3((unsigned)nb, (unsigned)groups), dim3(threads), 0, s,
                   (const int8_t *)w.data, (const float *)w.scales, xq, sh, x, y, (int)R, (int)K, batch);
     };
-    if (longm) {
+    const char *nl = getenv("MIDGE_HIP_Q8_NO_ROWS");   // per call: A/B against the register-operand kernel
+    if (longm && !(nl && *nl && *nl != '0')) {
+        // one block of 4 waves per CU (133 KB of LDS), each wave 32-row tiles
+        const int64_t nb = std::min<int64_t>((R + 31) / 32 / kQ8RowWaves + 1, (int64_t)device_cus());
+        auto go2 = [&](auto kern) {
+            MH_LAUNCH("gemm_q8r_rows", kern, dim3((unsigned)nb, (unsigned)groups), dim3(64 * kQ8RowWaves), 0, s,
+                      (const int8_t *)w.data, (const float *)w.scales, xq, sh, x, y, (int)R, (int)K, batch);
+        };
+        if (NT == 2) go2(k_gemm_q8r_rows<2, 2>);
+        else go2(k_gemm_q8r_rows<1, 2>);
+    } else if (longm) {
         if (NT == 2) go(k_gemm_q8r<2, Q8Long>, Q8Long::rows, Q8Long::threads);
         else go(k_gemm_q8r<1, Q8Long>, Q8Long::rows, Q8Long::threads);
     } else {
