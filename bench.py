@@ -400,6 +400,22 @@ def lm_head_sample_probe(ev, s, reps: int = 20) -> dict:
             token(i)
         ev.record(b, s)
         res[name + "_us"] = 1e3 * ev.elapsed_ms(a, b) / reps
+    # sample() alone at temperature 1 / top-p 0.9 on normal logits of other
+    # spreads: the nucleus from a few tokens (20) to most of the vocabulary
+    # (0.2), which decides the selection's way (fast list, sorted
+    # candidates, radix select)
+    alone = {}
+    for sd in (20.0, 6.0, 3.0, 0.2):
+        _lib.call("mh_synth_normal_dev", lg.ptr, V, 915, float(synth.normal_c(sd)))
+        sample_dev(lg, V, 1.0, 0.9, 0.5, out)
+        midge_amd.sync()
+        a, b = ev.event(), ev.event()
+        ev.record(a, s)
+        for i in range(10):
+            sample_dev(lg, V, 1.0, 0.9, (i * 0.618034) % 1.0, out)
+        ev.record(b, s)
+        alone[f"sd{sd:g}_us"] = 1e3 * ev.elapsed_ms(a, b) / 10
+    res["sample_alone_temp1_topp0.9"] = alone
     midge_amd.sync()
     for d in (w, sc, nw, x, xb, lg, out):
         d.free()

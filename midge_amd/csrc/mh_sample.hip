@@ -18,30 +18,44 @@
 // (blocks publish with device-scope stores, the last one is found by a
 // counter it resets):
 //   k_samp_max      per-block maxima; last block: the maximum (greedy: the
-//                   answer). Block 0 also clears the histogram.
-//   k_samp_exp      e = expf((l - max) / temp): per-block f64 sums and a
-//                   histogram of the nonzero e over their top 12 bits
-//                   (count, f32 mass). Last block: den = (float) of the f64
-//                   sum, and the candidate threshold T: the highest bin
-//                   whose mass from the top reaches topp * den by a margin
-//                   that covers the histogram's f32 rounding; p >= RN(lower
-//                   edge / den) then holds every token of those bins
-//                   (division is monotone).
-//   k_samp_select   the ids of the tokens with p >= T (a prefix of the
-//                   sorted order whatever the ids, so it holds the nucleus
-//                   if its mass reaches topp). Last block: if they fit
-//                   (<= kCap) they are sorted in LDS (bitonic, by falling p
-//                   then id), scanned in f64, and the nucleus and the pick
-//                   read off. Otherwise (a flat distribution, or topp close
-//                   to 1, where every block has stored p instead) an exact
-//                   radix select over all V: four histogram levels over p's
-//                   bits with f64 masses (one histogram per wave, then added
-//                   in a fixed order) find where the running sum crosses
-//                   topp, then u * cum; a count over index order finds the
-//                   token among equal p.
+//                   answer). Block 0 also clears the candidate counts.
+//   k_samp_topp     every block: e = expf((l - max) / temp) of its tokens,
+//                   their f64 sum, a histogram of e over its top 12 bits
+//                   from 2^-40 up (count, f32 mass; stored per block), and
+//                   the ids of its tokens with e >= tc = (1 - topp) / 2V,
+//                   appended to the fast list. The last block: den =
+//                   (float) of the f64 sum, then the fast path over the
+//                   list (every token left out has p at most the list's
+//                   smallest, so the list above that p is the head of the
+//                   whole order; since den >= 1 and the tokens left out
+//                   carry at most half of 1 - topp, it usually holds the
+//                   nucleus):
+//       <= 64 tokens  one wave: ranked with cross-lane reads, and the
+//                     reference's own loops (the f64 running sum in order,
+//                     the nucleus, the draw) in one lane;
+//       <= kCapF      the block: a histogram of the list's p cuts it to the
+//                     bins whose mass reaches topp, which are sorted in LDS.
+//                   Taken when the nucleus ends above the list's smallest p.
+//   k_samp_select   nothing if the fast path picked. Otherwise every block
+//                   finds the candidate threshold T from the stored
+//                   histograms (the highest bin whose mass from the top
+//                   reaches topp * den by a margin that covers the f32
+//                   rounding; p >= RN(lower edge / den) holds every token of
+//                   those bins, division being monotone) and gathers its
+//                   tokens with p >= T. Last block: if they fit (<= kCap)
+//                   they are sorted in LDS (bitonic, by falling p then id),
+//                   scanned in f64, and the nucleus and the pick read off.
+//                   Otherwise (a flat distribution, or topp close to 1,
+//                   where every block has stored p instead) an exact radix
+//                   select over all V: four histogram levels over p's bits
+//                   with f64 masses (one histogram per wave, then added in a
+//                   fixed order) find where the running sum crosses topp,
+//                   then u * cum; a count over index order finds the token
+//                   among equal p.
 //
 // Rounding: the reference adds the sorted probabilities one by one in f64;
-// here the f64 sums run in another order, which moves a sum by a few units
+// so does the one-wave fast path, but elsewhere the f64 sums run in another
+// order, which moves a sum by a few units
 // of 2^-53 relative, so a pick can differ only when u * cum or topp falls
 // that close to a running sum.
 #include "mh_internal.h"
@@ -50,11 +64,13 @@ namespace mh {
 namespace {
 
 constexpr int kSampThreads = 256;
-constexpr int kSampBlocks = 256;   // blocks of the first two launches
-constexpr int kSelThreads = 1024;  // the select launch and its last block
+constexpr int kSampBlocks = 256;   // blocks of the max launch
+constexpr int kSelThreads = 1024;  // the top-p launch and its last block
 constexpr int kSelBlocks = 64;
-constexpr int kBins = 1024;        // e histogram: bits(e) >> 20, e in [0, 1]
+constexpr int kHLo = 87 << 3;      // e histogram: bins bits(e) >> 20 from 2^-40 (e in [2^-40, 1])
+constexpr int kHB = 1024 - kHLo;
 constexpr int kCap = 8192;         // candidates the one-block sort takes
+constexpr int kCapF = 1024;        // candidates the fast path ranks (one per thread)
 constexpr int kRadixBins = 256;    // bins per radix level (8 bits)
 
 struct MaxIdx {
@@ -65,19 +81,19 @@ struct MaxIdx {
 // The workspace of one sample call (device memory): a fixed head, then p
 // (V floats) when the radix select needs it.
 struct SampWs {
-    uint64_t part[kSampBlocks];   // per-block maxima (MaxIdx as bits)
-    double dsum[kSampBlocks];     // per-block f64 sums of e
-    unsigned hcnt[kBins];         // nonzero e per bin
-    float hmass[kBins];           // their mass (f32: only steers T)
-    float mx;                     // the maximum logit
-    float den;                    // (float) of the f64 sum of e
-    float tp;                     // the candidate threshold T
-    int radix;                    // 1: the candidates cannot fit; p is stored
-    unsigned done[3];             // last-block counters, one per launch
-    unsigned ncand;               // tokens with p >= T
+    uint64_t part[kSampBlocks];     // per-block maxima (MaxIdx as bits)
+    double dsum[kSelBlocks];        // per-block f64 sums of e
+    unsigned bcnt[kSelBlocks][kHB]; // per-block histograms of e: counts
+    float bmass[kSelBlocks][kHB];   // and masses (f32: they only steer T)
+    float mx;                       // the maximum logit
+    float den;                      // (float) of the f64 sum of e
+    int fast;                       // 1: the fast path picked (the select launch has nothing to do)
+    unsigned done[3];               // last-block counters, one per launch
+    unsigned ncand;                 // tokens with e >= tc (the fast list)
+    unsigned nsel;                  // tokens with p >= T (the select launch's list)
     unsigned pad[56];
-    int cand[kCap];               // their ids (the first kCap)
-    float p[1];                   // [V] (only when radix)
+    int cand[kCap];                 // the fast list (the first kCapF), then the select launch's (the first kCap)
+    alignas(16) float p[4];         // [V] (only when radix; 16-byte aligned for the block scans)
 };
 constexpr uint64_t kWsHead = offsetof(SampWs, p);
 
@@ -199,15 +215,12 @@ __device__ int block_scan_int(int v, int *total) {
 
 // Per-block maxima of logits[V] (grid-stride); the last block takes the
 // maximum, with the reference loop's index-0 rule, and writes the greedy
-// answer. Block 0 clears the histogram and the candidate count.
+// answer. Block 0 clears the candidate counts.
 __global__ void __launch_bounds__(kSampThreads) k_samp_max(const float *__restrict__ lg, int V, SampWs *ws,
                                                            int32_t *__restrict__ greedy_out) {
-    if (blockIdx.x == 0) {
-        for (int b = threadIdx.x; b < kBins; b += kSampThreads) {
-            ws->hcnt[b] = 0;
-            ws->hmass[b] = 0.f;
-        }
-        if (threadIdx.x == 0) ws->ncand = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        ws->ncand = 0;
+        ws->nsel = 0;
     }
     MaxIdx m{-INFINITY, INT32_MAX};
     for (int i = blockIdx.x * kSampThreads + threadIdx.x; i < V; i += gridDim.x * kSampThreads)
@@ -225,97 +238,9 @@ __global__ void __launch_bounds__(kSampThreads) k_samp_max(const float *__restri
     }
 }
 
-// e, its per-block f64 sums and the e histogram (per block in LDS, then
-// added to the global one); the last block: den and the threshold.
-__global__ void __launch_bounds__(kSampThreads) k_samp_exp(const float *__restrict__ lg, int V, float temp,
-                                                           float topp, SampWs *ws) {
-    __shared__ unsigned s_cnt[kBins];
-    __shared__ float s_mass[kBins];
-    __shared__ double sd[kSampThreads / 64];
-    for (int b = threadIdx.x; b < kBins; b += kSampThreads) {
-        s_cnt[b] = 0;
-        s_mass[b] = 0.f;
-    }
-    const float mx = ws->mx;
-    __syncthreads();
-    double s = 0;
-    for (int i = blockIdx.x * kSampThreads + threadIdx.x; i < V; i += gridDim.x * kSampThreads) {
-        const float e = samp_e(lg[i], mx, temp);
-        s += e;
-        if (e != 0.f) {
-            const int b = min((int)(__float_as_uint(e) >> 20), kBins - 1);   // (NaN: the top bin)
-            atomicAdd(&s_cnt[b], 1u);
-            atomicAdd(&s_mass[b], e);
-        }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    if ((threadIdx.x & 63) == 0) sd[threadIdx.x >> 6] = s;
-    __syncthreads();
-    for (int b = threadIdx.x; b < kBins; b += kSampThreads) {
-        if (s_cnt[b]) {
-            atomicAdd(&ws->hcnt[b], s_cnt[b]);
-            atomicAdd(&ws->hmass[b], s_mass[b]);
-        }
-    }
-    if (threadIdx.x == 0) {
-        double t = 0;
-        for (int w = 0; w < kSampThreads / 64; ++w) t += sd[w];
-        st_agent(&ws->dsum[blockIdx.x], t);
-    }
-    if (!last_block(&ws->done[1]) || threadIdx.x >= 64) return;
-    // the first wave: den (lane l adds blocks l, l + 64, ... in order, then a
-    // butterfly: every lane gets the same bits)
-    const int lane = threadIdx.x;
-    double d = 0;
-    for (int b = lane; b < (int)gridDim.x; b += 64) d += ld_agent(&ws->dsum[b]);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) d += __shfl_xor(d, o, 64);
-    const float den = (float)d;
-    // the threshold: lane l holds bins kBins-1-16l .. falling
-    constexpr int kPer = kBins / 64;
-    const double target = (double)topp * (double)den * (1.0 + 1e-4);
-    double m[kPer];
-    unsigned c[kPer];
-    double tot = 0;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const int b = kBins - 1 - (kPer * lane + j);
-        m[j] = (double)ld_agent(&ws->hmass[b]);
-        c[j] = ld_agent(&ws->hcnt[b]);
-        tot += m[j];
-    }
-    double incl = tot;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double n = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += n;
-    }
-    double run = incl - tot;
-    int hit = -1;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        run += m[j];
-        if (hit < 0 && run >= target) hit = kBins - 1 - (kPer * lane + j);
-    }
-    const unsigned long long any = __ballot(hit >= 0);
-    const int B = any ? __shfl(hit, __ffsll((long long)any) - 1, 64) : 0;
-    // at least the tokens of bins >= B are candidates (all V if B = 0)
-    unsigned n = 0;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) n += kBins - 1 - (kPer * lane + j) >= B ? c[j] : 0u;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) n += __shfl_xor(n, o, 64);
-    if (lane == 0) {
-        ws->den = den;
-        ws->tp = __uint_as_float((uint32_t)B << 20) / den;
-        ws->radix = (B == 0 ? V : (int)n) > kCap ? 1 : 0;
-    }
-}
+// ------------------------------------------------------- the top-p launch
 
-// ------------------------------------------------------- the select launch
-
-// LDS of the select launch's last block: the sort's keys, ids and running
+// LDS of the top-p launch's last block: the sort's keys, ids and running
 // sums, or the radix select's per-wave histograms
 union SelLds {
     struct {
@@ -337,10 +262,45 @@ __device__ __forceinline__ bool before(float pa, int ia, float pb, int ib) {
 struct Probs {   // p of token i: stored (radix) or as the other kernels compute it
     const float *lg, *ps;
     float mx, temp, den;
-    __device__ __forceinline__ float operator()(int i) const {
-        return ps ? ps[i] : samp_e(lg[i], mx, temp) / den;
-    }
+    // p from the loaded value (a logit, or p itself when stored)
+    __device__ __forceinline__ float of(float v) const { return ps ? v : samp_e(v, mx, temp) / den; }
+    __device__ __forceinline__ float operator()(int i) const { return of(ps ? ps[i] : lg[i]); }
 };
+
+// f(i, p_i, ok) for every token i of [0, V), by the whole block: four
+// tokens per 16-byte load and four loads in flight per thread (a scan by
+// one block is bound by its loads in flight). Whole waves take every step
+// (ok is false on the padding), so f may use wave-wide operations.
+template <class F>
+__device__ __forceinline__ void scan_p(const Probs &P, int V, F &&f) {
+    const int t = threadIdx.x, lane = t & 63;
+    const float *src = P.ps ? P.ps : P.lg;
+    const int n4 = ((uintptr_t)src & 15) == 0 ? V >> 2 : 0;
+    constexpr int U = 4;
+    for (int c0 = t; c0 - lane < n4; c0 += U * kSelThreads) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u * kSelThreads;
+            v[u] = c < n4 ? ((const float4 *)src)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u * kSelThreads;
+            const bool ok = c < n4;
+            f(4 * c + 0, P.of(v[u].x), ok);
+            f(4 * c + 1, P.of(v[u].y), ok);
+            f(4 * c + 2, P.of(v[u].z), ok);
+            f(4 * c + 3, P.of(v[u].w), ok);
+        }
+    }
+    // the last V mod 4 tokens (every token when the data is not 16-byte aligned)
+    for (int i0 = 4 * n4 + t - lane; i0 < V; i0 += kSelThreads) {
+        const int i = i0 + lane;
+        const bool ok = i < V;
+        f(i, ok ? P(i) : 0.f, ok);
+    }
+}
 
 // Where the running sum of the sorted p first reaches X (> 0): p's bits key
 // k*, the tokens before the group of p == k* (above, their mass above_mass),
@@ -358,9 +318,9 @@ __device__ Select radix_select(const Probs &P, int V, double X, SelLds &L) {
     const int t = threadIdx.x, w = t >> 6;
     Select r{false, 0u, 0, 0, 0.0, 0.0};
     uint32_t prefix = 0;
-    constexpr int kSh[4] = {23, 15, 7, 0}, kW[4] = {8, 8, 8, 7};
     for (int lv = 0; lv < 4; ++lv) {
-        const int sh = kSh[lv], nb = 1 << kW[lv];
+        // levels of 8, 8, 8 and 7 bits: p's bits 30-23, 22-15, 14-7, 6-0
+        const int kw = lv < 3 ? 8 : 7, sh = lv < 3 ? 23 - 8 * lv : 0, nb = 1 << kw;
         for (int j = t; j < (kSelThreads / 64) * kRadixBins; j += kSelThreads) {
             (&L.hist.cnt[0][0])[j] = 0;
             (&L.hist.mass[0][0])[j] = 0.0;
@@ -370,15 +330,14 @@ __device__ Select radix_select(const Probs &P, int V, double X, SelLds &L) {
             s_low = INT32_MAX;
         }
         __syncthreads();
-        for (int i = t; i < V; i += kSelThreads) {
-            const float p = P(i);
+        scan_p(P, V, [&](int, float p, bool ok) {
             const uint32_t k = __float_as_uint(p);
-            if (lv == 0 || (k >> (sh + kW[lv])) == prefix) {
+            if (ok && (lv == 0 || (k >> (sh + kw)) == prefix)) {
                 const int b = (int)((k >> sh) & (uint32_t)(nb - 1));
                 atomicAdd(&L.hist.cnt[w][b], 1u);
                 atomicAdd(&L.hist.mass[w][b], (double)p);
             }
-        }
+        });
         __syncthreads();
         // thread t < nb takes bin nb-1-t (the waves' copies added in order);
         // the running sums' intervals (lo, hi] tile (above_mass, total], so
@@ -422,7 +381,7 @@ __device__ Select radix_select(const Probs &P, int V, double X, SelLds &L) {
         r.above_mass = s_mass;
         r.above = s_above;
         r.ties = s_ties;
-        prefix = (prefix << kW[lv]) | (uint32_t)s_b;
+        prefix = (prefix << kw) | (uint32_t)s_b;
         __syncthreads();
     }
     r.found = true;
@@ -443,16 +402,29 @@ __device__ int tie_place(double above_mass, float v, int ties, double X) {
 
 // The id of the (rank + 1)-th token in index order whose p has the bits
 // key: each wave counts the matches of its contiguous segment (lanes on
-// consecutive tokens), the segment holding the rank is searched again.
+// consecutive tokens, four loads in flight), the segment holding the rank
+// is searched again.
 __device__ int id_of(const Probs &P, int V, uint32_t key, int rank) {
     __shared__ int s_cnt[kSelThreads / 64];
     __shared__ int s_id;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    constexpr int nw = kSelThreads / 64;
+    constexpr int nw = kSelThreads / 64, U = 4;
     const int seg = ((V + nw - 1) / nw + 63) & ~63;
     const int lo = min(w * seg, V), hi = min(lo + seg, V);
     int c = 0;
-    for (int i = lo; i < hi; i += 64) c += __popcll(__ballot(i + lane < hi && __float_as_uint(P(i + lane)) == key));
+    for (int i = lo; i < hi; i += 64 * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = i + 64 * u + lane;
+            v[u] = j < hi ? (P.ps ? P.ps[j] : P.lg[j]) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = i + 64 * u + lane;
+            c += __popcll(__ballot(j < hi && __float_as_uint(P.of(v[u])) == key));
+        }
+    }
     if (lane == 0) s_cnt[w] = c;
     if (t == 0) s_id = -1;
     __syncthreads();
@@ -488,64 +460,109 @@ __device__ int last_in_order(const Probs &P, int V) {
     }
     __syncthreads();
     uint32_t k = 0xFFFFFFFFu;
-    for (int i = t; i < V; i += kSelThreads) k = min(k, __float_as_uint(P(i)));
+    scan_p(P, V, [&](int, float p, bool ok) {
+        if (ok) k = min(k, __float_as_uint(p));
+    });
     atomicMin(&s_key, k);
     __syncthreads();
     const uint32_t key = s_key;
     int id = -1;
-    for (int i = t; i < V; i += kSelThreads)
-        if (__float_as_uint(P(i)) == key) id = i;
+    scan_p(P, V, [&](int i, float p, bool ok) {
+        if (ok && __float_as_uint(p) == key) id = max(id, i);
+    });
     atomicMax(&s_id, id);
     __syncthreads();
     return s_id;
 }
 
-// The nucleus and the pick from the sorted candidates in LDS; false if the
-// nucleus reaches past them.
-__device__ bool pick_sorted(const Probs &P, int cnt, int V, float topp, float u, const int *cand, SelLds &L,
-                            int32_t *out) {
-    __shared__ int s_n, s_pick;
+// The nucleus and the pick from the cnt candidates whose ids are in
+// L.sort.id[0, cnt), sorted in LDS by falling p then id: by rank (one
+// candidate per thread, a 64-bit key of p's bits above the complement of
+// the id, so a larger key comes first; p >= 0) up to kRankMax of them,
+// bitonic above. False if the nucleus reaches past the list; with `head`,
+// also if it reaches the list's group of its smallest p: the list then
+// holds every token of p above that one but maybe not every token of that
+// p. have_p: L.sort.p[0, cnt) already holds their p.
+constexpr int kRankMax = 128;
+__device__ bool pick_sorted(const Probs &P, int cnt, int V, float topp, float u, SelLds &L, int32_t *out,
+                            bool head, bool have_p = false) {
+    __shared__ int s_n, s_pick, s_m;
     const int t = threadIdx.x;
-    // the candidates, padded to a power of two with entries that sort last
-    int N2 = 64;
-    while (N2 < cnt) N2 <<= 1;
-    for (int i = t; i < N2; i += kSelThreads) {
-        const int id = i < cnt ? ld_agent(&cand[i]) : INT32_MAX;
-        L.sort.p[i] = i < cnt ? P(id) : -1.f;
-        L.sort.id[i] = id;
+    if (t == 0) {
+        s_n = INT32_MAX;
+        s_m = 0;
     }
-    __syncthreads();
-    for (int k = 2; k <= N2; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = t; i < N2; i += kSelThreads) {
-                const int x = i ^ j;
-                if (x > i) {
-                    const float pa = L.sort.p[i], pb = L.sort.p[x];
-                    const int ia = L.sort.id[i], ib = L.sort.id[x];
-                    const bool swap = (i & k) == 0 ? before(pb, ib, pa, ia) : before(pa, ia, pb, ib);
-                    if (swap) {
-                        L.sort.p[i] = pb;
-                        L.sort.p[x] = pa;
-                        L.sort.id[i] = ib;
-                        L.sort.id[x] = ia;
+    if (cnt <= kRankMax) {
+        uint64_t *key = (uint64_t *)(L.sort.pre + kCap - kRankMax);   // (clear of pre[0, cnt))
+        uint64_t k = 0;
+        float p = 0.f;
+        int id = 0;
+        if (t < cnt) {
+            id = L.sort.id[t];
+            p = have_p ? L.sort.p[t] : P(id);
+            k = ((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(~(uint32_t)id);
+            key[t] = k;
+        }
+        __syncthreads();
+        int rank = 0;
+        if (t < cnt)
+            for (int j = 0; j < cnt; ++j) rank += key[j] > k ? 1 : 0;
+        __syncthreads();
+        if (t < cnt) {
+            L.sort.p[rank] = p;
+            L.sort.id[rank] = id;
+        }
+        __syncthreads();
+    } else {
+        // padded to a power of two with entries that sort last
+        int N2 = 64;
+        while (N2 < cnt) N2 <<= 1;
+        for (int i = t; i < N2; i += kSelThreads) {
+            if (i < cnt) {
+                if (!have_p) L.sort.p[i] = P(L.sort.id[i]);
+            } else {
+                L.sort.p[i] = -1.f;
+                L.sort.id[i] = INT32_MAX;
+            }
+        }
+        __syncthreads();
+        for (int k = 2; k <= N2; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                for (int i = t; i < N2; i += kSelThreads) {
+                    const int x = i ^ j;
+                    if (x > i) {
+                        const float pa = L.sort.p[i], pb = L.sort.p[x];
+                        const int ia = L.sort.id[i], ib = L.sort.id[x];
+                        const bool swap = (i & k) == 0 ? before(pb, ib, pa, ia) : before(pa, ia, pb, ib);
+                        if (swap) {
+                            L.sort.p[i] = pb;
+                            L.sort.p[x] = pa;
+                            L.sort.id[i] = ib;
+                            L.sort.id[x] = ia;
+                        }
                     }
                 }
+                __syncthreads();
             }
-            __syncthreads();
         }
     }
     // running f64 sums: thread t adds its run of C sorted entries in order
     const int C = (cnt + kSelThreads - 1) / kSelThreads;
     const int lo = min(t * C, cnt), hi = min(lo + C, cnt);
     double run = 0;
-    for (int i = lo; i < hi; ++i) run += (double)L.sort.p[i];
+    int above = 0;
+    const float pmin = L.sort.p[cnt - 1];
+    for (int i = lo; i < hi; ++i) {
+        run += (double)L.sort.p[i];
+        above += L.sort.p[i] > pmin ? 1 : 0;
+    }
+    if (head && above) atomicAdd(&s_m, above);
     double tot, acc;
     (void)block_scan_f64(run, &acc, &tot);
     for (int i = lo; i < hi; ++i) {
         acc += (double)L.sort.p[i];
         L.sort.pre[i] = acc;
     }
-    if (t == 0) s_n = INT32_MAX;
     __syncthreads();
     for (int i = lo; i < hi; ++i)
         if (L.sort.pre[i] >= (double)topp) {
@@ -557,6 +574,7 @@ __device__ bool pick_sorted(const Probs &P, int cnt, int V, float topp, float u,
     int n = s_n;
     if (n == INT32_MAX && cnt == V) n = V;
     if (n == INT32_MAX) return false;
+    if (head && cnt != V && n > s_m) return false;
     const float r = u * (float)L.sort.pre[n - 1];
     if (t == 0) s_pick = n - 1;
     __syncthreads();
@@ -604,44 +622,326 @@ __device__ void pick_radix(const Probs &P, int V, float topp, float u, SelLds &L
     if (threadIdx.x == 0) *out = id >= 0 ? id : 0;   // (id >= 0: every pass counts the same tokens)
 }
 
-// The tokens with p >= T into the candidate list (the first kCap; the count
-// goes on), or, when they cannot fit, p of every token into ws->p; then, in
-// the last block, the nucleus and the pick.
+// The fast candidates' threshold: tokens with e >= tc go on the fast list.
+// Any tc gives exact picks (the fast path checks that what it orders is a
+// head of the whole order and holds the nucleus); with tc = (1 - topp) / 2V
+// the tokens left out carry less than (1 - topp) / 2 of den (den >= 1: the
+// maximum's e is 1), so the list usually holds the nucleus.
+__device__ __forceinline__ float fast_tc(float topp, int V) { return (1.f - topp) / (2.f * (float)V); }
+
+// The fast path, in the top-p launch's last block: the cnt (<= kCapF)
+// tokens of the fast list, one per thread (its id and logit lv). Every token left out of the list
+// has p at most the list's smallest, pmin (its e is below every listed e).
+// A histogram of the list's p over their top 10 bits (f64 masses) gives the
+// highest bin edge from which the listed mass reaches topp; the tokens at
+// or above that edge are ordered. If the edge is above pmin they are every
+// token of p >= edge, a head of the whole order closed under equal p;
+// otherwise they are the whole list, whose order is exact above pmin.
+// False (nothing written) if the nucleus is not inside what was ordered.
+__device__ bool pick_fast(const Probs &P, int cnt, int V, float topp, float u, int id, float lv, SelLds &L,
+                          int32_t *out) {
+    __shared__ double s_lm[256];
+    __shared__ int s_hit, s_nf;
+    __shared__ uint32_t s_pmin;
+    const int t = threadIdx.x, lane = t & 63;
+    if (t < 256) s_lm[t] = 0.0;
+    if (t == 0) {
+        s_hit = INT32_MAX;
+        s_nf = 0;
+        s_pmin = 0xFFFFFFFFu;
+    }
+    const float p = t < cnt ? P.of(lv) : 0.f;
+    __syncthreads();
+    const uint32_t bits = __float_as_uint(p);
+    if (t < cnt) {
+        atomicAdd(&s_lm[bits >> 22], (double)p);   // (p in [0, 1]: bins 0..254)
+        atomicMin(&s_pmin, bits);
+    }
+    __syncthreads();
+    // thread t takes bin 255 - t; the first bin from the top where the
+    // listed mass reaches topp (a relative margin far above the f64
+    // rounding of these sums)
+    const int hb = 255 - t;
+    double ex, tot;
+    const double in = block_scan_f64(hb >= 0 ? s_lm[hb] : 0.0, &ex, &tot);
+    if (hb >= 0 && in >= (double)topp * (1.0 + 1e-12)) atomicMin(&s_hit, t);
+    __syncthreads();
+    const uint32_t edge = s_hit == INT32_MAX ? 0u : (uint32_t)(255 - s_hit) << 22;
+    const bool head = edge <= s_pmin && cnt != V;
+    // the listed tokens at or above the edge, gathered in LDS
+    const bool keep = t < cnt && bits >= edge;
+    const unsigned long long bal = __ballot(keep);
+    if (bal) {
+        const int lead = __ffsll((long long)bal) - 1;
+        int base = 0;
+        if (lane == lead) base = atomicAdd(&s_nf, __popcll(bal));
+        base = __shfl(base, lead, 64);
+        if (keep) {
+            const int pos = base + __popcll(bal & ((1ull << lane) - 1));
+            L.sort.id[pos] = id;
+            L.sort.p[pos] = p;
+        }
+    }
+    __syncthreads();
+    const int nf = s_nf;
+    return pick_sorted(P, nf, V, topp, u, L, out, head, true);
+}
+
+// The fast path for a list of at most 64 tokens, in one wave (lane i holds
+// entry i: id, logit lv): ranked by falling p then id with cross-lane
+// reads, moved to their places, then the reference's own loops over the
+// sorted p in one lane (the f64 running sum in order, the nucleus, the
+// draw): no block-wide step. As pick_fast, false unless the nucleus ends
+// above the list's smallest p (or the list is the vocabulary).
+__device__ bool pick_fast_wave(const Probs &P, int cnt, int V, float topp, float u, int id, float lv,
+                               int32_t *out) {
+    const int lane = threadIdx.x & 63;
+    const bool valid = lane < cnt;
+    const float p = valid ? P.of(lv) : 0.f;
+    // keys: p's bits above the id's complement (>= 2^31); padding lanes get
+    // distinct keys below every real one, so the ranks are a permutation
+    const uint64_t key = valid ? ((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(~(uint32_t)id)
+                               : (uint64_t)(63 - lane);
+    const uint32_t klo = (uint32_t)key, khi = (uint32_t)(key >> 32);
+    int rank = 0;
+    for (int j = 0; j < 64; ++j) {
+        const uint64_t kj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(khi, j) << 32) |
+                            (uint64_t)(uint32_t)__builtin_amdgcn_readlane(klo, j);
+        rank += kj > key ? 1 : 0;
+    }
+    // lane r receives the entry of rank r
+    const float sp = __int_as_float(__builtin_amdgcn_ds_permute(rank * 4, __float_as_int(p)));
+    const int sid = __builtin_amdgcn_ds_permute(rank * 4, id);
+    // the reference's loops (engine/midge.c:669-676), run by every lane on
+    // the same values
+    double cum = 0;
+    int n = 0;
+    bool reached = false;
+    for (; n < cnt; ++n) {
+        cum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(sp), n));
+        if (cum >= (double)topp) {
+            ++n;
+            reached = true;
+            break;
+        }
+    }
+    if (!reached && cnt != V) return false;
+    if (cnt != V) {
+        // the entries above the smallest p are the head of the whole order
+        const float pmin = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sp), cnt - 1));
+        const int m = __popcll(__ballot(lane < cnt && sp > pmin));
+        if (n > m) return false;
+    }
+    const float r = u * (float)cum;
+    double acc = 0;
+    int pick = __builtin_amdgcn_readlane(sid, n - 1);
+    for (int i = 0; i < n; ++i) {
+        acc += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(sp), i));
+        if ((double)r <= acc) {
+            pick = __builtin_amdgcn_readlane(sid, i);
+            break;
+        }
+    }
+    if (lane == 0) *out = pick;
+    return true;
+}
+
+// The top-p launch (temp > 0). Every block: e of its tokens (grid-stride),
+// their f64 sum, its e histogram (stored for the select launch), and its
+// fast candidates, gathered in LDS and appended to the fast list with one
+// counter add per block. The last block: den, then the fast path.
+__global__ void __launch_bounds__(kSelThreads) k_samp_topp(const float *__restrict__ lg, int V, float temp,
+                                                           float topp, float u, SampWs *ws,
+                                                           int32_t *__restrict__ out) {
+    __shared__ SelLds L;
+    __shared__ unsigned s_cnt[kHB];
+    __shared__ float s_mass[kHB];
+    __shared__ double sd[kSelThreads / 64];
+    __shared__ float s_den;
+    __shared__ int s_n, s_fb;
+    __shared__ int s_fid[kCapF];
+    const int t = threadIdx.x, lane = t & 63;
+    for (int b = t; b < kHB; b += kSelThreads) {
+        s_cnt[b] = 0;
+        s_mass[b] = 0.f;
+    }
+    if (t == 0) s_n = 0;
+    const float mx = ws->mx;
+    const float tc = fast_tc(topp, V);
+    __syncthreads();
+    const int Vr = (V + 63) & ~63;   // whole waves take part in the ballots
+    double s = 0;
+    for (int i = blockIdx.x * kSelThreads + t; i < Vr; i += gridDim.x * kSelThreads) {
+        const float e = i < V ? samp_e(lg[i], mx, temp) : 0.f;
+        s += e;
+        const int hb = (int)(__float_as_uint(e) >> 20);
+        if (i < V && hb >= kHLo) {   // e >= 2^-40, or NaN (the top bin)
+            const int b = min(hb - kHLo, kHB - 1);
+            atomicAdd(&s_cnt[b], 1u);
+            atomicAdd(&s_mass[b], e);
+        }
+        // the block's fast candidates into LDS (the first kCapF; the count goes on)
+        const bool in = i < V && e >= tc;
+        const unsigned long long bal = __ballot(in);
+        if (!bal) continue;
+        const int lead = __ffsll((long long)bal) - 1;
+        int base = 0;
+        if (lane == lead) base = atomicAdd(&s_n, __popcll(bal));
+        base = __shfl(base, lead, 64);
+        const int pos = base + __popcll(bal & ((1ull << lane) - 1));
+        if (in && pos < kCapF) s_fid[pos] = i;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if (lane == 0) sd[t >> 6] = s;
+    __syncthreads();
+    // one counter add per block appends them to the fast list
+    const int nb = s_n;
+    if (t == 0) s_fb = nb ? (int)atomicAdd(&ws->ncand, (unsigned)nb) : 0;
+    __syncthreads();
+    const int fb = s_fb;
+    for (int j = t; j < nb && fb + j < kCapF; j += kSelThreads) st_agent(&ws->cand[fb + j], s_fid[j]);
+    for (int b = t; b < kHB; b += kSelThreads) {
+        st_agent(&ws->bcnt[blockIdx.x][b], s_cnt[b]);
+        st_agent(&ws->bmass[blockIdx.x][b], s_mass[b]);
+    }
+    if (t == 0) {
+        double d = 0;
+        for (int w = 0; w < kSelThreads / 64; ++w) d += sd[w];
+        st_agent(&ws->dsum[blockIdx.x], d);
+    }
+    if (!last_block(&ws->done[1])) return;
+
+    // one round of loads: the blocks' sums, the fast list's count and its
+    // entries whatever the count (an entry past it may be an earlier call's,
+    // so the index is clamped to the vocabulary; it is not used), then the
+    // entries' logits
+    double d = 0;
+    if (t < 64)
+        for (int b = t; b < (int)gridDim.x; b += 64) d += ld_agent(&ws->dsum[b]);
+    const int cnt = (int)ld_agent(&ws->ncand);
+    const int id = t < kCapF ? min(max(ld_agent(&ws->cand[t]), 0), V - 1) : 0;
+    const float lv = lg[id];
+    // den: lane l adds blocks l, l + 64, ... in order, then a butterfly
+    if (t < 64) {
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) d += __shfl_xor(d, o, 64);
+        if (t == 0) s_den = (float)d;
+    }
+    __syncthreads();
+    const float den = s_den;
+    const Probs P{lg, nullptr, mx, temp, den};
+    const bool ok = den > 0.f && den <= 3.402823466e38f && cnt >= 1;
+    if (ok && cnt <= 64) {
+        // one wave
+        if (t >= 64) return;
+        const bool fast = pick_fast_wave(P, cnt, V, topp, u, id, lv, out);
+        if (t == 0) {
+            ws->den = den;
+            ws->fast = fast ? 1 : 0;
+        }
+        return;
+    }
+    const bool fast = ok && cnt <= kCapF && pick_fast(P, cnt, V, topp, u, id, lv, L, out);
+    if (t == 0) {
+        ws->den = den;
+        ws->fast = fast ? 1 : 0;
+    }
+}
+
+// The select launch: nothing when the fast path picked. Otherwise every
+// block reads the top-p launch's per-block e histograms (the same sums in
+// the same order in every block) and finds the candidate threshold T: the
+// highest bin whose mass from the top reaches topp * den by a margin that
+// covers the histogram's f32 rounding, T = RN(lower edge / den), so p >= T
+// holds every token of those bins (division is monotone). Then, over its
+// share of the tokens, the ids with p >= T (gathered in LDS, one counter add
+// per block; the first kCap), or, when the candidates cannot fit, p itself.
+// The last block: the sort and the pick, or the radix select.
 __global__ void __launch_bounds__(kSelThreads) k_samp_select(const float *__restrict__ lg, int V, float temp,
                                                              float topp, float u, SampWs *ws,
                                                              int32_t *__restrict__ out) {
     __shared__ SelLds L;
-    const float mx = ws->mx, den = ws->den, tp = ws->tp;
-    const bool radix = ws->radix != 0;
-    const int lane = threadIdx.x & 63;
-    const int Vr = (V + 63) & ~63;   // whole waves take part in the ballots
-    for (int i = blockIdx.x * kSelThreads + threadIdx.x; i < Vr; i += gridDim.x * kSelThreads) {
-        const float p = i < V ? samp_e(lg[i], mx, temp) / den : 0.f;
+    __shared__ int s_hit, s_n, s_fb;
+    if (ws->fast) return;
+    const int t = threadIdx.x, lane = t & 63;
+    const float mx = ws->mx, den = ws->den;
+    const Probs P{lg, nullptr, mx, temp, den};
+    // the threshold: thread t takes bin kHB - 1 - t (the blocks' histograms
+    // added in block order); eight rows in flight
+    const int hb = kHB - 1 - t;
+    double m = 0;
+    unsigned c = 0;
+    if (hb >= 0) {
+        const int nq = kSelBlocks;
+        for (int q0 = 0; q0 < nq; q0 += 8) {
+            float fm[8];
+            unsigned fc[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                fm[j] = ws->bmass[q0 + j][hb];
+                fc[j] = ws->bcnt[q0 + j][hb];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                m += (double)fm[j];
+                c += fc[j];
+            }
+        }
+    }
+    const double target = (double)topp * (double)den * (1.0 + 1e-4);
+    double ex, tot;
+    const double in = block_scan_f64(m, &ex, &tot);
+    if (t == 0) {
+        s_hit = INT32_MAX;
+        s_n = 0;
+    }
+    __syncthreads();
+    if (hb >= 0 && in >= target) atomicMin(&s_hit, t);
+    __syncthreads();
+    const int hit = s_hit;
+    int nc;
+    (void)block_scan_int(t <= hit ? (int)c : 0, &nc);
+    // at least the tokens of the bins from the top through the hit are
+    // candidates (every token when no bin reaches the target)
+    const float tp = hit == INT32_MAX ? 0.f : __uint_as_float((uint32_t)(kHLo + kHB - 1 - hit) << 20) / den;
+    const bool radix = (hit == INT32_MAX ? V : nc) > kCap;
+    const int Vr = (V + 63) & ~63;
+    for (int i = blockIdx.x * kSelThreads + t; i < Vr; i += gridDim.x * kSelThreads) {
+        const float p = i < V ? P(i) : 0.f;
         if (radix) {
             if (i < V) st_agent(&ws->p[i], p);
             continue;
         }
-        const bool in = i < V && p >= tp;
-        const unsigned long long bal = __ballot(in);
+        const bool inc = i < V && p >= tp;
+        const unsigned long long bal = __ballot(inc);
         if (!bal) continue;
-        unsigned base = 0;
         const int lead = __ffsll((long long)bal) - 1;
-        if (lane == lead) base = atomicAdd(&ws->ncand, (unsigned)__popcll(bal));
+        int base = 0;
+        if (lane == lead) base = atomicAdd(&s_n, __popcll(bal));
         base = __shfl(base, lead, 64);
-        const unsigned pos = base + (unsigned)__popcll(bal & ((1ull << lane) - 1));
-        if (in && pos < kCap) st_agent(&ws->cand[pos], i);
+        const int pos = base + __popcll(bal & ((1ull << lane) - 1));
+        if (inc && pos < kCap) L.sort.id[pos] = i;
+    }
+    __syncthreads();
+    if (!radix) {
+        const int nb = s_n;
+        if (t == 0) s_fb = nb ? (int)atomicAdd(&ws->nsel, (unsigned)nb) : 0;
+        __syncthreads();
+        const int fb = s_fb;
+        for (int j = t; j < nb && fb + j < kCap; j += kSelThreads) st_agent(&ws->cand[fb + j], L.sort.id[j]);
     }
     if (!last_block(&ws->done[2])) return;
-    const int cnt = (int)ld_agent(&ws->ncand);
-    if (!radix && cnt <= kCap) {
-        const Probs P{lg, nullptr, mx, temp, den};
-        if (pick_sorted(P, cnt, V, topp, u, ws->cand, L, out)) return;
+    const int cnt = (int)ld_agent(&ws->nsel);
+    if (!radix && cnt >= 1 && cnt <= kCap) {
+        for (int j = t; j < cnt; j += kSelThreads) L.sort.id[j] = ld_agent(&ws->cand[j]);
+        __syncthreads();
+        if (pick_sorted(P, cnt, V, topp, u, L, out, false)) return;
         __syncthreads();
         pick_radix(P, V, topp, u, L, out);   // (the histogram fell short: recomputed p)
         return;
     }
-    const Probs P{lg, radix ? ws->p : nullptr, mx, temp, den};
-    pick_radix(P, V, topp, u, L, out);
+    pick_radix(radix ? Probs{lg, ws->p, mx, temp, den} : P, V, topp, u, L, out);
 }
 
 // zeroes the workspace head (counters, histogram) of a fresh workspace
@@ -685,7 +985,7 @@ int sample_launch(const float *logits, int V, float temp, float topp, float u, v
     SAMP_LAUNCH("sample_max", k_samp_max, dim3(kSampBlocks), dim3(kSampThreads), logits, V, ws,
                 greedy ? out : nullptr);
     if (greedy) return hip_check(hipGetLastError(), "sample launch");
-    SAMP_LAUNCH("sample_exp", k_samp_exp, dim3(kSampBlocks), dim3(kSampThreads), logits, V, temp, topp, ws);
+    SAMP_LAUNCH("sample_topp", k_samp_topp, dim3(kSelBlocks), dim3(kSelThreads), logits, V, temp, topp, u, ws, out);
     SAMP_LAUNCH("sample_select", k_samp_select, dim3(kSelBlocks), dim3(kSelThreads), logits, V, temp, topp, u, ws,
                 out);
 #undef SAMP_LAUNCH

@@ -358,19 +358,29 @@ def test_sample_dev_vs_oracle(mh, V):
     out.free()
 
 
-@pytest.mark.parametrize("shape", ["peaked", "flat", "equal", "steps", "cap_edge"])
+@pytest.mark.parametrize("shape", ["lm_head", "tied_top", "peaked", "flat", "equal", "steps", "cap_edge"])
 def test_sample_dev_nucleus_paths(mh, shape):
-    # The nucleus selection's two ways (a sort of the candidates in LDS, or
-    # the exact radix select over the whole vocabulary when the candidates
-    # are too many or the nucleus reaches past them): peaked logits (a few
-    # candidates), flat ones (the nucleus is most of the vocabulary), all
-    # logits equal (one group of V equal p: ties by token id), a staircase
-    # of equal-p groups, and a nucleus of about the candidate capacity.
+    # The nucleus selection's three ways (the fast list of tokens with e
+    # above a bound fixed by topp and V, ranked in LDS; the histogram
+    # threshold's candidates sorted in LDS; the exact radix select over the
+    # whole vocabulary when the candidates are too many or the nucleus
+    # reaches past them): logits of the lm_head's spread (standard deviation
+    # 20: a nucleus of a few tokens, the fast list), ten tied top tokens (the
+    # fast list ends in a group of equal p, so it is not taken), peaked
+    # logits (a few thousand candidates), flat ones (the nucleus is most of
+    # the vocabulary), all logits equal (one group of V equal p: ties by
+    # token id), a staircase of equal-p groups, and a nucleus of about the
+    # candidate capacity.
     from midge_amd.moe import sample_dev
     say(f"sample_dev nucleus {shape}")
     rng = np.random.default_rng(hash(shape) % 2**32)
     V = 201088
-    if shape == "peaked":
+    if shape == "lm_head":
+        lg = (rng.standard_normal(V) * 20).astype(np.float32)
+    elif shape == "tied_top":
+        lg = np.full(V, -200.0, np.float32)
+        lg[rng.choice(V, 10, replace=False)] = 20.0
+    elif shape == "peaked":
         lg = (rng.standard_normal(V) * 6).astype(np.float32)
     elif shape == "flat":
         lg = (rng.standard_normal(V) * 0.2).astype(np.float32)
