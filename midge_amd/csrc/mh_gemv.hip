@@ -322,22 +322,24 @@ k_gemm_q8r(const int8_t *__restrict__ W, const float *__restrict__ S, const uint
 }
 
 // Long int8 matrices (the lm_head) at batch 2+: a wave owns tiles of 16 MT
-// rows, an equal contiguous share of them. Per K super-step of 1024 columns
-// it loads each of its rows' next kilobyte with one 64-lane instruction
-// (whole rows per instruction: the fastest HBM pattern; the matrix-core
+// rows, an equal contiguous share of them. Per K super-step of 512 columns
+// it loads two of its rows' next 512 bytes with each 64-lane instruction
+// (contiguous runs of whole rows: the fastest HBM pattern; the matrix-core
 // operand layout, 16 rows x 64 bytes per instruction, streams ~25% slower),
-// writes them to its private LDS buffer at a row stride of 1040 bytes (the
+// writes them to its private LDS buffer at a row stride of 528 bytes (the
 // operand lanes' 16 rows then fall in distinct banks), issues the next
 // super-step's loads, and runs the step's matrix instructions from LDS.
-// Digits as in k_gemm_q8r (L2 hits), DB chunks ahead. (lm_head 201088 x
-// 2880 at batch 32: 252 us with the operand-layout loads, 226 us with this
-// kernel at MT = 1, 214 at MT = 2, 208 with the digits four chunks ahead.)
-constexpr int kQ8SS = 1024;        // bytes of a row per super-step (16 chunks of 64)
-constexpr int kQ8RowLds = 1040;    // LDS row stride
+// Digits as in k_gemm_q8r (L2 hits), DB chunks ahead. 67.6 KB of LDS and
+// under 256 VGPRs: two blocks per CU. (lm_head 201088 x 2880 at batch 32:
+// 252 us with the operand-layout loads; with this kernel and 1024-column
+// super-steps (one block per CU) 226 us at MT = 1, 214 at MT = 2, 208 with
+// the digits four chunks ahead; 200 us with 512-column super-steps.)
+constexpr int kQ8SS = 512;         // bytes of a row per super-step (8 chunks of 64)
+constexpr int kQ8RowLds = 528;     // LDS row stride
 constexpr int kQ8RowWaves = 4;     // waves per block (each with its own buffer)
 
-template <int NT, int MT>
-__global__ void __launch_bounds__(64 * kQ8RowWaves, MT == 1 ? 2 : 1)
+template <int NT, int MT, int DB>
+__global__ void __launch_bounds__(64 * kQ8RowWaves, 2)
 k_gemm_q8r_rows(const int8_t *__restrict__ W, const float *__restrict__ S, const uint8_t *__restrict__ xq,
                 const int *__restrict__ shift, const float *__restrict__ X, float *__restrict__ Y, int R, int K,
                 int batch) {
@@ -349,8 +351,7 @@ k_gemm_q8r_rows(const int8_t *__restrict__ W, const float *__restrict__ S, const
     const int tbeg = (int)(gw * T / nw), tend = (int)((gw + 1) * T / nw);
     uint8_t *buf = lds[wave];
     const mh_gbytes bp = mh_global(xq + ((size_t)grp * KC * 3 * NT * 64 + lane) * 16);
-    constexpr int DB = 4;   // digit chunks in flight (their L2 latency exceeds a chunk's math)
-    mh_u4 st[16 * MT];   // one super-step of the 16 MT rows: row j's bytes 16 lane .. +15
+    mh_u4 st[8 * MT];    // one super-step of the 16 MT rows: rows 2 j, 2 j + 1 (lane halves), 16 bytes a lane
     mh_u4 b[DB][3 * NT];
     auto load_b = [&](int set, int kc) {
 #pragma unroll
@@ -360,10 +361,10 @@ k_gemm_q8r_rows(const int8_t *__restrict__ W, const float *__restrict__ S, const
     for (int tile = tbeg; tile < tend; ++tile) {
         const int r0 = tile * 16 * MT;
         auto load_ss = [&](int ss) {
-            const int o = ss * kQ8SS + 16 * lane;
+            const int o = ss * kQ8SS + 16 * (lane & 31);
 #pragma unroll
-            for (int j = 0; j < 16 * MT; ++j) {
-                const int r = min(r0 + j, R - 1);
+            for (int j = 0; j < 8 * MT; ++j) {
+                const int r = min(r0 + 2 * j + (lane >> 5), R - 1);
                 st[j] = o < K ? mh_load16(mh_global(W + (size_t)r * K + o)) : mh_u4{0u, 0u, 0u, 0u};
             }
         };
@@ -382,15 +383,16 @@ k_gemm_q8r_rows(const int8_t *__restrict__ W, const float *__restrict__ S, const
             // complete in order: the last step's reads are done), then the
             // next super-step's loads
 #pragma unroll
-            for (int j = 0; j < 16 * MT; ++j) *(mh_u4 *)(buf + j * kQ8RowLds + 16 * lane) = st[j];
+            for (int j = 0; j < 8 * MT; ++j)
+                *(mh_u4 *)(buf + (2 * j + (lane >> 5)) * kQ8RowLds + 16 * (lane & 31)) = st[j];
             if (ss + 1 < NSS) load_ss(ss + 1);
-            const int nc = min(16, KC - 16 * ss);
+            const int nc = min(kQ8SS / 64, KC - (kQ8SS / 64) * ss);
             const uint8_t *ab = buf + i * kQ8RowLds + 16 * g;
             for (int c = 0; c < nc; c += DB) {
 #pragma unroll
                 for (int h = 0; h < DB; ++h) {
                     if (c + h >= nc) break;
-                    const int kc = 16 * ss + c + h;   // its digits are in set kc % DB = h
+                    const int kc = (kQ8SS / 64) * ss + c + h;   // its digits are in set kc % DB = h
                     load_b((h + DB - 1) % DB, min(kc + DB - 1, KC - 1));
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
@@ -554,14 +556,16 @@ int launch_gemm_q8r(const DevWT &w, const float *x, float *y, int batch, hipStre
     };
     const char *nl = getenv("MIDGE_HIP_Q8_NO_ROWS");   // per call: A/B against the register-operand kernel
     if (longm && !(nl && *nl && *nl != '0')) {
-        // one block of 4 waves per CU (133 KB of LDS), each wave 32-row tiles
-        const int64_t nb = std::min<int64_t>((R + 31) / 32 / kQ8RowWaves + 1, (int64_t)device_cus());
+        // two blocks of 4 waves per CU, each wave 32-row tiles
+        const int64_t nb = std::min<int64_t>((R + 31) / 32 / kQ8RowWaves + 1, 2 * (int64_t)device_cus());
         auto go2 = [&](auto kern) {
             MH_LAUNCH("gemm_q8r_rows", kern, dim3((unsigned)nb, (unsigned)groups), dim3(64 * kQ8RowWaves), 0, s,
                       (const int8_t *)w.data, (const float *)w.scales, xq, sh, x, y, (int)R, (int)K, batch);
         };
-        if (NT == 2) go2(k_gemm_q8r_rows<2, 2>);
-        else go2(k_gemm_q8r_rows<1, 2>);
+        // digit chunks in flight: as many as fit beside the staged rows at
+        // two waves per SIMD (three spill at two column groups)
+        if (NT == 2) go2(k_gemm_q8r_rows<2, 2, 2>);
+        else go2(k_gemm_q8r_rows<1, 2, 4>);
     } else if (longm) {
         if (NT == 2) go(k_gemm_q8r<2, Q8Long>, Q8Long::rows, Q8Long::threads);
         else go(k_gemm_q8r<1, Q8Long>, Q8Long::rows, Q8Long::threads);
