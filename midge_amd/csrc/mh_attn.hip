@@ -5,13 +5,15 @@
 //   rmsnorm          launch_rmsnorm (k_rmsnorm)
 //   q, k, v          one launch on the GEMV engine (k_gemv3), any weight
 //                    dtype; three launch_gemv calls where the shapes differ
-//   k_attn_prep      one block per head, one thread per element: biases,
-//                    per-head RMSNorm (the reference's sequential sum), RoPE
-//                    from the given tables, k and v to the f16 cache slot
-//                    pos % cap with the reference's conversion (wk_to_f16)
-//   k_attn_heads     one block per query head: scores over the cached
-//                    positions, softmax with the optional sink logit in the
-//                    denominator, the weighted sum of the cached v
+//   k_attn_split     per query head and split of the cached positions:
+//                    biases, per-head RMSNorm (the reference's sequential
+//                    sum), RoPE from the given tables, the current k and v
+//                    rounded to f16 as wk_to_f16 does (and written to the
+//                    cache slot pos % cap by one block of the kv head); the
+//                    scores over the cached positions, softmax with the
+//                    optional sink logit in the denominator, the weighted
+//                    sum of the cached v (splits combined by the last one
+//                    to finish when a head has more than one)
 //   o                the GEMV engine with the residual in its epilogue
 //                    (k_gemv_res: + bias, x += o); GEMV + k_attn_residual
 //                    where the shape needs the general kernel
@@ -159,7 +161,6 @@ int launch_qkv_t(const DevWT *w, const float *x, float *const *y, hipStream_t s,
     *done = true;
     return hip_check(hipGetLastError(), "q/k/v launch");
 }
-constexpr int kHeadThreads = 1024;   // per query head: positions, then head_dim x position groups
 
 // The cache's f16 as wk_to_f16 (engine/mkern.h:261-273) makes it: the
 // hardware's round-to-nearest-even conversion (which already overflows to
@@ -171,73 +172,6 @@ __device__ __forceinline__ uint16_t to_f16_ref(float f) {
     if (!(a >= 0x1p-14f)) return a != a ? (uint16_t)(sign | 0x7c00u) : sign;
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
-
-struct PrepArgs {
-    float *q, *k, *v;
-    const float *bq, *bk, *bv, *qn, *kn, *co, *si;
-    uint16_t *kc, *vc;
-    int nh, nkv, hd, slot, qk_norm;
-    float eps;
-};
-
-// Block h: query head h (h < nh) or key/value head h - nh, one thread per
-// element, the vector in LDS: + bias, RMSNorm with the head norm weights (if
-// enabled; the reference's sequential sum of squares, in one thread), RoPE;
-// q goes back to memory, k and v (+ bias) to the cache slot as f16.
-__global__ void __launch_bounds__(256) k_attn_prep(PrepArgs A) {
-#pragma clang fp contract(off)
-    __shared__ float u[256];
-    __shared__ float s_inv;
-    const int h = blockIdx.x, i = threadIdx.x, hd = A.hd, half = hd / 2;
-    const bool isq = h < A.nh;
-    const int g = isq ? h : h - A.nh;
-    float *src = isq ? A.q + (size_t)h * hd : A.k + (size_t)g * hd;
-    const float *b = isq ? A.bq + (size_t)h * hd : A.bk + (size_t)g * hd;
-    if (i < hd) u[i] = src[i] + b[i];
-    __syncthreads();
-    if (A.qk_norm) {
-        const float *w = isq ? A.qn : A.kn;
-        if (i == 0) {
-            float ss = 0.f;
-            for (int j = 0; j < hd; ++j) ss += u[j] * u[j];
-            s_inv = 1.0f / sqrtf(ss / (float)hd + A.eps);
-        }
-        __syncthreads();
-        const float val = i < hd ? u[i] * s_inv * w[i] : 0.f;
-        __syncthreads();
-        if (i < hd) u[i] = val;
-        __syncthreads();
-    }
-    float r0 = 0.f, r1 = 0.f;
-    if (i < half) {
-        const float a = u[i], c = u[i + half];
-        r0 = a * A.co[i] - c * A.si[i];
-        r1 = c * A.co[i] + a * A.si[i];
-    }
-    __syncthreads();
-    if (i < half) {
-        u[i] = r0;
-        u[i + half] = r1;
-    }
-    __syncthreads();
-    if (i >= hd) return;
-    if (isq) {
-        src[i] = u[i];
-    } else {
-        const size_t o = (size_t)A.slot * A.nkv * hd + (size_t)g * hd + i;
-        A.kc[o] = to_f16_ref(u[i]);
-        A.vc[o] = to_f16_ref(A.v[(size_t)g * hd + i] + A.bv[(size_t)g * hd + i]);
-    }
-}
-
-struct HeadArgs {
-    const float *q, *sink;
-    const uint16_t *kc, *vc;
-    float *att, *ao;
-    int hd, gq, kvd, nctx, cap, sinks;
-    int kvec;   // 1: cached keys read 16 bytes at a time (hd % 8 == 0, 16-byte aligned cache)
-    float scale;
-};
 
 __device__ __forceinline__ float block_max_f(float v, float *part) {
 #pragma unroll
@@ -261,66 +195,316 @@ __device__ __forceinline__ float block_sum_f(float v, float *part) {
     return r;
 }
 
-// Block h = query head h over the nctx cached positions. Scores are the
-// reference's sequential f16 dot (one position per thread); the softmax sum
-// and the weighted sum of v are split over the block (hd dims x 1024 / hd
-// position groups), so they round in a different order than the
-// reference's loops.
-__global__ void __launch_bounds__(kHeadThreads) k_attn_heads(HeadArgs A) {
+// The decode attention of one token in one launch: prep and heads split
+// over the cached positions. Block (h, s) takes query head h and positions
+// [P s, P s + P) of the nctx cached ones (P = 256 on 256 threads up to 256
+// positions, else 2048 on 1024 threads: contexts up to 2048 need no
+// combine):
+//   prep     q of head h and the current token's k, v of its kv head
+//            (biases, per-head RMSNorm with the reference's sequential sum
+//            of squares, RoPE, k and v rounded to f16 as wk_to_f16 does),
+//            every global value loaded in one round; every block of a kv
+//            head computes the same k, v and uses them for the current
+//            slot, and block (first head of the group, split 0) writes them
+//            to the cache slot, so no block waits for another
+//   scores   the reference's sequential f16 dot per position (16-byte
+//            loads, all of a thread's positions in flight), times scale
+//   partial  m = the split's maximum score, l = sum of e = expf(score - m),
+//            o = sum of e * v (head_dim 64: threads of 8 dims x a position
+//            group with 16-byte loads, the groups added in order; else
+//            waves over positions, lanes over dims)
+//   combine  in the block when the head has one split; else the last split
+//            of head h to finish (a per-head counter it resets) reads the
+//            others' partials: M = max(m over splits, sink), den = sum of l *
+//            expf(m - M) (+ expf(sink - M)), ao = sum of o * expf(m - M) /
+//            den. The factors round differently from the reference's single
+//            pass over expf(score - max); the result stays within its own
+//            AVX2-vs-scalar divergence.
+constexpr int kSplitT = 1024;     // threads per block
+constexpr int kSplitP = 2;        // positions per thread: 2048 positions per split
+constexpr int kMaxSplits = 1024;  // splits per head (cached positions <= 2^21)
+
+struct SplitArgs {
+    const float *q, *k, *v;
+    const float *bq, *bk, *bv, *qn, *kn, *co, *si, *sink;
+    uint16_t *kc, *vc;
+    float *part;      // [nh][S][hd + 2]: o, m, l
+    unsigned *cnt;    // [nh] arrivals (zero between calls)
+    float *ao;        // [nh][hd]
+    int nh, hd, gq, kvd, nctx, slot, S, sinks, qk_norm, kvec;
+    float scale, eps;
+};
+
+__device__ __forceinline__ float f16_at(const uint16_t *p) { return mh_f16(*p); }
+
+template <int T, int PPT>
+__global__ void __launch_bounds__(T) k_attn_split(SplitArgs A) {
 #pragma clang fp contract(off)
-    __shared__ float part[kHeadThreads / 64];
-    __shared__ float qs[256];
-    __shared__ float acc[kHeadThreads];
-    const int h = blockIdx.x, kh = h / A.gq, hd = A.hd;
-    const float *qh = A.q + (size_t)h * hd;
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) qs[i] = qh[i];
+    constexpr int P = T * PPT;   // positions per split
+    __shared__ float uq[256], uk[256];
+    __shared__ __attribute__((aligned(16))) uint16_t kcur[256], vcur[256];
+    __shared__ float s_inv[2];
+    __shared__ float sc[P];
+    __shared__ float red[T / 64];
+    // o partials: per wave [T / 64][256], or per position group [T / 8][64]
+    __shared__ float ob[T / 8 * 64 > T / 64 * 256 ? T / 8 * 64 : T / 64 * 256];
+    __shared__ int s_last;
+    __shared__ float s_m[kMaxSplits], s_l[kMaxSplits];
+    const int h = blockIdx.x / A.S, s = blockIdx.x - h * A.S;
+    const int kh = h / A.gq, hd = A.hd, half = hd / 2, i = threadIdx.x, lane = i & 63, wv = i >> 6;
+    // ---------------------------------------------------------- prep
+    // every global value the prep needs, loaded in one round
+    float xq = 0.f, xk = 0.f, xv = 0.f, cs = 0.f, sn = 0.f, wq = 0.f, wk = 0.f;
+    if (i < hd) {
+        xq = A.q[(size_t)h * hd + i] + A.bq[(size_t)h * hd + i];
+        xk = A.k[(size_t)kh * hd + i] + A.bk[(size_t)kh * hd + i];
+        xv = A.v[(size_t)kh * hd + i] + A.bv[(size_t)kh * hd + i];
+        if (A.qk_norm) {
+            wq = A.qn[i];
+            wk = A.kn[i];
+        }
+    }
+    if (i < half) {
+        cs = A.co[i];
+        sn = A.si[i];
+    }
+    if (i < hd) {
+        uq[i] = xq;
+        uk[i] = xk;
+    }
     __syncthreads();
-    float *sc = A.att + (size_t)h * A.cap;
-    float mx = -1e30f;
-    for (int t = threadIdx.x; t < A.nctx; t += blockDim.x) {
-        const uint16_t *kt = A.kc + (size_t)t * A.kvd + (size_t)kh * hd;
-        float d = 0.f;
-        if (A.kvec) {   // 16-byte loads of 8 cached values, summed in order
-            for (int i0 = 0; i0 < hd; i0 += 8) {
-                const uint4 w = *(const uint4 *)(kt + i0);
-                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    if (A.qk_norm) {
+        if (i == 0 || i == 64) {   // the reference's sequential sums of squares
+            const float *u = i == 0 ? uq : uk;
+            float ss = 0.f;
+            for (int j = 0; j < hd; ++j) ss += u[j] * u[j];
+            s_inv[i == 0 ? 0 : 1] = 1.0f / sqrtf(ss / (float)hd + A.eps);
+        }
+        __syncthreads();
+        const float vq = i < hd ? uq[i] * s_inv[0] * wq : 0.f;
+        const float vk = i < hd ? uk[i] * s_inv[1] * wk : 0.f;
+        __syncthreads();
+        if (i < hd) {
+            uq[i] = vq;
+            uk[i] = vk;
+        }
+        __syncthreads();
+    }
+    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f;
+    if (i < half) {
+        const float a = uq[i], c = uq[i + half], b = uk[i], d = uk[i + half];
+        q0 = a * cs - c * sn;
+        q1 = c * cs + a * sn;
+        k0 = b * cs - d * sn;
+        k1 = d * cs + b * sn;
+    }
+    __syncthreads();
+    if (i < half) {
+        uq[i] = q0;
+        uq[i + half] = q1;
+        uk[i] = k0;
+        uk[i + half] = k1;
+    }
+    __syncthreads();
+    if (i < hd) {
+        kcur[i] = to_f16_ref(uk[i]);
+        vcur[i] = to_f16_ref(xv);
+        if (h % A.gq == 0 && s == 0) {
+            const size_t o = (size_t)A.slot * A.kvd + (size_t)kh * hd + i;
+            A.kc[o] = kcur[i];
+            A.vc[o] = vcur[i];
+        }
+    }
+    __syncthreads();
+    // ---------------------------------------------------------- scores
+    // positions t0 + i + T r, r < PPT (one 16-byte load per 8 cached values,
+    // every load of the thread's positions issued before the sums, which
+    // keep the reference's order within a position)
+    const int t0 = P * s;
+    float dd[PPT];
+    if (A.kvec && hd == 64) {
+        uint4 kw[PPT][8];
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            const int t = t0 + i + T * r;
+            const bool cur = t == A.slot || t >= A.nctx;
+            const uint16_t *kt = cur ? kcur : A.kc + (size_t)t * A.kvd + (size_t)kh * hd;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) kw[r][c] = *(const uint4 *)(kt + 8 * c);
+        }
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            float d = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t ww[4] = {kw[r][c].x, kw[r][c].y, kw[r][c].z, kw[r][c].w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    d += qs[i0 + 2 * j] * mh_f16((uint16_t)(ww[j] & 0xffffu));
-                    d += qs[i0 + 2 * j + 1] * mh_f16((uint16_t)(ww[j] >> 16));
+                    d += uq[8 * c + 2 * j] * mh_f16((uint16_t)(ww[j] & 0xffffu));
+                    d += uq[8 * c + 2 * j + 1] * mh_f16((uint16_t)(ww[j] >> 16));
                 }
             }
-        } else {
-            for (int i = 0; i < hd; ++i) d += qs[i] * mh_f16(kt[i]);
+            dd[r] = d;
         }
-        d *= A.scale;
-        sc[t] = d;
-        mx = fmaxf(mx, d);
+    } else {
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            const int t = t0 + i + T * r;
+            float d = 0.f;
+            if (t < A.nctx) {
+                const uint16_t *kt = t == A.slot ? kcur : A.kc + (size_t)t * A.kvd + (size_t)kh * hd;
+                for (int j = 0; j < hd; ++j) d += uq[j] * f16_at(kt + j);
+            }
+            dd[r] = d;
+        }
     }
-    mx = block_max_f(mx, part);
-    const float sinkv = A.sinks ? A.sink[h] : -1e30f;
-    if (sinkv > mx) mx = sinkv;
-    float s = 0.f;
-    for (int t = threadIdx.x; t < A.nctx; t += blockDim.x) {
-        const float e = expf(sc[t] - mx);
-        sc[t] = e;
-        s += e;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < PPT; ++r) {
+        dd[r] = t0 + i + T * r < A.nctx ? dd[r] * A.scale : -INFINITY;
+        mloc = fmaxf(mloc, dd[r]);
     }
-    const float den = (A.sinks ? expf(sinkv - mx) : 0.f) + block_sum_f(s, part);
-    const float inv = 1.0f / den;
-    // thread (group j, dim i): positions j, j + nq, ... of dim i
-    const int i = threadIdx.x % hd, j = threadIdx.x / hd, nq = blockDim.x / hd;
-    float o = 0.f;
-    if (j < nq)
-        for (int t = j; t < A.nctx; t += nq)
-            o += (sc[t] * inv) * mh_f16(A.vc[(size_t)t * A.kvd + (size_t)kh * hd + i]);
-    if (j < nq) acc[j * hd + i] = o;
+    const float m = block_max_f(mloc, red);
+    float el = 0.f;
+#pragma unroll
+    for (int r = 0; r < PPT; ++r) {
+        const float e = t0 + i + T * r < A.nctx ? expf(dd[r] - m) : 0.f;
+        sc[i + T * r] = e;
+        el += e;
+    }
+    const float l = block_sum_f(el, red);   // (its barriers also order the sc writes)
+    const int np = min(P, A.nctx - t0);
+    if (A.kvec && hd == 64) {
+        // 16-byte loads: thread (position group pg, dims 8 dc .. 8 dc + 7)
+        // takes positions pg, pg + NG, ... (all its loads in flight), then
+        // the groups' sums are added in order
+        constexpr int NG = T / 8, NPT = P / NG;
+        const int pg = i >> 3, dc = i & 7;
+        float o8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        uint4 w8[NPT];
+#pragma unroll
+        for (int u = 0; u < NPT; ++u) {
+            const int j = pg + NG * u, tt = t0 + j;
+            w8[u] = (j < np && tt != A.slot) ? *(const uint4 *)(A.vc + (size_t)tt * A.kvd + (size_t)kh * hd + 8 * dc)
+                                             : *(const uint4 *)(vcur + 8 * dc);
+        }
+#pragma unroll
+        for (int u = 0; u < NPT; ++u) {
+            const int j = pg + NG * u;
+            if (j < np) {
+                const float e = sc[j];
+                const uint32_t ww[4] = {w8[u].x, w8[u].y, w8[u].z, w8[u].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    o8[2 * q] += e * mh_f16((uint16_t)(ww[q] & 0xffffu));
+                    o8[2 * q + 1] += e * mh_f16((uint16_t)(ww[q] >> 16));
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ob[pg * 64 + 8 * dc + q] = o8[q];
+        __syncthreads();
+        float o = 0.f;
+        if (i < 64)
+            for (int g2 = 0; g2 < NG; ++g2) o += ob[g2 * 64 + i];
+        __syncthreads();
+        // as the per-wave layout below: wave 0's row holds the sums, the
+        // other rows zero
+        for (int q = i; q < T / 64 * 256; q += T) ob[q] = 0.f;
+        __syncthreads();
+        if (i < 64) ob[i] = o;
+    } else {
+        // waves over positions (stride T / 64), lanes over dims; eight
+        // positions' loads issued before their products, which are still
+        // added in position order
+        constexpr int NW = T / 64, U = 8;
+        for (int i0 = 0; i0 < hd; i0 += 64) {
+            const int dm = i0 + lane;
+            float o = 0.f;
+            if (dm < hd) {
+                const uint16_t *vb = A.vc + (size_t)kh * hd + dm;
+                const float vslot = mh_f16(vcur[dm]);
+                int j = wv;
+                for (; j + NW * (U - 1) < np; j += NW * U) {
+                    float vv[U];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int tt = t0 + j + NW * u;
+                        vv[u] = tt == A.slot ? vslot : mh_f16(vb[(size_t)tt * A.kvd]);
+                    }
+#pragma unroll
+                    for (int u = 0; u < U; ++u) o += sc[j + NW * u] * vv[u];
+                }
+                for (; j < np; j += NW) {
+                    const int tt = t0 + j;
+                    o += sc[j] * (tt == A.slot ? vslot : mh_f16(vb[(size_t)tt * A.kvd]));
+                }
+            }
+            if (dm < 256) ob[wv * 256 + dm] = dm < hd ? o : 0.f;
+        }
+    }
     __syncthreads();
-    if (threadIdx.x < hd) {
-        float r = 0.f;
-        for (int q = 0; q < nq; ++q) r += acc[q * hd + threadIdx.x];
-        A.ao[(size_t)h * hd + threadIdx.x] = r;
+    if (A.S == 1) {   // one split: the combine's arithmetic without the memory round trip
+        float M = m;
+        const float sinkv = A.sinks ? A.sink[h] : -1e30f;
+        if (sinkv > M) M = sinkv;
+        const float f = expf(m - M);
+        float den = l * f;
+        if (A.sinks) den += expf(sinkv - M);
+        const float inv = 1.0f / den;
+        for (int dm = i; dm < hd; dm += T) {
+            float o = 0.f;
+#pragma unroll
+            for (int w = 0; w < T / 64; ++w) o += ob[w * 256 + dm];
+            A.ao[(size_t)h * hd + dm] = o * f * inv;
+        }
+        return;
     }
+    float *pp = A.part + ((size_t)h * A.S + s) * (hd + 2);
+    for (int dm = i; dm < hd; dm += T) {
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < T / 64; ++w) o += ob[w * 256 + dm];
+        __hip_atomic_store(pp + dm, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (i == 0) {
+        __hip_atomic_store(pp + hd, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + hd + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // ---------------------------------------------------------- combine
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (i == 0)
+        s_last = __hip_atomic_fetch_add(&A.cnt[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)A.S - 1u;
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (i == 0) __hip_atomic_store(&A.cnt[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // after the acquire, plain loads in one round: every split's m and l
+    // into LDS, then each thread's o values
+    const float *ph = A.part + (size_t)h * A.S * (hd + 2);
+    for (int q = i; q < A.S; q += T) {
+        s_m[q] = ph[(size_t)q * (hd + 2) + hd];
+        s_l[q] = ph[(size_t)q * (hd + 2) + hd + 1];
+    }
+    __syncthreads();
+    float M = -1e30f;
+    for (int q = 0; q < A.S; ++q) M = fmaxf(M, s_m[q]);
+    const float sinkv = A.sinks ? A.sink[h] : -1e30f;
+    if (sinkv > M) M = sinkv;
+    float den = 0.f;
+    for (int q = 0; q < A.S; ++q) den += s_l[q] * expf(s_m[q] - M);
+    if (A.sinks) den += expf(sinkv - M);
+    const float inv = 1.0f / den;
+    for (int dm = i; dm < hd; dm += T) {
+        float o = 0.f;
+        for (int q = 0; q < A.S; ++q) o += ph[(size_t)q * (hd + 2) + dm] * expf(s_m[q] - M);
+        A.ao[(size_t)h * hd + dm] = o * inv;
+    }
+}
+
+__global__ void k_attn_clear(unsigned *p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
 }
 
 // y = o + bias; x += y (two roundings, as wk_addbias then the residual loop)
@@ -350,6 +534,8 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
         return fail(MH_E_ARG, "mh_attention_dev: shape (hidden %lld, heads %d/%d, head_dim %d, ctx %d)", (long long)H,
                     nh, nkv, hd, L->ctx);
     if (pos < 0 || pos >= L->ctx) return fail(MH_E_ARG, "mh_attention_dev: position %d outside [0, %d)", pos, L->ctx);
+    if ((int64_t)std::min(L->ctx, L->window > 0 ? L->window : L->ctx) > (int64_t)kSplitT * kSplitP * kMaxSplits)
+        return fail(MH_E_UNSUPPORTED, "mh_attention_dev: more than %d cached positions", kSplitT * kSplitP * kMaxSplits);
     if (L->qk_norm && (!L->qn || !L->kn)) return fail(MH_E_ARG, "mh_attention_dev: qk_norm without weights");
     if (L->sinks && !L->sink) return fail(MH_E_ARG, "mh_attention_dev: sinks without values");
     const int kvd = nkv * hd, qd = nh * hd;
@@ -380,15 +566,36 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
     MH_TRY(resolve_dev(L->kc, (uint64_t)cap * kvd * 2, "attention k cache"));
     MH_TRY(resolve_dev(L->vc, (uint64_t)cap * kvd * 2, "attention v cache"));
     MH_TRY(resolve_dev(x, (uint64_t)H * 4, "mh_attention_dev x"));
-    // scratch: xb / o [H], q [qd], k, v [kvd], scores [nh][cap], ao [qd]
-    const size_t oq = ((size_t)H * 4 + 255) & ~(size_t)255, ok = oq + (((size_t)qd * 4 + 255) & ~(size_t)255);
-    const size_t ov = ok + (((size_t)kvd * 4 + 255) & ~(size_t)255), oa = ov + (((size_t)kvd * 4 + 255) & ~(size_t)255);
-    const size_t oo = oa + (((size_t)nh * cap * 4 + 255) & ~(size_t)255), total = oo + (size_t)qd * 4;
+    // scratch: the heads' arrival counters [nh] (zeroed when the slot is
+    // (re)allocated; every call leaves them zero), xb / o [H], q [qd], k, v
+    // [kvd], the splits' partials [nh][S][hd + 2], ao [qd]
+    const int nctx = pos + 1 < cap ? pos + 1 : cap;
+    // up to 256 cached positions (the sliding layers): 256-thread blocks,
+    // one position per thread; beyond: 1024 threads, two positions each
+    const bool small = nctx <= 256;
+    const int P = small ? 256 : kSplitT * kSplitP;
+    const int S = (nctx + P - 1) / P;
+    const size_t oc = 0, ox = ((size_t)nh * 4 + 255) & ~(size_t)255;
+    const size_t oq = ox + (((size_t)H * 4 + 255) & ~(size_t)255), ok = oq + (((size_t)qd * 4 + 255) & ~(size_t)255);
+    const size_t ov = ok + (((size_t)kvd * 4 + 255) & ~(size_t)255), op = ov + (((size_t)kvd * 4 + 255) & ~(size_t)255);
+    const size_t oo = op + (((size_t)nh * S * (hd + 2) * 4 + 255) & ~(size_t)255), total = oo + (size_t)qd * 4;
+    // sized for the longest context, so the slot is not reallocated as the
+    // context grows
+    const int Smax = (cap + kSplitT * kSplitP - 1) / (kSplitT * kSplitP);
+    const size_t total_max = total + (size_t)nh * (Smax - S) * (hd + 2) * 4 + 256;
     void *p;
-    MH_TRY(scratch(S_ATTN, total, &p));
+    MH_TRY(scratch(S_ATTN, total_max, &p));
+    static void *cleared = nullptr;
+    static int cleared_nh = 0;
     uint8_t *b8 = (uint8_t *)p;
-    float *xb = (float *)b8, *q = (float *)(b8 + oq), *k = (float *)(b8 + ok), *v = (float *)(b8 + ov);
-    float *att = (float *)(b8 + oa), *ao = (float *)(b8 + oo);
+    unsigned *cnt = (unsigned *)(b8 + oc);
+    if (p != cleared || nh > cleared_nh) {
+        MH_LAUNCH("attn_clear", k_attn_clear, dim3(1), dim3(256), 0, stream(), cnt, nh);
+        cleared = p;
+        cleared_nh = nh;
+    }
+    float *xb = (float *)(b8 + ox), *q = (float *)(b8 + oq), *k = (float *)(b8 + ok), *v = (float *)(b8 + ov);
+    float *part = (float *)(b8 + op), *ao = (float *)(b8 + oo);
     hipStream_t s = stream();
     MH_TRY(launch_rmsnorm(x, (const float *)an, xb, H, L->norm_eps, 1, s));
     {
@@ -407,14 +614,13 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
             MH_TRY(launch_gemv(wv, xb, v, 1, s));
         }
     }
-    PrepArgs P{q, k, v, (const float *)bq, (const float *)bk, (const float *)bv, (const float *)qn, (const float *)kn,
-               (const float *)co + (size_t)pos * (hd / 2), (const float *)si + (size_t)pos * (hd / 2), L->kc, L->vc,
-               nh, nkv, hd, pos % cap, L->qk_norm ? 1 : 0, L->norm_eps};
-    MH_LAUNCH("attn_prep", k_attn_prep, dim3((unsigned)(nh + nkv)), dim3((unsigned)((hd + 63) / 64 * 64)), 0, s, P);
-    const int kvec = hd % 8 == 0 && (uintptr_t)L->kc % 16 == 0;
-    HeadArgs A{q, (const float *)sk, L->kc, L->vc, att, ao, hd, nh / nkv, kvd, pos + 1 < cap ? pos + 1 : cap, cap,
-               L->sinks ? 1 : 0, kvec, L->attn_scale};
-    MH_LAUNCH("attn_heads", k_attn_heads, dim3((unsigned)nh), dim3(kHeadThreads), 0, s, A);
+    const int kvec = hd % 8 == 0 && (uintptr_t)L->kc % 16 == 0 && (uintptr_t)L->vc % 16 == 0;
+    SplitArgs A{q, k, v, (const float *)bq, (const float *)bk, (const float *)bv, (const float *)qn, (const float *)kn,
+                (const float *)co + (size_t)pos * (hd / 2), (const float *)si + (size_t)pos * (hd / 2),
+                (const float *)sk, L->kc, L->vc, part, cnt, ao, nh, hd, nh / nkv, kvd, nctx, pos % cap, S,
+                L->sinks ? 1 : 0, L->qk_norm ? 1 : 0, kvec, L->attn_scale, L->norm_eps};
+    if (small) MH_LAUNCH("attn_split", (k_attn_split<256, 1>), dim3((unsigned)(nh * S)), dim3(256), 0, s, A);
+    else MH_LAUNCH("attn_split", (k_attn_split<kSplitT, kSplitP>), dim3((unsigned)(nh * S)), dim3(kSplitT), 0, s, A);
     bool fused = false;
     switch (wo.dt) {
     case MH_DT_F32: MH_TRY(launch_o_res_t<MH_DT_F32>(wo, ao, (const float *)bo, x, s, &fused)); break;
