@@ -408,7 +408,17 @@ def test_sample_dev_nucleus_paths(mh, shape):
     out.free()
 
 
-@pytest.mark.parametrize("name", ["small_sliding_sinks", "small_full_qknorm", "gpt_oss"])
+# Past 256 cached positions the split kernel runs 1024-thread blocks of 2048
+# positions, and past 2048 a head's splits are combined by the last to
+# finish: full-attention layers of 2200 positions reach both, with head_dim
+# 64 (16-byte cache loads) and 32 (the per-element path).
+LONG_ATTN_SHAPES = {
+    "long_full_hd64_sinks": dict(hidden=256, nh=4, nkv=2, hd=64, ctx=2200, window=0, qk_norm=0, sinks=1),
+    "long_full_hd32_qknorm": dict(hidden=256, nh=4, nkv=2, hd=32, ctx=2200, window=0, qk_norm=1, sinks=0),
+}
+
+
+@pytest.mark.parametrize("name", ["small_sliding_sinks", "small_full_qknorm", "gpt_oss", *LONG_ATTN_SHAPES])
 def test_attention_dev_vs_oracle(mh, name):
     # attention() for a run of decode positions (past the sliding window, so
     # the ring wraps): the device x and f16 caches against the oracle's
@@ -416,7 +426,7 @@ def test_attention_dev_vs_oracle(mh, name):
     import ctypes
     from test_oracle_kernels import ATTN_DIV_FIXTURE, ATTN_SHAPES, GPT_OSS_ATTN, GPT_OSS_ROPE, AttnHost
     from midge_amd import _lib
-    cfgs = dict(ATTN_SHAPES, gpt_oss=GPT_OSS_ATTN)
+    cfgs = dict(ATTN_SHAPES, gpt_oss=GPT_OSS_ATTN, **LONG_ATTN_SHAPES)
     cfg = cfgs[name]
     say(f"attention_dev {name}")
     host = AttnHost(**cfg, seed=13, rope=GPT_OSS_ROPE if name == "gpt_oss" else None)
@@ -460,13 +470,24 @@ def test_attention_dev_vs_oracle(mh, name):
     # cache, 8 query heads share each cached value and the peaked softmax
     # amplifies score differences); each position is held to max(1e-3,
     # twice the reference's divergence there), the mean to twice its mean.
+    # The long shapes measure that divergence here (the compiled reference's
+    # AVX2 build against the oracle, which is its scalar build bit for bit).
+    # Over 2199 positions a last-bit difference in a projection flips the f16
+    # rounding of ~0.3% of the cached values, at different places in the
+    # GPU's cache and in the AVX2 build's, so the two builds' errors peak at
+    # different positions: the worst over the run is held to max(1e-4,
+    # twice the reference's worst), the mean to max(2e-5, twice its mean).
+    long = name in LONG_ATTN_SHAPES
+    if long and not po.have_ref():
+        pytest.fail("the compiled reference (oracle/_ref) is missing: it sets this shape's bar")
     if name == "gpt_oss":
         div = np.load(ATTN_DIV_FIXTURE)["div"]
         assert len(div) == cfg["ctx"] - 1
         bars, mean_bar = np.maximum(1e-3, 2.0 * div), 2.0 * float(div.mean())
     else:
         bars, mean_bar = np.full(cfg["ctx"] - 1, 1e-4), 2e-5
-    errs = []
+    avx = AttnHost(**cfg, seed=13) if long else None
+    errs, divs = [], []
     for pos in range(cfg["ctx"] - 1):
         x = rng.standard_normal(H).astype(np.float32)
         want = host.run(po.oracle().mo_attention, x, pos)
@@ -475,8 +496,15 @@ def test_attention_dev_vs_oracle(mh, name):
         got = xd.download(np.float32, (H,))
         err = rel_l2(got - x, want - x)
         errs.append(err)
-        assert err < bars[pos], (pos, err, bars[pos])
+        if long:
+            divs.append(rel_l2(avx.run(po.ref().ref_attention, x, pos) - x, want - x))
+        else:
+            assert err < bars[pos], (pos, err, bars[pos])
     errs = np.array(errs)
+    if long:
+        mean_bar = max(2e-5, 2.0 * float(np.mean(divs)))
+        say(f"attention_dev {name}: the reference's own divergence worst {max(divs):.3g}, mean {np.mean(divs):.3g}")
+        assert errs.max() < max(1e-4, 2.0 * max(divs)), (int(errs.argmax()), errs.max(), max(divs))
     say(f"attention_dev {name}: worst {errs.max():.3g} at {int(errs.argmax())}, mean {errs.mean():.3g}")
     assert errs.mean() < mean_bar, (errs.mean(), mean_bar)
     kcg = kc_d.download(np.uint16, host.kc.shape)
