@@ -9,9 +9,11 @@
 //   per CU). Block (slot i, index gi) owns gate/up pairs [PB gi, +PB) and
 //   down rows [RB gi, +RB) of slot i's expert, so a block's work touches one
 //   expert and its h comes from its own group of G blocks. Per layer:
-//     A  every block reads x (the previous layer's output, tagged words from
-//        one of kXR copies) and forms xb = rmsnorm(x) * w in LDS; blocks
-//        b < E compute router logit b and publish it in kLR copies;
+//     A  every block forms x itself: R.x at layer 0, else the previous
+//        layer's x plus moe = sum_i w_i y_i (engine/midge.c:544-548) from the
+//        y words every block published (one of kYR copies); then xb =
+//        rmsnorm(x) * w in LDS; blocks b < E compute router logit b and
+//        publish it in kLR copies;
 //     R  every block's first wave gathers the logits and ranks them itself
 //        (stable top-k, ties to the lower index): all blocks reach the same
 //        selection and weights and nothing is broadcast;
@@ -22,14 +24,14 @@
 //        (h as two f16 terms) to the slot's group;
 //     C  the down rows are staged in LDS; each wave polls only the part of
 //        h that its matrix-core K steps read and multiplies (f16 MFMA); the
-//        down bias completes y_i for the block's rows, which slots i > 0
-//        publish as tagged words;
-//     D  the slot-0 block of each row slice gathers y_1 .. y_{K-1} of its
-//        rows, forms moe = sum_i w_i y_i in selection order and x += moe
-//        (engine/midge.c:544-548), and publishes x in kXR copies.
+//        down bias completes y_i for the block's rows;
+//     D  every block publishes its rows of y_i in kYR copies (32-bit words
+//        with a 4-bit tag, double-buffered by layer parity); after the last
+//        layer the slot-0 block of each row slice forms x += moe for its
+//        rows into R.x.
 //   There is no grid-wide barrier: every exchange is a tagged word the
-//   consumer polls, and every block's y is waited for once per layer, which
-//   also orders the reuse of the exchange buffers from layer to layer.
+//   consumer polls, and every block gathers every block's y once per layer,
+//   which also orders the reuse of the exchange buffers from layer to layer.
 //
 // k_decode_step — the vector-ALU path (q4g32 experts, plain SiLU, down
 //   scales the f16 path cannot hold exactly). One block per CU; a block
@@ -98,12 +100,11 @@ struct GrpArgs {             // k_decode_grp
     uint64_t stride;
     uint64_t off[9];
     float alpha, limit;
-    uint64_t *xw;            // [kXR][xws] tagged x
-    int xws;
     uint64_t *hw;            // [kHR][K][hws] tagged h (payload: hi f16 | lo f16 << 16)
     int hws;
-    uint64_t *yw;            // [K][H] tagged y of slots 1 .. K-1
-    unsigned *flags;         // [gridDim.x] per-block flags (layers with an unfilled slot)
+    uint32_t *yw;            // [2][kYR][K][yws] y words (layer parity, copy, slot): f32 with a 4-bit tag
+    int yws;
+    unsigned *flags;         // [gridDim.x] per-block flags: x of layer 0 read
     unsigned seq0;           // first sequence number of this launch (4 per layer)
 };
 
@@ -120,12 +121,12 @@ constexpr unsigned kSpinLimit = 1u << 20;
 constexpr int kStamps = 24;     // phase timestamps per layer and block while profiling
 constexpr int kEL = 2;          // logits per lane in the routing wave (E <= 64 * kEL)
 constexpr int kLR = 8;          // copies of the logits (each polled by NB / kLR blocks)
-constexpr int kXR = 8;          // copies of x (k_decode_grp)
+constexpr int kYR = 8;          // copies of y (k_decode_grp: each polled by NB / kYR blocks)
 constexpr int kHR = 2;          // copies of h (k_decode_grp: each polled by G / kHR blocks)
 constexpr int kGoCopies = 8;    // copies of the barrier's release word
 constexpr int kGoStride = 64;   // words between them (256 B)
 constexpr int kMaxK = 16;       // engine/midge.c:44 MAX_TOPK
-constexpr int kMaxGrpK = 8;     // top-k of k_decode_grp (its combine polls (k - 1) x kRBMax words)
+constexpr int kMaxGrpK = 4;     // top-k of k_decode_grp (every block gathers k x H words of y per layer)
 // static LDS capacities (plan creation checks a stack against them)
 constexpr int kHMax = 3072;         // hidden size
 constexpr int kResMax = 1024;       // floats of reduced rows
@@ -274,6 +275,26 @@ __device__ __forceinline__ uint64_t ld_tag(uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ bool tag_is(uint64_t w, unsigned tag) { return (unsigned)(w >> 32) == tag; }
+
+// y words (k_decode_grp): one 32-bit word per value, an f32 rounded to a
+// multiple of 16 units in the last place (within 2^-20 relative; inf and nan
+// keep their class) whose low 4 bits carry the producer's sequence number
+// mod 15, plus 1, so that zeroed memory never reads as ready. A location is
+// written once per two layers, and every reader has read its previous value
+// before it is written again, so a value 15 writes old cannot be met.
+__device__ __forceinline__ uint32_t ynib(unsigned tag) { return tag % 15u + 1u; }
+__device__ __forceinline__ uint32_t y_word(float v, uint32_t nib) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t r = (u & 0x7F800000u) == 0x7F800000u ? u : u + 8u;   // a carry rounds up into the exponent
+    return (r & ~15u) | nib;
+}
+__device__ __forceinline__ float y_val(uint32_t w) { return __uint_as_float(w & ~15u); }
+__device__ __forceinline__ uint32_t ld_u32_dev(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_u32_dev(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Maximum over the wave (every lane gets it): DPP within rows of 16, then
 // row broadcasts; lanes a DPP step does not write keep their value.
@@ -440,9 +461,57 @@ struct RouteLds {
     float *xbs;      // xb = rmsnorm(x) * w in 32-element groups padded to 33 floats
 };
 
+// x of layer l from R.x (layer 0) or as tagged words from xsrc (tag xtag, the
+// previous layer's output that k_decode_step publishes): thread t gets
+// elements t + k kThreads (0 past H); each thread loads its <= kNX words and
+// re-polls only the late ones. Returns false (in every thread) if a wait
+// timed out.
+__device__ __forceinline__ bool gather_x_tagged(const RouteArgs &R, int l, uint64_t *xsrc, unsigned xtag,
+                                                float (&xv)[kNX]) {
+    const int H = R.H, t = threadIdx.x;
+    if (l == 0) {
+        const rsrc_t rx = make_rsrc(R.x, (uint32_t)H * 4u);
+#pragma unroll
+        for (int k = 0; k < kNX; ++k) xv[k] = ld_dev(rx, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
+        return true;
+    }
+    uint64_t wv[kNX];
+    const int tt = opaque(t);
+#pragma unroll
+    for (int k = 0; k < kNX; ++k) {
+        const int i = tt + k * kThreads;
+        wv[k] = i < H ? ld_tag(xsrc + i) : (uint64_t)xtag << 32;
+    }
+    bool late = false;
+    for (unsigned spins = 0;; ++spins) {
+        bool ready = true;
+#pragma unroll
+        for (int k = 0; k < kNX; ++k) ready = ready && tag_is(wv[k], xtag);
+        if (ready) break;
+        if (spins > kSpinLimit) {
+            late = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < kNX; ++k) {
+            const int i = tt + k * kThreads;
+            if (i < H && !tag_is(wv[k], xtag)) wv[k] = ld_tag(xsrc + i);
+        }
+    }
+    if (__syncthreads_or(late)) {
+        if (t == 0) raise_err(R.err);
+        return false;
+    }
+#pragma unroll
+    for (int k = 0; k < kNX; ++k) xv[k] = __uint_as_float((uint32_t)wv[k]);
+    return true;
+}
+
 // Phase A and the routing of layer l, common to both kernels.
-//  - x: from R.x at layer 0, else as tagged words from xsrc (tag xtag); each
-//    thread loads its <= kNX words and re-polls only the late ones.
+//  - x: getx(xv) fills this thread's elements t + k kThreads of x (0 past H)
+//    and returns false if a wait timed out (gather_x_tagged, or k_decode_grp's
+//    combine of the previous layer's y).
 //  - One DPP-reduced block sum gives both sum(x^2) and this block's router
 //    dot with x * w (the norm weights): logit b = inv * dot * scale + bias,
 //    with inv = 1 / sqrt(mean(x^2) + eps) factored out of the row's dot
@@ -457,50 +526,15 @@ struct RouteLds {
 //    usage counts. The block's other waves wait at the closing barrier.
 // Returns false, with the error flag raised, if a wait timed out (every
 // thread of the block returns the same value).
-template <int RDT>
-__device__ __forceinline__ bool route_layer(const RouteArgs &R, const RouterPref &pf, int l, uint64_t *xsrc,
-                                            unsigned xtag, unsigned ltag, const RouteLds &S, const Stamper &stamp) {
+template <int RDT, class GetX>
+__device__ __forceinline__ bool route_layer(const RouteArgs &R, const RouterPref &pf, int l, GetX getx,
+                                            unsigned ltag, const RouteLds &S, const Stamper &stamp) {
     const int H = R.H, E = R.E, K = R.K;
     const int NB = gridDim.x, b = blockIdx.x, t = threadIdx.x;
     const StepLayer Ly = R.layers[l];
     {
         float xv[kNX];
-        if (l == 0) {
-            const rsrc_t rx = make_rsrc(R.x, (uint32_t)H * 4u);
-#pragma unroll
-            for (int k = 0; k < kNX; ++k) xv[k] = ld_dev(rx, (uint32_t)(t + k * kThreads) * 4u);   // 0 past H
-        } else {
-            uint64_t wv[kNX];
-            const int tt = opaque(t);
-#pragma unroll
-            for (int k = 0; k < kNX; ++k) {
-                const int i = tt + k * kThreads;
-                wv[k] = i < H ? ld_tag(xsrc + i) : (uint64_t)xtag << 32;
-            }
-            bool late = false;
-            for (unsigned spins = 0;; ++spins) {
-                bool ready = true;
-#pragma unroll
-                for (int k = 0; k < kNX; ++k) ready = ready && tag_is(wv[k], xtag);
-                if (ready) break;
-                if (spins > kSpinLimit) {
-                    late = true;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-                for (int k = 0; k < kNX; ++k) {
-                    const int i = tt + k * kThreads;
-                    if (i < H && !tag_is(wv[k], xtag)) wv[k] = ld_tag(xsrc + i);
-                }
-            }
-            if (__syncthreads_or(late)) {
-                if (t == 0) raise_err(R.err);
-                return false;
-            }
-#pragma unroll
-            for (int k = 0; k < kNX; ++k) xv[k] = __uint_as_float((uint32_t)wv[k]);
-        }
+        if (!getx(xv)) return false;
         stamp(l, 15);
         float ss = 0.f, dp = 0.f;
 #pragma unroll
@@ -712,39 +746,104 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
     __shared__ __attribute__((aligned(16))) _Float16 s_hp[kThreads / 64][2 * kQ * 128];
     __shared__ float s_dred[kThreads / 64 * kRBMax];
     __shared__ float s_bd[kRBMax];
-    __shared__ float s_y[kMaxGrpK * kRBMax];   // the combine's y_i rows, then x
+    __shared__ float s_y[kMaxGrpK * kRBMax];   // the last layer's combine: y_i of the block's rows
     const RouteArgs &R = A.R;
     const int H = R.H, F = A.F, K = R.K;
     const int b = blockIdx.x, t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63;
-    const int slot = b / A.G, gi = b - slot * A.G;
+    // (Numbering the blocks so that each XCD runs a contiguous range of
+    // slots and rows was measured 2-3% slower than this plain order.)
+    const int NB = (int)gridDim.x, n = b;
+    const int slot = n / A.G, gi = n - slot * A.G;
     const int p0 = A.PB * gi, np = max(0, min(F - p0, A.PB));
     const int r0 = A.RB * gi, nr = max(0, min(H - r0, A.RB));   // >= 1 (plan check)
     const Stamper stamp{(R.trace && t == 0) ? R.trace + b : nullptr, (int)gridDim.x};
     const RouteLds S{s_part, s_sel, s_w, s_xs, s_xbs};
     const uint32_t layer_bytes = (uint32_t)((uint64_t)R.E * A.stride - 1u) + 1u;   // < 4 GiB (plan check)
-    uint64_t *xsrc = A.xw + (size_t)(b % kXR) * A.xws;
     uint64_t *hsrc = A.hw + (size_t)((gi % kHR) * K + slot) * A.hws;
+    const size_t ycopy = (size_t)K * A.yws;   // words between copies of y
     for (int l = 0; l < R.n_layers; ++l) {
         const StepLayer Ly = R.layers[l];
-        // sequence numbers of this layer: logits, h, y, and x for the next layer
-        const unsigned tagL = A.seq0 + 4u * (unsigned)l, tagH = tagL + 1u, tagY = tagL + 2u, tagX = tagL + 3u;
+        // sequence numbers of this layer: logits, h, y (the fourth is unused)
+        const unsigned tagL = A.seq0 + 4u * (unsigned)l, tagH = tagL + 1u, tagY = tagL + 2u;
         stamp(l, 0);
         {
+            // x (l): R.x at layer 0, else x (l - 1) + moe (l - 1) with moe =
+            // sum_i w_i y_i in selection order, each product and sum rounded
+            // on its own (engine/midge.c:544-548), from the y words every
+            // block published (layer l - 1's parity, copy n % kYR). Every
+            // block forms the same x from the same words with the previous
+            // layer's selection and weights (still in LDS).
+            auto getx = [&](float (&xv)[kNX]) __attribute__((always_inline)) {
+                if (l == 0) return gather_x_tagged(R, 0, nullptr, 0u, xv);
+                const uint32_t nib = ynib(tagL - 2u);
+                const uint32_t *ys = A.yw + (size_t)(((l - 1) & 1) * kYR + n % kYR) * ycopy;
+                // (branch-free: slots past K and elements past H re-read the
+                // last slot's last element, a word of this layer)
+                const int tt = opaque(t);
+                auto yaddr = [&](int s, int k) __attribute__((always_inline)) {
+                    return ys + (size_t)min(s, K - 1) * A.yws + min(tt + k * kThreads, H - 1);
+                };
+                uint32_t yv[kMaxGrpK][kNX];
+#pragma unroll
+                for (int s = 0; s < kMaxGrpK; ++s)
+#pragma unroll
+                    for (int k = 0; k < kNX; ++k) yv[s][k] = ld_u32_dev(yaddr(s, k));
+                bool late = false;
+                for (unsigned spins = 0;; ++spins) {
+                    bool ready = true;
+#pragma unroll
+                    for (int s = 0; s < kMaxGrpK; ++s)
+#pragma unroll
+                        for (int k = 0; k < kNX; ++k) ready = ready && (yv[s][k] & 15u) == nib;
+                    if (ready) break;
+                    if (spins > kSpinLimit) {
+                        late = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                    for (int k = 0; k < kNX; ++k) {   // an element's K words are re-read together
+                        bool rd = true;
+#pragma unroll
+                        for (int s = 0; s < kMaxGrpK; ++s) rd = rd && (yv[s][k] & 15u) == nib;
+                        if (!rd) {
+#pragma unroll
+                            for (int s = 0; s < kMaxGrpK; ++s) yv[s][k] = ld_u32_dev(yaddr(s, k));
+                        }
+                    }
+                }
+                if (__syncthreads_or(late)) {
+                    if (t == 0) raise_err(R.err);
+                    return false;
+                }
+#pragma unroll
+                for (int k = 0; k < kNX; ++k) {
+#pragma clang fp contract(off)
+                    const int i = t + k * kThreads;
+                    float moe = 0.f;
+#pragma unroll
+                    for (int s = 0; s < kMaxGrpK; ++s)
+                        if (s < K && s_sel[s] >= 0) moe = moe + s_w[s] * y_val(yv[s][k]);
+                    xv[k] = i < H ? s_xs[min(i, H - 1)] + moe : 0.f;
+                }
+                return true;
+            };
             // the router row's loads are issued here and land while x is on
             // its way (held across the layer they would cost 18 registers)
             const RouterPref pf = prefetch_router<RDT>(R, l);
-            if (!route_layer<RDT>(R, pf, l, xsrc, tagL - 1u, tagL, S, stamp)) return;
+            if (!route_layer<RDT>(R, pf, l, getx, tagL, S, stamp)) return;
         }
+        // x (0) read: the last layer's combine overwrites R.x only once every
+        // block has raised this flag
+        if (l == 0 && t == 0) __hip_atomic_store(&A.flags[b], A.seq0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         stamp(l, 2);
         const int e = s_sel[slot];   // block-uniform
-        // A slot with nothing routed (fewer than k logits above -1e30) takes
-        // its blocks out of the h exchange, the one wait that otherwise
-        // shows a block has read x; in such a layer every block raises a
-        // flag once it has routed, and x (l + 1) is published after all are
-        // up. (Every block ranks the same logits, so all agree on this.)
-        const bool unfilled = s_sel[K - 1] < 0;
-        if (unfilled && t == 0) __hip_atomic_store(&A.flags[b], tagY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // A slot with nothing routed (fewer than k logits above -1e30) skips
+        // the h exchange and publishes y = 0. Every block gathers every
+        // block's y at the next layer's start, which orders the reuse of the
+        // exchange buffers (the logits, h, and y of the same parity) from
+        // layer to layer.
         float y = 0.f;               // row t of this slot's y (t < nr)
         if (e >= 0) {
             const rsrc_t rex = make_rsrc(Ly.experts, layer_bytes);
@@ -943,36 +1042,46 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                 y = sum + s_bd[t];   // the matvec, then wk_addbias (engine/midge.c:539-541)
             }
         }
-        // y of slots 1.. goes to the slot-0 block of the same rows (a slot
-        // with nothing routed publishes 0, so that its rows are marked done)
-        if (slot > 0 && t < nr) st_tag(A.yw + (size_t)slot * H + r0 + t, tagY, y);
+        // -------------------------------------- D: y
+        // every block publishes its rows of its slot's y (0 for a slot with
+        // nothing routed) in kYR copies of the layer's parity
+        const uint32_t nibY = ynib(tagY);
+        uint32_t *yd = A.yw + (size_t)((l & 1) * kYR) * ycopy + (size_t)slot * A.yws + r0;
+        if (t < nr) {
+            const uint32_t yw = y_word(y, nibY);
+#pragma unroll
+            for (int cp = 0; cp < kYR; ++cp) st_u32_dev(yd + (size_t)cp * ycopy + t, yw);
+        }
         stamp(l, 14);
-        // -------------------------------------- D: combine (slot 0)
-        if (slot == 0) {
-            // thread (slot i >= 1, row j) polls y_i[j]; the values meet in LDS
+        // the last layer's combine (slot 0 of each row slice): x (L) = x (L - 1)
+        // + moe, from the same y words the other layers' gathers read, written
+        // to R.x once every block has read x (0) from there
+        if (l + 1 == R.n_layers && slot == 0) {
             bool late = false;
             const int tq = opaque(t);
-            const int iq = 1 + tq / kRBMax, jq = tq - (iq - 1) * kRBMax;
-            if (iq < K && jq < nr) {
-                uint64_t *yp = A.yw + (size_t)iq * H + r0 + jq;
-                uint64_t yw = ld_tag(yp);
-                for (unsigned spins = 0; !tag_is(yw, tagY); ++spins) {
-                    if (spins > kSpinLimit) {
-                        late = true;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                    yw = ld_tag(yp);
+            const int iq = tq / kRBMax, jq = tq - iq * kRBMax;
+            const bool hasy = iq < K && jq < nr;
+            const uint32_t *yp = A.yw + (size_t)((l & 1) * kYR + n % kYR) * ycopy + (size_t)iq * A.yws + r0 + jq;
+            uint32_t yw = hasy ? ld_u32_dev(yp) : nibY;
+            bool up = true;
+            for (int i = tq; i < NB; i += kThreads)
+                up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.seq0;
+            for (unsigned spins = 0; (yw & 15u) != nibY || !up; ++spins) {
+                if (spins > kSpinLimit) {
+                    late = true;
+                    break;
                 }
-                s_y[iq * kRBMax + jq] = __uint_as_float((uint32_t)yw);
+                __builtin_amdgcn_s_sleep(1);
+                if ((yw & 15u) != nibY) yw = ld_u32_dev(yp);
+                up = true;
+                for (int i = tq; i < NB; i += kThreads)
+                    up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.seq0;
             }
-            if (t < nr) s_y[t] = y;
+            if (hasy) s_y[iq * kRBMax + jq] = y_val(yw);
             if (__syncthreads_or(late)) {
                 if (t == 0) raise_err(R.err);
                 return;
             }
-            // moe = sum_i w_i y_i in selection order, then x += moe, each
-            // product and sum rounded on its own (engine/midge.c:544-548)
             if (t < nr) {
 #pragma clang fp contract(off)
                 float moe = 0.f;
@@ -980,34 +1089,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                     if (s_sel[i] < 0) continue;
                     moe = moe + s_w[i] * s_y[i * kRBMax + t];
                 }
-                const float xn = s_xs[r0 + t] + moe;
-                if (l + 1 < R.n_layers) s_y[t] = xn;   // (slot 0's y is consumed)
-                else st_dev(R.x + r0 + t, xn);
-            }
-            if (unfilled && l + 1 < R.n_layers) {
-                if (t < 64) {
-                    for (unsigned spins = 0;; ++spins) {
-                        bool up = true;
-                        for (int i = t; i < (int)gridDim.x; i += 64)
-                            up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tagY;
-                        if (__all(up)) break;
-                        if (spins > kSpinLimit) {
-                            late = true;
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(1);
-                    }
-                }
-                if (__syncthreads_or(late)) {
-                    if (t == 0) raise_err(R.err);
-                    return;
-                }
-            }
-            if (l + 1 < R.n_layers) {
-                __syncthreads();
-                // thread (copy cp, row j) publishes x[r0 + j] in copy cp
-                const int cp = tq / kRBMax, j = tq - cp * kRBMax;
-                if (cp < kXR && j < nr) st_tag(A.xw + (size_t)cp * A.xws + r0 + j, tagX, s_y[j]);
+                st_dev(R.x + r0 + t, s_xs[r0 + t] + moe);
             }
         }
         stamp(l, 6);
@@ -1045,7 +1127,10 @@ __global__ void __launch_bounds__(kThreads) k_decode_step(StepArgs A) {
         // phase, x for the next layer
         const unsigned tagA = A.seq0 + 3u * (unsigned)l, tagB = tagA + 1u, tagC = tagA + 2u;
         stamp(l, 0);
-        if (!route_layer<RDT>(R, pf, l, A.xw, tagA - 1u, tagA, S, stamp)) return;
+        auto getx = [&](float (&xv)[kNX]) __attribute__((always_inline)) {
+            return gather_x_tagged(R, l, A.xw, tagA - 1u, xv);
+        };
+        if (!route_layer<RDT>(R, pf, l, getx, tagA, S, stamp)) return;
         stamp(l, 2);
 
         // ------------------------------------------------ B: gate/up
@@ -1353,10 +1438,12 @@ static void plan_release(void *key) {
     p->flat = p->grp = p->ok = 0;
 }
 
-// Exchange-word layout in StepPlan::tagged: the logits' kLR copies, x's kXR
-// copies, h's kHR x K planes, y's K rows (offsets in words).
+// Exchange-word layout in StepPlan::tagged (offsets in 64-bit words): the
+// logits' kLR copies; x (k_decode_step); h's kHR x K planes (k_decode_grp);
+// y's 2 parities x kYR copies x K rows of 32-bit words (k_decode_grp; yws
+// in 32-bit words).
 struct TagLayout {
-    int lws, xws, hws;
+    int lws, xws, hws, yws;
     size_t lw, xw, hw, yw, total;
 };
 static TagLayout tag_layout(const DevLayer &L0) {
@@ -1364,11 +1451,12 @@ static TagLayout tag_layout(const DevLayer &L0) {
     t.lws = copy_stride(L0.n_experts);
     t.xws = copy_stride((int)L0.hidden);
     t.hws = copy_stride((int)L0.ffn);
+    t.yws = copy_stride((int)L0.hidden);
     t.lw = 0;
     t.xw = t.lw + (size_t)kLR * t.lws;
-    t.hw = t.xw + (size_t)kXR * t.xws;
+    t.hw = t.xw + (size_t)t.xws;
     t.yw = t.hw + (size_t)kHR * L0.top_k * t.hws;
-    t.total = t.yw + (size_t)L0.top_k * L0.hidden;
+    t.total = t.yw + ((size_t)2 * kYR * L0.top_k * t.yws + 1) / 2;
     return t;
 }
 
@@ -1647,11 +1735,10 @@ int step_run(StepPlan *p, const DevLayer *layers, int first, int n_layers, float
         for (int i = 0; i < 9; i++) A.off[i] = L0.off[i];
         A.alpha = L0.alpha;
         A.limit = L0.limit;
-        A.xw = p->tagged + tl.xw;
-        A.xws = tl.xws;
         A.hw = p->tagged + tl.hw;
         A.hws = tl.hws;
-        A.yw = p->tagged + tl.yw;
+        A.yw = (uint32_t *)(p->tagged + tl.yw);
+        A.yws = tl.yws;
         A.flags = p->flags;
         A.seq0 = seq0;
         rc = q8 ? launch_grp<MH_DT_Q8R>(A, nb, s) : launch_grp<MH_DT_F32>(A, nb, s);
