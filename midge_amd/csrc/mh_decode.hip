@@ -104,8 +104,10 @@ struct GrpArgs {             // k_decode_grp
     int hws;
     uint32_t *yw;            // [2][kYR][K][yws] y words (layer parity, copy, slot): f32 with a 4-bit tag
     int yws;
-    unsigned *flags;         // [gridDim.x] per-block flags: x of layer 0 read
+    uint64_t *y1;            // [K][yws] tagged y of slots 1.. (one-layer launches)
+    unsigned *flags;         // [gridDim.x] per-block flags: x of layer 0 read (one-layer launches)
     unsigned seq0;           // first sequence number of this launch (4 per layer)
+    unsigned bank;           // the y tags' bank: the plan's count of launches of several layers, mod 2
 };
 
 namespace {
@@ -129,6 +131,7 @@ constexpr int kMaxK = 16;       // engine/midge.c:44 MAX_TOPK
 constexpr int kMaxGrpK = 4;     // top-k of k_decode_grp (every block gathers k x H words of y per layer)
 // static LDS capacities (plan creation checks a stack against them)
 constexpr int kHMax = 3072;         // hidden size
+constexpr int kNG = (kHMax + kThreads - 1) / kThreads;   // x elements per thread in k_decode_grp's y gather
 constexpr int kResMax = 1024;       // floats of reduced rows
 constexpr int kRedMax = 8192;       // floats of partial sums
 constexpr int kQ = 3;               // 128-column K steps per wave (ffn <= 8 * kQ * 128)
@@ -278,11 +281,16 @@ __device__ __forceinline__ bool tag_is(uint64_t w, unsigned tag) { return (unsig
 
 // y words (k_decode_grp): one 32-bit word per value, an f32 rounded to a
 // multiple of 16 units in the last place (within 2^-20 relative; inf and nan
-// keep their class) whose low 4 bits carry the producer's sequence number
-// mod 15, plus 1, so that zeroed memory never reads as ready. A location is
-// written once per two layers, and every reader has read its previous value
-// before it is written again, so a value 15 writes old cannot be met.
-__device__ __forceinline__ uint32_t ynib(unsigned tag) { return tag % 15u + 1u; }
+// keep their class) whose low 4 bits carry a tag, never 0 (zeroed memory
+// never reads as ready). Launches alternate between two banks of tags (1..7
+// and 8..14); within a launch the tag of layer l is its bank's (l / 2) mod 7.
+// Every launch of several layers writes every y location at least once (a
+// one-layer launch uses its own tagged words instead), and kernel boundaries
+// order one launch's stores before the next launch's loads, so a location
+// holds this launch's words or the previous launch's (the other bank); within
+// a launch a location is written once per two layers and every reader has
+// read its previous value before it is written again.
+__device__ __forceinline__ uint32_t ynib(unsigned bank, int l) { return 1u + 7u * bank + (unsigned)(l >> 1) % 7u; }
 __device__ __forceinline__ uint32_t y_word(float v, uint32_t nib) {
     const uint32_t u = __float_as_uint(v);
     const uint32_t r = (u & 0x7F800000u) == 0x7F800000u ? u : u + 8u;   // a carry rounds up into the exponent
@@ -776,7 +784,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
             // layer's selection and weights (still in LDS).
             auto getx = [&](float (&xv)[kNX]) __attribute__((always_inline)) {
                 if (l == 0) return gather_x_tagged(R, 0, nullptr, 0u, xv);
-                const uint32_t nib = ynib(tagL - 2u);
+                const uint32_t nib = ynib(A.bank, l - 1);
                 const uint32_t *ys = A.yw + (size_t)(((l - 1) & 1) * kYR + n % kYR) * ycopy;
                 // (branch-free: slots past K and elements past H re-read the
                 // last slot's last element, a word of this layer)
@@ -784,18 +792,18 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                 auto yaddr = [&](int s, int k) __attribute__((always_inline)) {
                     return ys + (size_t)min(s, K - 1) * A.yws + min(tt + k * kThreads, H - 1);
                 };
-                uint32_t yv[kMaxGrpK][kNX];
+                uint32_t yv[kMaxGrpK][kNG];
 #pragma unroll
                 for (int s = 0; s < kMaxGrpK; ++s)
 #pragma unroll
-                    for (int k = 0; k < kNX; ++k) yv[s][k] = ld_u32_dev(yaddr(s, k));
+                    for (int k = 0; k < kNG; ++k) yv[s][k] = ld_u32_dev(yaddr(s, k));
                 bool late = false;
                 for (unsigned spins = 0;; ++spins) {
                     bool ready = true;
 #pragma unroll
                     for (int s = 0; s < kMaxGrpK; ++s)
 #pragma unroll
-                        for (int k = 0; k < kNX; ++k) ready = ready && (yv[s][k] & 15u) == nib;
+                        for (int k = 0; k < kNG; ++k) ready = ready && (yv[s][k] & 15u) == nib;
                     if (ready) break;
                     if (spins > kSpinLimit) {
                         late = true;
@@ -803,7 +811,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                     }
                     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-                    for (int k = 0; k < kNX; ++k) {   // an element's K words are re-read together
+                    for (int k = 0; k < kNG; ++k) {   // an element's K words are re-read together
                         bool rd = true;
 #pragma unroll
                         for (int s = 0; s < kMaxGrpK; ++s) rd = rd && (yv[s][k] & 15u) == nib;
@@ -822,9 +830,11 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
 #pragma clang fp contract(off)
                     const int i = t + k * kThreads;
                     float moe = 0.f;
+                    if (k < kNG) {
 #pragma unroll
-                    for (int s = 0; s < kMaxGrpK; ++s)
-                        if (s < K && s_sel[s] >= 0) moe = moe + s_w[s] * y_val(yv[s][k]);
+                        for (int s = 0; s < kMaxGrpK; ++s)
+                            if (s < K && s_sel[s] >= 0) moe = moe + s_w[s] * y_val(yv[s][min(k, kNG - 1)]);
+                    }
                     xv[k] = i < H ? s_xs[min(i, H - 1)] + moe : 0.f;
                 }
                 return true;
@@ -836,7 +846,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
         }
         // x (0) read: the last layer's combine overwrites R.x only once every
         // block has raised this flag
-        if (l == 0 && t == 0) __hip_atomic_store(&A.flags[b], A.seq0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (l == 0 && R.n_layers == 1 && t == 0)
+            __hip_atomic_store(&A.flags[b], A.seq0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         stamp(l, 2);
         const int e = s_sel[slot];   // block-uniform
         // A slot with nothing routed (fewer than k logits above -1e30) skips
@@ -1044,40 +1055,56 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
         }
         // -------------------------------------- D: y
         // every block publishes its rows of its slot's y (0 for a slot with
-        // nothing routed) in kYR copies of the layer's parity
-        const uint32_t nibY = ynib(tagY);
-        uint32_t *yd = A.yw + (size_t)((l & 1) * kYR) * ycopy + (size_t)slot * A.yws + r0;
+        // nothing routed): in kYR copies of the layer's parity, or, in a
+        // one-layer launch, as tagged words read only by the slot-0 block of
+        // the same rows
+        const uint32_t nibY = ynib(A.bank, l);
+        const bool one = R.n_layers == 1;
+        const uint32_t ymine = y_word(y, nibY);
         if (t < nr) {
-            const uint32_t yw = y_word(y, nibY);
+            if (!one) {
+                uint32_t *yd = A.yw + (size_t)((l & 1) * kYR) * ycopy + (size_t)slot * A.yws + r0;
 #pragma unroll
-            for (int cp = 0; cp < kYR; ++cp) st_u32_dev(yd + (size_t)cp * ycopy + t, yw);
+                for (int cp = 0; cp < kYR; ++cp) st_u32_dev(yd + (size_t)cp * ycopy + t, ymine);
+            } else if (slot > 0) {
+                st_tag(A.y1 + (size_t)slot * A.yws + r0 + t, tagY, y);
+            }
         }
         stamp(l, 14);
         // the last layer's combine (slot 0 of each row slice): x (L) = x (L - 1)
-        // + moe, from the same y words the other layers' gathers read, written
-        // to R.x once every block has read x (0) from there
+        // + moe (its own slot's y from registers), written to R.x once every
+        // block has read x (0) from there: in a launch of several layers every
+        // block's y of the layer before shows it; in a one-layer launch the
+        // flags every block raised after reading x (0). The y words of a
+        // launch of several layers are rounded as its gathers see them.
         if (l + 1 == R.n_layers && slot == 0) {
             bool late = false;
             const int tq = opaque(t);
             const int iq = tq / kRBMax, jq = tq - iq * kRBMax;
-            const bool hasy = iq < K && jq < nr;
-            const uint32_t *yp = A.yw + (size_t)((l & 1) * kYR + n % kYR) * ycopy + (size_t)iq * A.yws + r0 + jq;
-            uint32_t yw = hasy ? ld_u32_dev(yp) : nibY;
+            const bool hasy = iq >= 1 && iq < K && jq < nr;
+            const uint32_t *yp = A.yw + (size_t)((l & 1) * kYR) * ycopy + (size_t)iq * A.yws + r0 + jq;
+            uint64_t *yq = A.y1 + (size_t)iq * A.yws + r0 + jq;
+            auto ready = [&](uint64_t w) { return one ? tag_is(w, tagY) : ((uint32_t)w & 15u) == nibY; };
+            auto load = [&]() { return one ? ld_tag(yq) : (uint64_t)ld_u32_dev(yp); };
+            uint64_t yw = hasy ? load() : (one ? (uint64_t)tagY << 32 : (uint64_t)nibY);
             bool up = true;
-            for (int i = tq; i < NB; i += kThreads)
-                up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.seq0;
-            for (unsigned spins = 0; (yw & 15u) != nibY || !up; ++spins) {
+            if (one)
+                for (int i = tq; i < NB; i += kThreads)
+                    up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.seq0;
+            for (unsigned spins = 0; !ready(yw) || !up; ++spins) {
                 if (spins > kSpinLimit) {
                     late = true;
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
-                if ((yw & 15u) != nibY) yw = ld_u32_dev(yp);
+                if (!ready(yw)) yw = load();
                 up = true;
-                for (int i = tq; i < NB; i += kThreads)
-                    up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.seq0;
+                if (one)
+                    for (int i = tq; i < NB; i += kThreads)
+                        up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.seq0;
             }
-            if (hasy) s_y[iq * kRBMax + jq] = y_val(yw);
+            if (hasy) s_y[iq * kRBMax + jq] = one ? __uint_as_float((uint32_t)yw) : y_val((uint32_t)yw);
+            if (t < nr) s_y[t] = one ? y : y_val(ymine);
             if (__syncthreads_or(late)) {
                 if (t == 0) raise_err(R.err);
                 return;
@@ -1401,6 +1428,7 @@ struct StepPlan {
     unsigned *err_dev = nullptr;   // its device address
     float *h = nullptr;            // device [K][F] (k_decode_step)
     unsigned seq = 0;              // next sequence number
+    unsigned launches = 0;         // k_decode_grp launches of several layers so far (the y tags' bank)
     int nb = 0;                    // CUs: k_decode_step's grid
     int flat = 0;                  // 1 = k_decode_step can run the stack
     int grp = 0;                   // 1 = k_decode_grp can run the stack
@@ -1441,10 +1469,11 @@ static void plan_release(void *key) {
 // Exchange-word layout in StepPlan::tagged (offsets in 64-bit words): the
 // logits' kLR copies; x (k_decode_step); h's kHR x K planes (k_decode_grp);
 // y's 2 parities x kYR copies x K rows of 32-bit words (k_decode_grp; yws
-// in 32-bit words).
+// in 32-bit words); y's K rows of tagged words for one-layer launches of
+// k_decode_grp.
 struct TagLayout {
     int lws, xws, hws, yws;
-    size_t lw, xw, hw, yw, total;
+    size_t lw, xw, hw, yw, y1, total;
 };
 static TagLayout tag_layout(const DevLayer &L0) {
     TagLayout t;
@@ -1456,7 +1485,8 @@ static TagLayout tag_layout(const DevLayer &L0) {
     t.xw = t.lw + (size_t)kLR * t.lws;
     t.hw = t.xw + (size_t)t.xws;
     t.yw = t.hw + (size_t)kHR * L0.top_k * t.hws;
-    t.total = t.yw + ((size_t)2 * kYR * L0.top_k * t.yws + 1) / 2;
+    t.y1 = t.yw + ((size_t)2 * kYR * L0.top_k * t.yws + 1) / 2;
+    t.total = t.y1 + (size_t)L0.top_k * t.yws;
     return t;
 }
 
@@ -1741,6 +1771,9 @@ int step_run(StepPlan *p, const DevLayer *layers, int first, int n_layers, float
         A.yws = tl.yws;
         A.flags = p->flags;
         A.seq0 = seq0;
+        A.y1 = p->tagged + tl.y1;
+        A.bank = p->launches & 1u;
+        if (n_layers > 1) ++p->launches;
         rc = q8 ? launch_grp<MH_DT_Q8R>(A, nb, s) : launch_grp<MH_DT_F32>(A, nb, s);
     } else {
         StepArgs A;
