@@ -216,6 +216,37 @@ def test_lm_head_batch32_sampled_rows(mh):
         assert abs(lhs - rhs) <= 1e-5 * float(np.abs(colsum) @ np.abs(X[b])), b
 
 
+@pytest.mark.parametrize("batch", [8, 17, 40])
+def test_long_q8r_batched_shapes(mh, batch):
+    # the long-matrix path (131072+ rows: the block-shared digits kernel) at
+    # one and two 16-column tiles and two column groups, with a last 16-row
+    # tile holding 3 rows and a last 256-column super-step of one chunk:
+    # sampled rows (the first, the last tile's, random ones) against the
+    # oracle, and per column the linearity identity over all rows
+    rows, cols = 131075, 2880
+    say(f"long q8r {rows}x{cols} batch {batch}")
+    data = RNG.integers(-127, 128, size=rows * cols, dtype=np.int8)
+    sc = RNG.uniform(1e-3, 1e-2, rows).astype(np.float32)
+    X = RNG.standard_normal((batch, cols)).astype(np.float32)
+    X *= (10.0 ** RNG.uniform(-3, 3, batch)).astype(np.float32)[:, None]
+    wd, sd = DevBuf.from_array(data), DevBuf.from_array(sc)
+    xd, yd = DevBuf.from_array(X), DevBuf(batch * rows * 4)
+    matvec_dev(WT(DT_Q8R, rows, cols, wd.ptr, sd.ptr), xd, yd, batch)
+    Y = yd.download(np.float32, (batch, rows))
+    for d in (wd, sd, xd, yd):
+        d.free()
+    W = data.reshape(rows, cols)
+    idx = np.unique(np.concatenate([[0, 1, 15, 16], np.arange(rows - 19, rows),
+                                    RNG.choice(rows, 200, replace=False)]))
+    sub, ssub = np.ascontiguousarray(W[idx]), np.ascontiguousarray(sc[idx])
+    colsum = W.sum(axis=0, dtype=np.int64).astype(np.float64)
+    for b in range(batch):
+        assert rel_l2(Y[b][idx], po.matvec(DT_Q8R, sub, ssub, X[b], len(idx), cols)) < 1e-5, b
+        lhs = float(np.sum(Y[b].astype(np.float64) / sc.astype(np.float64)))
+        rhs = float(colsum @ X[b].astype(np.float64))
+        assert abs(lhs - rhs) <= 1e-5 * float(np.abs(colsum) @ np.abs(X[b])), b
+
+
 @pytest.mark.parametrize("dt,rows,cols", [(DT_F32, 7, 37), (DT_Q8R, 5, 100), (DT_F32, 3, 8192)])
 def test_matvec_fallback_shapes(mh, dt, rows, cols):
     say(f"matvec fallback dt={dt} {rows}x{cols}")
