@@ -2,9 +2,10 @@
 // (engine/midge.c:341-400), on the device: the next component of the
 // decode step beside the MoE layers.
 //
-//   rmsnorm          launch_rmsnorm (k_rmsnorm)
-//   q, k, v          one launch on the GEMV engine (k_gemv3), any weight
-//                    dtype; three launch_gemv calls where the shapes differ
+//   rmsnorm, q, k, v one launch on the GEMV engine (k_gemv3), any weight
+//                    dtype: every block forms xb = rmsnorm(x) * w for its
+//                    own chunks of x; k_rmsnorm and three launch_gemv calls
+//                    where the shapes differ
 //   k_attn_split     per query head and split of the cached positions:
 //                    biases, per-head RMSNorm (the reference's sequential
 //                    sum), RoPE from the given tables, the current k and v
@@ -24,15 +25,19 @@ namespace {
 
 constexpr int kAttnThreads = 256;
 
-// q, k and v in one launch: the three matrices (same dtype and width) as
-// consecutive block ranges of one grid, each block a k_gemv block over rows
-// of one of them (block-uniform choice), into y[m] = W[m] x.
+// The attention RMSNorm and q, k and v in one launch: the three matrices
+// (same dtype and width) as consecutive block ranges of one grid, each block
+// a k_gemv block over rows of one of them (block-uniform choice), into
+// y[m] = W[m] xb with xb = x * inv * w, inv = 1 / sqrt(mean(x^2) + eps)
+// (engine/mkern.h:238-243). Every block sums x^2 over the distinct chunks in
+// the same fixed order, so all reach the same inv.
 struct Gemv3Args {
     const uint8_t *W[3];
     const void *S[3];
     float *Y[3];
     int rows[3], nb[3];
-    const float *x;
+    const float *x, *nw;
+    float eps;
     int cols, ns, rpb;
 };
 
@@ -59,6 +64,31 @@ __global__ void __launch_bounds__(kGemvThreads) k_gemv3(Gemv3Args A) {
     const uint32_t rowbytes = (uint32_t)C * 16u * gemv_chunk<DT>::W;
     float xr[E];
     load_x<DT>(A.x, C, A.ns, xr);
+    {
+        __shared__ float part[kGemvThreads / 64];
+        const int t = threadIdx.x, slot = t / C, c = t - slot * C;
+        float ss = 0.f;
+        if (slot == 0)   // each chunk once
+#pragma unroll
+            for (int j = 0; j < E; ++j) ss = __builtin_fmaf(xr[j], xr[j], ss);
+        ss = mh_wave_sum(ss);
+        if ((t & 63) == 0) part[t >> 6] = ss;
+        __syncthreads();
+        ss = 0.f;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) ss += part[w];
+        const float inv = 1.0f / sqrtf(ss / (float)A.cols + A.eps);
+        if (slot < A.ns) {
+            const float4 *wp = (const float4 *)(A.nw + (size_t)c * E);
+#pragma unroll
+            for (int i = 0; i < E / 4; ++i) {
+                const float4 w4 = wp[i];
+                xr[4 * i + 0] = xr[4 * i + 0] * inv * w4.x;
+                xr[4 * i + 1] = xr[4 * i + 1] * inv * w4.y;
+                xr[4 * i + 2] = xr[4 * i + 2] * inv * w4.z;
+                xr[4 * i + 3] = xr[4 * i + 3] * inv * w4.w;
+            }
+        }
+    }
     const mh_rsrc rd = gemv_rsrc(W + (size_t)r0 * rowbytes, (uint32_t)nf * rowbytes);
     const mh_rsrc rs = gemv_rsrc((const uint16_t *)S + (size_t)r0 * C, (uint32_t)nf * (uint32_t)C * 2u);
     block_gemv<DT>(
@@ -123,17 +153,20 @@ int launch_o_res_t(const DevWT &w, const float *ao, const float *bo, float *x, h
     return hip_check(hipGetLastError(), "o projection launch");
 }
 
-// One launch for q, k, v when their dtype and layout allow the GEMV
-// engine's chunked kernel; *done = false leaves them to three launch_gemv.
+// One launch for the RMSNorm and q, k, v when their dtype and layout allow
+// the GEMV engine's chunked kernel; *done = false leaves them to k_rmsnorm
+// and three launch_gemv.
 template <int DT>
-int launch_qkv_t(const DevWT *w, const float *x, float *const *y, hipStream_t s, bool *done) {
+int launch_qkv_t(const DevWT *w, const float *x, const float *nw, float eps, float *const *y, hipStream_t s,
+                 bool *done) {
     constexpr int E = gemv_chunk<DT>::E;
     const int64_t cols = w[0].cols;
     *done = false;
     for (int m = 0; m < 3; ++m)
         if (w[m].dt != DT || w[m].cols != cols || ((uintptr_t)w[m].data % 16) != 0 || w[m].rows > INT32_MAX)
             return MH_OK;
-    if (cols % E != 0 || cols / E > kGemvThreads || ((uintptr_t)x % 16) != 0) return MH_OK;
+    if (cols % E != 0 || cols / E > kGemvThreads || ((uintptr_t)x % 16) != 0 || ((uintptr_t)nw % 16) != 0)
+        return MH_OK;
     const int C = (int)(cols / E);
     int ns, nt;
     gemv_shape(C, &ns, &nt);
@@ -153,6 +186,8 @@ int launch_qkv_t(const DevWT *w, const float *x, float *const *y, hipStream_t s,
         nblk += A.nb[m];
     }
     A.x = x;
+    A.nw = nw;
+    A.eps = eps;
     A.cols = (int)cols;
     A.ns = ns;
     A.rpb = (int)rpb;
@@ -597,18 +632,19 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
     float *xb = (float *)(b8 + ox), *q = (float *)(b8 + oq), *k = (float *)(b8 + ok), *v = (float *)(b8 + ov);
     float *part = (float *)(b8 + op), *ao = (float *)(b8 + oo);
     hipStream_t s = stream();
-    MH_TRY(launch_rmsnorm(x, (const float *)an, xb, H, L->norm_eps, 1, s));
     {
         const DevWT w3[3] = {wq, wk, wv};
         float *const y3[3] = {q, k, v};
+        const float *nw = (const float *)an;
         bool done = false;
         switch (wq.dt) {
-        case MH_DT_F32: MH_TRY(launch_qkv_t<MH_DT_F32>(w3, xb, y3, s, &done)); break;
-        case MH_DT_Q8R: MH_TRY(launch_qkv_t<MH_DT_Q8R>(w3, xb, y3, s, &done)); break;
-        case MH_DT_Q4G32: MH_TRY(launch_qkv_t<MH_DT_Q4G32>(w3, xb, y3, s, &done)); break;
-        case MH_DT_MXFP4: MH_TRY(launch_qkv_t<MH_DT_MXFP4>(w3, xb, y3, s, &done)); break;
+        case MH_DT_F32: MH_TRY(launch_qkv_t<MH_DT_F32>(w3, x, nw, L->norm_eps, y3, s, &done)); break;
+        case MH_DT_Q8R: MH_TRY(launch_qkv_t<MH_DT_Q8R>(w3, x, nw, L->norm_eps, y3, s, &done)); break;
+        case MH_DT_Q4G32: MH_TRY(launch_qkv_t<MH_DT_Q4G32>(w3, x, nw, L->norm_eps, y3, s, &done)); break;
+        case MH_DT_MXFP4: MH_TRY(launch_qkv_t<MH_DT_MXFP4>(w3, x, nw, L->norm_eps, y3, s, &done)); break;
         }
         if (!done) {
+            MH_TRY(launch_rmsnorm(x, nw, xb, H, L->norm_eps, 1, s));
             MH_TRY(launch_gemv(wq, xb, q, 1, s));
             MH_TRY(launch_gemv(wk, xb, k, 1, s));
             MH_TRY(launch_gemv(wv, xb, v, 1, s));
