@@ -19,6 +19,7 @@
 //                    (k_gemv_res: + bias, x += o); GEMV + k_attn_residual
 //                    where the shape needs the general kernel
 #include "mh_gemv.cuh"
+#include "mh_xchg.cuh"
 
 namespace mh {
 namespace {
@@ -538,6 +539,482 @@ __global__ void __launch_bounds__(T) k_attn_split(SplitArgs A) {
     }
 }
 
+// ------------------------------------------------ attention in one launch
+//
+// The whole of attention() for one token in one persistent grid of NB blocks
+// (one per CU at most, all resident: every wait is a bounded poll on a
+// tagged word, and a timeout raises the error flag instead of hanging), for
+// int8 (q8r) projections:
+//   1  every block owning q/k/v rows reads x, forms xb = rmsnorm(x) * w in
+//      LDS (the same fixed-order sum of squares in every block), computes
+//      its RQ rows of [q; k; v] = W xb (* row scale, + bias) and publishes
+//      them as tagged words;
+//   2  block (head h, split s) for h < nh, s < S gathers q of head h and k,
+//      v of its kv head and runs k_attn_split's per-head arithmetic over its
+//      positions (per-head RMSNorm with the reference's sequential sums,
+//      RoPE, k and v rounded to f16 as wk_to_f16 does and written to the
+//      cache slot by one block of the kv head, the f16 dots in position
+//      order, the softmax partials); with S > 1 block (h, 0) combines the
+//      splits' partials; the head's output is published in kAR copies;
+//   3  every block gathers the attention output and computes its RO rows of
+//      o = Wo ao (* scale, + bias) and x[r] = x[r] + o[r] (two roundings, as
+//      wk_addbias then the residual loop).
+// x is read in phase 1 and written in phase 3: a block writes only after it
+// has gathered every head's output, which needs every block's q/k/v rows,
+// each published after that block read x. Every block owns q/k/v rows
+// (NB = ceil(QR / RQ)).
+constexpr int kA1Threads = 512;
+constexpr int kA1HMax = 3072;     // hidden size
+constexpr int kA1QMax = 4096;     // n_heads * head_dim
+constexpr int kA1U = 8;           // row iterations per thread of phases 1 and 3
+constexpr int kA1PPT = 2;         // positions per thread and split: 1024 per split
+constexpr int kA1P = kA1Threads * kA1PPT;
+constexpr int kA1MaxS = 8;        // splits per head
+constexpr int kAR = 8;            // copies of the attention output (each polled by NB / kAR blocks)
+
+struct Attn1Args {
+    const int8_t *w[4];        // q, k, v, o rows
+    const float *ws[4];        // their row scales
+    const float *b[4];         // biases
+    const float *an, *qn, *kn, *co, *si, *sink;
+    uint16_t *kc, *vc;
+    float *x;                  // [H], updated in place
+    uint64_t *qkv;             // [QR] tagged rows of q, k, v (with biases)
+    uint64_t *part;            // [nh][S][hd + 2] tagged split partials: o, m, l
+    uint64_t *ao;              // [kAR][aos] tagged attention output
+    unsigned *err;
+    int H, nh, hd, gq, qd, kvd, QR, nctx, slot, S, sinks, qk_norm, kvec, RQ, RO, aos;
+    float eps, scale;
+    unsigned tag;
+};
+
+// Rows [r0, r0 + nr) of an int8 matrix of C 32-element chunks per row times
+// v (LDS, 32-float groups padded to 33): thread (slot, chunk c) takes rows
+// slot + ns u; per-row sums of the chunk partials in a fixed order into
+// out[0 .. nr). red: LDS of kA1U * kA1Threads floats.
+__device__ __forceinline__ void a1_rows(const int8_t *W, int r0, int nr, int C, const float *v, float *red,
+                                        float *out) {
+    const int t = threadIdx.x, ns = kA1Threads / C;
+    const int slot = t / C, c = t - slot * C;
+    const bool act = slot < ns;
+    float xr[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xr[j] = act ? v[c * 33 + j] : 0.f;
+    mh_u4 q[kA1U][2];
+#pragma unroll
+    for (int u = 0; u < kA1U; ++u) {
+        const int j = slot + ns * u;
+        const int r = r0 + min(j, nr - 1);
+        const int8_t *p = W + (size_t)r * (size_t)C * 32 + (size_t)c * 32;
+        if (act && j < nr) {
+            q[u][0] = *(const mh_u4 *)p;
+            q[u][1] = *(const mh_u4 *)(p + 16);
+        } else {
+            q[u][0] = q[u][1] = mh_u4{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kA1U; ++u) {
+        const int j = slot + ns * u;
+        float d = 0.f;
+        const uint32_t ww[8] = {q[u][0].x, q[u][0].y, q[u][0].z, q[u][0].w, q[u][1].x, q[u][1].y, q[u][1].z, q[u][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int bt = 0; bt < 4; ++bt)
+                d = __builtin_fmaf((float)(int8_t)(ww[e] >> (8 * bt)), xr[4 * e + bt], d);
+        if (act && j < nr) red[j * C + c] = d;
+    }
+    __syncthreads();
+    // row sums: 8 lanes per row, then 3 xor-shuffles (fixed order)
+    const int wave = t >> 6, lane = t & 63, rl = lane >> 3, part = lane & 7;
+    for (int rr = wave * 8; rr < nr; rr += (kA1Threads / 64) * 8) {
+        const int r = rr + rl;
+        float s = 0.f;
+        if (r < nr)
+            for (int cc = part; cc < C; cc += 8) s += red[r * C + cc];
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if (part == 0 && r < nr) out[r] = s;
+    }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(kA1Threads) k_attn1(Attn1Args A) {
+#pragma clang fp contract(off)
+    __shared__ float s_x[kA1HMax];
+    __shared__ float s_v[kA1QMax / 32 * 33];     // xb (phase 1), then the attention output (phase 3)
+    __shared__ float red[kA1U * kA1Threads];
+    __shared__ float s_out[kA1U * 64];
+    __shared__ float s_part[16];
+    __shared__ float uq[256], uk[256];
+    __shared__ __attribute__((aligned(16))) uint16_t kcur[256], vcur[256];
+    __shared__ float s_inv[2];
+    __shared__ float sc[kA1P];
+    __shared__ float ob[kA1Threads / 8 * 64 > kA1Threads / 64 * 256 ? kA1Threads / 8 * 64 : kA1Threads / 64 * 256];
+    __shared__ float s_m[kA1MaxS], s_l[kA1MaxS];
+    __shared__ int s_late;
+    const int b = blockIdx.x, t = threadIdx.x, NB = gridDim.x;
+    const int H = A.H, hd = A.hd, C1 = H / 32, C3 = A.qd / 32;
+    const unsigned tag = A.tag;
+    if (t == 0) s_late = 0;
+    // ------------------------------------------------------------ 1: q, k, v
+    const int q0 = A.RQ * b, nq = max(0, min(A.QR - q0, A.RQ));
+    {
+        float ss = 0.f;
+        for (int i = t; i < H; i += kA1Threads) {
+            const float xv = A.x[i];
+            s_x[i] = xv;
+            ss = __builtin_fmaf(xv, xv, ss);
+        }
+        ss = mh_wave_sum(ss);
+        if ((t & 63) == 0) s_part[t >> 6] = ss;
+        __syncthreads();
+        ss = 0.f;
+        for (int w = 0; w < kA1Threads / 64; ++w) ss += s_part[w];
+        const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+        for (int i = t; i < H; i += kA1Threads) s_v[(i >> 5) * 33 + (i & 31)] = s_x[i] * inv * A.an[i];
+        __syncthreads();
+        // the block's rows lie in q, k and v: one pass per matrix it touches
+        for (int m = 0; m < 3; ++m) {
+            const int mb = m == 0 ? 0 : m == 1 ? A.qd : A.qd + A.kvd;
+            const int me = m == 0 ? A.qd : m == 1 ? A.qd + A.kvd : A.QR;
+            const int lo = max(q0, mb), hi = min(q0 + nq, me);
+            if (lo >= hi) continue;
+            a1_rows(A.w[m], lo - mb, hi - lo, C1, s_v, red, s_out);
+            for (int j = t; j < hi - lo; j += kA1Threads) {
+                const float y = s_out[j] * A.ws[m][lo - mb + j];
+                st_tag(A.qkv + lo + j, tag, y + A.b[m][lo - mb + j]);
+            }
+        }
+    }
+    // ------------------------------------------------------------ 2: heads
+    if (b < A.nh * A.S) {
+        constexpr int T = kA1Threads, PPT = kA1PPT, P = kA1P;
+        const int h = b / A.S, s = b - h * A.S;
+        const int kh = h / A.gq, half = hd / 2, i = t, lane = t & 63, wv = t >> 6;
+        float xq = 0.f, xk = 0.f, xv = 0.f, cs = 0.f, sn = 0.f, wq = 0.f, wk = 0.f;
+        if (i < hd) {
+            const uint64_t *pq = A.qkv + (size_t)h * hd + i, *pk = A.qkv + A.qd + (size_t)kh * hd + i;
+            const uint64_t *pv = A.qkv + A.qd + A.kvd + (size_t)kh * hd + i;
+            uint64_t a = ld_tag(pq), c = ld_tag(pk), d = ld_tag(pv);
+            for (unsigned spins = 0; !(tag_is(a, tag) && tag_is(c, tag) && tag_is(d, tag)); ++spins) {
+                if (spins > kSpinLimit) {
+                    s_late = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                if (!tag_is(a, tag)) a = ld_tag(pq);
+                if (!tag_is(c, tag)) c = ld_tag(pk);
+                if (!tag_is(d, tag)) d = ld_tag(pv);
+            }
+            xq = tag_val(a);
+            xk = tag_val(c);
+            xv = tag_val(d);
+            if (A.qk_norm) {
+                wq = A.qn[i];
+                wk = A.kn[i];
+            }
+            uq[i] = xq;
+            uk[i] = xk;
+        }
+        if (i < half) {
+            cs = A.co[i];
+            sn = A.si[i];
+        }
+        __syncthreads();
+        if (s_late) {
+            if (t == 0) raise_err(A.err);
+            return;
+        }
+        if (A.qk_norm) {
+            if (i == 0 || i == 64) {   // the reference's sequential sums of squares
+                const float *u = i == 0 ? uq : uk;
+                float ssq = 0.f;
+                for (int j = 0; j < hd; ++j) ssq += u[j] * u[j];
+                s_inv[i == 0 ? 0 : 1] = 1.0f / sqrtf(ssq / (float)hd + A.eps);
+            }
+            __syncthreads();
+            const float vq = i < hd ? uq[i] * s_inv[0] * wq : 0.f;
+            const float vk = i < hd ? uk[i] * s_inv[1] * wk : 0.f;
+            __syncthreads();
+            if (i < hd) {
+                uq[i] = vq;
+                uk[i] = vk;
+            }
+            __syncthreads();
+        }
+        float r0 = 0.f, r1 = 0.f, k0 = 0.f, k1 = 0.f;
+        if (i < half) {
+            const float a = uq[i], c = uq[i + half], bb = uk[i], d = uk[i + half];
+            r0 = a * cs - c * sn;
+            r1 = c * cs + a * sn;
+            k0 = bb * cs - d * sn;
+            k1 = d * cs + bb * sn;
+        }
+        __syncthreads();
+        if (i < half) {
+            uq[i] = r0;
+            uq[i + half] = r1;
+            uk[i] = k0;
+            uk[i + half] = k1;
+        }
+        __syncthreads();
+        if (i < hd) {
+            kcur[i] = to_f16_ref(uk[i]);
+            vcur[i] = to_f16_ref(xv);
+            if (h % A.gq == 0 && s == 0) {
+                const size_t o = (size_t)A.slot * A.kvd + (size_t)kh * hd + i;
+                A.kc[o] = kcur[i];
+                A.vc[o] = vcur[i];
+            }
+        }
+        __syncthreads();
+        // scores: positions t0 + i + T r, the reference's f16 dot order
+        const int t0 = P * s;
+        float dd[PPT];
+        if (A.kvec) {   // head_dim 64: one 16-byte load per 8 cached values
+            uint4 kw[PPT][8];
+#pragma unroll
+            for (int r = 0; r < PPT; ++r) {
+                const int tt = t0 + i + T * r;
+                const bool cur = tt == A.slot || tt >= A.nctx;
+                const uint16_t *kt = cur ? kcur : A.kc + (size_t)tt * A.kvd + (size_t)kh * hd;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) kw[r][c] = *(const uint4 *)(kt + 8 * c);
+            }
+#pragma unroll
+            for (int r = 0; r < PPT; ++r) {
+                float d = 0.f;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const uint32_t ww[4] = {kw[r][c].x, kw[r][c].y, kw[r][c].z, kw[r][c].w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        d += uq[8 * c + 2 * j] * mh_f16((uint16_t)(ww[j] & 0xffffu));
+                        d += uq[8 * c + 2 * j + 1] * mh_f16((uint16_t)(ww[j] >> 16));
+                    }
+                }
+                dd[r] = d;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < PPT; ++r) {
+                const int tt = t0 + i + T * r;
+                float d = 0.f;
+                if (tt < A.nctx) {
+                    const uint16_t *kt = tt == A.slot ? kcur : A.kc + (size_t)tt * A.kvd + (size_t)kh * hd;
+                    for (int j = 0; j < hd; ++j) d += uq[j] * f16_at(kt + j);
+                }
+                dd[r] = d;
+            }
+        }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            dd[r] = t0 + i + T * r < A.nctx ? dd[r] * A.scale : -INFINITY;
+            mloc = fmaxf(mloc, dd[r]);
+        }
+        const float m = block_max_f(mloc, s_part);
+        float el = 0.f;
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            const float e = t0 + i + T * r < A.nctx ? expf(dd[r] - m) : 0.f;
+            sc[i + T * r] = e;
+            el += e;
+        }
+        const float l = block_sum_f(el, s_part);   // (its barriers also order the sc writes)
+        const int np = min(P, A.nctx - t0);
+        if (A.kvec) {
+            constexpr int NG = T / 8, NPT = P / NG;
+            const int pg = i >> 3, dc = i & 7;
+            float o8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            uint4 w8[NPT];
+#pragma unroll
+            for (int u = 0; u < NPT; ++u) {
+                const int j = pg + NG * u, tt = t0 + j;
+                w8[u] = (j < np && tt != A.slot) ? *(const uint4 *)(A.vc + (size_t)tt * A.kvd + (size_t)kh * hd + 8 * dc)
+                                                 : *(const uint4 *)(vcur + 8 * dc);
+            }
+#pragma unroll
+            for (int u = 0; u < NPT; ++u) {
+                const int j = pg + NG * u;
+                if (j < np) {
+                    const float e = sc[j];
+                    const uint32_t ww[4] = {w8[u].x, w8[u].y, w8[u].z, w8[u].w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        o8[2 * q] += e * mh_f16((uint16_t)(ww[q] & 0xffffu));
+                        o8[2 * q + 1] += e * mh_f16((uint16_t)(ww[q] >> 16));
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) ob[pg * 64 + 8 * dc + q] = o8[q];
+            __syncthreads();
+            float o = 0.f;
+            if (i < 64)
+                for (int g2 = 0; g2 < NG; ++g2) o += ob[g2 * 64 + i];
+            __syncthreads();
+            for (int q = i; q < T / 64 * 256; q += T) ob[q] = 0.f;
+            __syncthreads();
+            if (i < 64) ob[i] = o;
+        } else {
+            constexpr int NW = T / 64, U = 8;
+            for (int i0 = 0; i0 < hd; i0 += 64) {
+                const int dm = i0 + lane;
+                float o = 0.f;
+                if (dm < hd) {
+                    const uint16_t *vb = A.vc + (size_t)kh * hd + dm;
+                    const float vslot = mh_f16(vcur[dm]);
+                    int j = wv;
+                    for (; j + NW * (U - 1) < np; j += NW * U) {
+                        float vvv[U];
+#pragma unroll
+                        for (int u = 0; u < U; ++u) {
+                            const int tt = t0 + j + NW * u;
+                            vvv[u] = tt == A.slot ? vslot : mh_f16(vb[(size_t)tt * A.kvd]);
+                        }
+#pragma unroll
+                        for (int u = 0; u < U; ++u) o += sc[j + NW * u] * vvv[u];
+                    }
+                    for (; j < np; j += NW) {
+                        const int tt = t0 + j;
+                        o += sc[j] * (tt == A.slot ? vslot : mh_f16(vb[(size_t)tt * A.kvd]));
+                    }
+                }
+                if (dm < 256) ob[wv * 256 + dm] = dm < hd ? o : 0.f;
+            }
+        }
+        __syncthreads();
+        const float sinkv = A.sinks ? A.sink[h] : -1e30f;
+        if (A.S == 1) {
+            float M = m;
+            if (sinkv > M) M = sinkv;
+            const float f = expf(m - M);
+            float den = l * f;
+            if (A.sinks) den += expf(sinkv - M);
+            const float inv = 1.0f / den;
+            for (int dm = i; dm < hd; dm += T) {
+                float o = 0.f;
+#pragma unroll
+                for (int w = 0; w < T / 64; ++w) o += ob[w * 256 + dm];
+                const float ov = o * f * inv;
+#pragma unroll
+                for (int cp = 0; cp < kAR; ++cp) st_tag(A.ao + (size_t)cp * A.aos + (size_t)h * hd + dm, tag, ov);
+            }
+        } else {
+            uint64_t *pp = A.part + ((size_t)h * A.S + s) * (hd + 2);
+            for (int dm = i; dm < hd; dm += T) {
+                float o = 0.f;
+#pragma unroll
+                for (int w = 0; w < T / 64; ++w) o += ob[w * 256 + dm];
+                st_tag(pp + dm, tag, o);
+            }
+            if (i == 0) {
+                st_tag(pp + hd, tag, m);
+                st_tag(pp + hd + 1, tag, l);
+            }
+            if (s == 0) {
+                // split 0 combines: every split's m and l, then its o values
+                if (i < A.S) {
+                    const uint64_t *ps = A.part + ((size_t)h * A.S + i) * (hd + 2);
+                    uint64_t wm = ld_tag(ps + hd), wl = ld_tag(ps + hd + 1);
+                    for (unsigned spins = 0; !(tag_is(wm, tag) && tag_is(wl, tag)); ++spins) {
+                        if (spins > kSpinLimit) {
+                            s_late = 1;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                        if (!tag_is(wm, tag)) wm = ld_tag(ps + hd);
+                        if (!tag_is(wl, tag)) wl = ld_tag(ps + hd + 1);
+                    }
+                    s_m[i] = tag_val(wm);
+                    s_l[i] = tag_val(wl);
+                }
+                __syncthreads();
+                if (s_late) {
+                    if (t == 0) raise_err(A.err);
+                    return;
+                }
+                float M = sinkv;
+                for (int q = 0; q < A.S; ++q) M = fmaxf(M, s_m[q]);
+                float den = 0.f;
+                for (int q = 0; q < A.S; ++q) den += s_l[q] * expf(s_m[q] - M);
+                if (A.sinks) den += expf(sinkv - M);
+                const float inv = 1.0f / den;
+                for (int dm = i; dm < hd; dm += T) {
+                    float o = 0.f;
+                    for (int q = 0; q < A.S; ++q) {
+                        const uint64_t *po = A.part + ((size_t)h * A.S + q) * (hd + 2) + dm;
+                        uint64_t wo = ld_tag(po);
+                        for (unsigned spins = 0; !tag_is(wo, tag); ++spins) {
+                            if (spins > kSpinLimit) {
+                                s_late = 1;
+                                break;
+                            }
+                            __builtin_amdgcn_s_sleep(1);
+                            wo = ld_tag(po);
+                        }
+                        o += tag_val(wo) * expf(s_m[q] - M);
+                    }
+                    const float ov = o * inv;
+#pragma unroll
+                    for (int cp = 0; cp < kAR; ++cp) st_tag(A.ao + (size_t)cp * A.aos + (size_t)h * hd + dm, tag, ov);
+                }
+            }
+        }
+    }
+    // ------------------------------------------------------------ 3: o + residual
+    const int o0 = A.RO * b, no = max(0, min(H - o0, A.RO));
+    if (no > 0) {
+        // every word of the thread's share loaded at once, then only the
+        // late ones polled again
+        constexpr int NA = kA1QMax / kA1Threads;
+        const uint64_t *src = A.ao + (size_t)(b % kAR) * A.aos;
+        const int tt = opaque(t);
+        uint64_t w[NA];
+#pragma unroll
+        for (int k = 0; k < NA; ++k) {
+            const int i = tt + k * kA1Threads;
+            w[k] = i < A.qd ? ld_tag(src + i) : (uint64_t)tag << 32;
+        }
+        bool late = false;
+        for (unsigned spins = 0;; ++spins) {
+            bool ready = true;
+#pragma unroll
+            for (int k = 0; k < NA; ++k) ready = ready && tag_is(w[k], tag);
+            if (ready) break;
+            if (spins > kSpinLimit) {
+                late = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int k = 0; k < NA; ++k) {
+                const int i = tt + k * kA1Threads;
+                if (i < A.qd && !tag_is(w[k], tag)) w[k] = ld_tag(src + i);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NA; ++k) {
+            const int i = t + k * kA1Threads;
+            if (i < A.qd) s_v[(i >> 5) * 33 + (i & 31)] = tag_val(w[k]);
+        }
+        if (__syncthreads_or(late)) {
+            if (t == 0) raise_err(A.err);
+            return;
+        }
+        a1_rows(A.w[3], o0, no, C3, s_v, red, s_out);
+        for (int j = t; j < no; j += kA1Threads) {
+            const float y = s_out[j] * A.ws[3][o0 + j] + A.b[3][o0 + j];
+            A.x[o0 + j] = s_x[o0 + j] + y;
+        }
+    }
+    (void)NB;
+}
+
 __global__ void k_attn_clear(unsigned *p, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
 }
@@ -632,6 +1109,107 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
     float *xb = (float *)(b8 + ox), *q = (float *)(b8 + oq), *k = (float *)(b8 + ok), *v = (float *)(b8 + ov);
     float *part = (float *)(b8 + op), *ao = (float *)(b8 + oo);
     hipStream_t s = stream();
+    {
+        // the one-launch kernel when its limits hold (int8 projections, the
+        // LDS capacities, every head's splits in the grid, one block per CU
+        // resident); MIDGE_HIP_ATTN_SPLIT=1 (read per call) keeps the
+        // separate launches, so callers can compare the two
+        const char *sp = getenv("MIDGE_HIP_ATTN_SPLIT");
+        const int cus = device_cus(), QR = qd + 2 * kvd;
+        const int RQ = (QR + cus - 1) / cus, NB = (QR + RQ - 1) / RQ;
+        const int C1 = (int)(H / 32), C3 = qd / 32;
+        const int ns1 = C1 >= 1 ? kA1Threads / C1 : 0, ns3 = C3 >= 1 ? kA1Threads / C3 : 0;
+        const int RO = (int)((H + NB - 1) / NB), S1 = (nctx + kA1P - 1) / kA1P;
+        bool ok1 = !(sp && sp[0] == '1');
+        for (const DevWT *w : {&wq, &wk, &wv, &wo})
+            ok1 = ok1 && w->dt == MH_DT_Q8R && w->scales && (uintptr_t)w->data % 16 == 0;
+        ok1 = ok1 && H % 32 == 0 && H <= kA1HMax && qd % 32 == 0 && qd <= kA1QMax && ns1 >= 1 && ns3 >= 1 &&
+              RQ <= std::min(512, ns1 * kA1U) && RO <= std::min(512, ns3 * kA1U) && hd <= 256 && S1 <= kA1MaxS &&
+              nh * S1 <= NB;
+        static int occ_dev = -1, occ = 0;
+        if (ok1) {
+            int dev = 0;
+            MH_HIP(hipGetDevice(&dev));
+            if (dev != occ_dev) {
+                MH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)k_attn1, kA1Threads, 0));
+                occ_dev = dev;
+            }
+            ok1 = occ >= 1;
+        }
+        if (ok1) {
+            static unsigned *err = nullptr, *err_dev = nullptr;
+            if (!err) {
+                MH_HIP(hipHostMalloc((void **)&err, sizeof(unsigned), hipHostMallocMapped));
+                *err = 0;
+                MH_HIP(hipHostGetDevicePointer((void **)&err_dev, err, 0));
+                watch_async_error(err, "attention: an exchange timed out (blocks not co-resident)");
+            }
+            // exchange words: q/k/v rows, the splits' partials, kAR copies of
+            // the attention output (zeroed when the slot is (re)allocated: a
+            // launch's tag is never 0 and never repeats)
+            const size_t aos = ((size_t)qd + 15) / 16 * 16 + 32;
+            const size_t wqkv = ((size_t)QR + 31) / 32 * 32, wpart = ((size_t)nh * kA1MaxS * (hd + 2) + 31) / 32 * 32;
+            const size_t words = wqkv + wpart + kAR * aos;
+            const size_t words_max = words;
+            void *p1;
+            MH_TRY(scratch(S_ATTN1, words_max * 8, &p1));
+            static void *zeroed = nullptr;
+            static size_t zeroed_words = 0;
+            if (p1 != zeroed || words > zeroed_words) {
+                MH_LAUNCH("attn_clear", k_attn_clear, dim3(64), dim3(256), 0, s, (unsigned *)p1, (int)(2 * words_max));
+                zeroed = p1;
+                zeroed_words = words_max;
+            }
+            static unsigned tag = 0;
+            Attn1Args A;
+            A.w[0] = (const int8_t *)wq.data;
+            A.w[1] = (const int8_t *)wk.data;
+            A.w[2] = (const int8_t *)wv.data;
+            A.w[3] = (const int8_t *)wo.data;
+            A.ws[0] = (const float *)wq.scales;
+            A.ws[1] = (const float *)wk.scales;
+            A.ws[2] = (const float *)wv.scales;
+            A.ws[3] = (const float *)wo.scales;
+            A.b[0] = (const float *)bq;
+            A.b[1] = (const float *)bk;
+            A.b[2] = (const float *)bv;
+            A.b[3] = (const float *)bo;
+            A.an = (const float *)an;
+            A.qn = (const float *)qn;
+            A.kn = (const float *)kn;
+            A.co = (const float *)co + (size_t)pos * (hd / 2);
+            A.si = (const float *)si + (size_t)pos * (hd / 2);
+            A.sink = (const float *)sk;
+            A.kc = L->kc;
+            A.vc = L->vc;
+            A.x = x;
+            A.qkv = (uint64_t *)p1;
+            A.part = A.qkv + wqkv;
+            A.ao = A.part + wpart;
+            A.err = err_dev;
+            A.H = (int)H;
+            A.nh = nh;
+            A.hd = hd;
+            A.gq = nh / nkv;
+            A.qd = qd;
+            A.kvd = kvd;
+            A.QR = QR;
+            A.nctx = nctx;
+            A.slot = pos % cap;
+            A.S = S1;
+            A.sinks = L->sinks ? 1 : 0;
+            A.qk_norm = L->qk_norm ? 1 : 0;
+            A.kvec = hd == 64 && (uintptr_t)L->kc % 16 == 0 && (uintptr_t)L->vc % 16 == 0;
+            A.RQ = RQ;
+            A.RO = RO;
+            A.aos = (int)aos;
+            A.eps = L->norm_eps;
+            A.scale = L->attn_scale;
+            A.tag = ++tag;
+            MH_LAUNCH("attn1", k_attn1, dim3((unsigned)NB), dim3(kA1Threads), 0, s, A);
+            return hip_check(hipGetLastError(), "attention launch");
+        }
+    }
     {
         const DevWT w3[3] = {wq, wk, wv};
         float *const y3[3] = {q, k, v};

@@ -50,6 +50,7 @@
 #include <vector>
 
 #include "mh_gemv.cuh"
+#include "mh_xchg.cuh"
 
 namespace mh {
 
@@ -119,7 +120,6 @@ constexpr int kUD = 9;          // down rows in flight per thread (k_decode_grp)
 constexpr int kPD = 4;          // gate/up pairs in flight per thread (k_decode_grp)
 static_assert(kPD <= kUP, "k_decode_grp's gate/up pipeline depth");
 constexpr int kNX = 8;          // x elements per thread in the router phase (H <= kNX * kThreads)
-constexpr unsigned kSpinLimit = 1u << 20;
 constexpr int kStamps = 24;     // phase timestamps per layer and block while profiling
 constexpr int kEL = 2;          // logits per lane in the routing wave (E <= 64 * kEL)
 constexpr int kLR = 8;          // copies of the logits (each polled by NB / kLR blocks)
@@ -179,17 +179,6 @@ __device__ __forceinline__ mh_u4 ld_dev16(rsrc_t r, uint32_t off) {
 }
 __device__ __forceinline__ void st_dev(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void raise_err(unsigned *err) {
-    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-// An opaque copy of v: values derived from it are recomputed where they are
-// used instead of being hoisted out of the layer loop and held in registers
-// (or spilled) across every phase.
-__device__ __forceinline__ int opaque(int v) {
-    asm volatile("" : "+v"(v));
-    return v;
 }
 
 // Per-block phase timestamps (100 MHz wall clock), written by thread 0 of
@@ -269,15 +258,6 @@ __device__ __forceinline__ float block_sum(float v, float *part) {
     return s;
 }
 
-// Tagged words: (tag << 32) | payload in one device-scope 64-bit store.
-__device__ __forceinline__ void st_tag_u(uint64_t *p, unsigned tag, uint32_t v) {
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_tag(uint64_t *p, unsigned tag, float v) { st_tag_u(p, tag, __float_as_uint(v)); }
-__device__ __forceinline__ uint64_t ld_tag(uint64_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool tag_is(uint64_t w, unsigned tag) { return (unsigned)(w >> 32) == tag; }
 
 // y words (k_decode_grp): one 32-bit word per value, an f32 rounded to a
 // multiple of 16 units in the last place (within 2^-20 relative; inf and nan

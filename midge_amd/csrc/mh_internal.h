@@ -55,7 +55,8 @@ void unregister_owner(void *key);
 
 // Library-owned device scratch that grows on demand (slot = purpose id).
 // Contents are not preserved across growth.
-enum Scratch { S_X = 0, S_Y, S_XB, S_H, S_YE, S_RL, S_SEL, S_W, S_PLAN, S_MISC, S_LIST, S_Q, S_XQ, S_ORD, S_SAMPLE, S_ATTN, S_COUNT };
+enum Scratch { S_X = 0, S_Y, S_XB, S_H, S_YE, S_RL, S_SEL, S_W, S_PLAN, S_MISC, S_LIST, S_Q, S_XQ, S_ORD, S_SAMPLE, S_ATTN,
+               S_ATTN1, S_COUNT };
 int scratch(Scratch slot, uint64_t bytes, void **p);
 
 // Bytes per element class for a tensor view.

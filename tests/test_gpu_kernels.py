@@ -449,12 +449,19 @@ LONG_ATTN_SHAPES = {
 }
 
 
+@pytest.mark.parametrize("path", ["one_launch", "split"])
 @pytest.mark.parametrize("name", ["small_sliding_sinks", "small_full_qknorm", "gpt_oss", *LONG_ATTN_SHAPES])
-def test_attention_dev_vs_oracle(mh, name):
+def test_attention_dev_vs_oracle(mh, name, path, monkeypatch):
     # attention() for a run of decode positions (past the sliding window, so
     # the ring wraps): the device x and f16 caches against the oracle's
-    # (bit-exact with the reference's scalar attention on the CPU)
+    # (bit-exact with the reference's scalar attention on the CPU), through
+    # the one-launch kernel (int8 projections) and the separate launches
+    # (MIDGE_HIP_ATTN_SPLIT=1)
     import ctypes
+    if path == "split":
+        monkeypatch.setenv("MIDGE_HIP_ATTN_SPLIT", "1")
+    else:
+        monkeypatch.delenv("MIDGE_HIP_ATTN_SPLIT", raising=False)
     from test_oracle_kernels import ATTN_DIV_FIXTURE, ATTN_SHAPES, GPT_OSS_ATTN, GPT_OSS_ROPE, AttnHost
     from midge_amd import _lib
     cfgs = dict(ATTN_SHAPES, gpt_oss=GPT_OSS_ATTN, **LONG_ATTN_SHAPES)
