@@ -566,7 +566,8 @@ __global__ void __launch_bounds__(T) k_attn_split(SplitArgs A) {
 constexpr int kA1Threads = 512;
 constexpr int kA1HMax = 3072;     // hidden size
 constexpr int kA1QMax = 4096;     // n_heads * head_dim
-constexpr int kA1U = 8;           // row iterations per thread of phases 1 and 3
+constexpr int kA1UQ = 4;          // row iterations per thread of phase 1 (q, k, v)
+constexpr int kA1UO = 4;          // row iterations per thread of phase 3 (o)
 constexpr int kA1PPT = 2;         // positions per thread and split: 1024 per split
 constexpr int kA1P = kA1Threads * kA1PPT;
 constexpr int kA1MaxS = 8;        // splits per head
@@ -588,11 +589,31 @@ struct Attn1Args {
     unsigned tag;
 };
 
-// Rows [r0, r0 + nr) of an int8 matrix of C 32-element chunks per row times
-// v (LDS, 32-float groups padded to 33): thread (slot, chunk c) takes rows
-// slot + ns u; per-row sums of the chunk partials in a fixed order into
-// out[0 .. nr). red: LDS of kA1U * kA1Threads floats.
-__device__ __forceinline__ void a1_rows(const int8_t *W, int r0, int nr, int C, const float *v, float *red,
+// Rows [0, nr) of a block's share of int8 rows of C 32-element chunks (row
+// j at rowp(j)) times v (LDS, 32-float groups padded to 33): thread (slot,
+// chunk c) takes rows slot + ns u, u < U. a1_issue loads them (2 x 16 bytes
+// a row and thread) so that they can be in flight long before a1_math uses
+// them; a1_math forms the chunk partials and the per-row sums in a fixed
+// order into out[0 .. nr). red: LDS of U * kA1Threads floats.
+template <int U, class RowP>
+__device__ __forceinline__ void a1_issue(RowP rowp, int nr, int C, mh_u4 (&q)[U][2]) {
+    const int t = threadIdx.x, ns = kA1Threads / C;
+    const int slot = t / C, c = t - slot * C;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int j = slot + ns * u;
+        if (slot < ns && j < nr) {
+            const int8_t *p = rowp(j) + (size_t)c * 32;
+            q[u][0] = *(const mh_u4 *)p;
+            q[u][1] = *(const mh_u4 *)(p + 16);
+        } else {
+            q[u][0] = q[u][1] = mh_u4{0u, 0u, 0u, 0u};
+        }
+    }
+}
+
+template <int U>
+__device__ __forceinline__ void a1_math(const mh_u4 (&q)[U][2], int nr, int C, const float *v, float *red,
                                         float *out) {
     const int t = threadIdx.x, ns = kA1Threads / C;
     const int slot = t / C, c = t - slot * C;
@@ -600,21 +621,8 @@ __device__ __forceinline__ void a1_rows(const int8_t *W, int r0, int nr, int C, 
     float xr[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j) xr[j] = act ? v[c * 33 + j] : 0.f;
-    mh_u4 q[kA1U][2];
 #pragma unroll
-    for (int u = 0; u < kA1U; ++u) {
-        const int j = slot + ns * u;
-        const int r = r0 + min(j, nr - 1);
-        const int8_t *p = W + (size_t)r * (size_t)C * 32 + (size_t)c * 32;
-        if (act && j < nr) {
-            q[u][0] = *(const mh_u4 *)p;
-            q[u][1] = *(const mh_u4 *)(p + 16);
-        } else {
-            q[u][0] = q[u][1] = mh_u4{0u, 0u, 0u, 0u};
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < kA1U; ++u) {
+    for (int u = 0; u < U; ++u) {
         const int j = slot + ns * u;
         float d = 0.f;
         const uint32_t ww[8] = {q[u][0].x, q[u][0].y, q[u][0].z, q[u][0].w, q[u][1].x, q[u][1].y, q[u][1].z, q[u][1].w};
@@ -645,8 +653,8 @@ __global__ void __launch_bounds__(kA1Threads) k_attn1(Attn1Args A) {
 #pragma clang fp contract(off)
     __shared__ float s_x[kA1HMax];
     __shared__ float s_v[kA1QMax / 32 * 33];     // xb (phase 1), then the attention output (phase 3)
-    __shared__ float red[kA1U * kA1Threads];
-    __shared__ float s_out[kA1U * 64];
+    __shared__ float red[kA1UQ * kA1Threads];
+    __shared__ float s_out[512];
     __shared__ float s_part[16];
     __shared__ float uq[256], uk[256];
     __shared__ __attribute__((aligned(16))) uint16_t kcur[256], vcur[256];
@@ -660,7 +668,20 @@ __global__ void __launch_bounds__(kA1Threads) k_attn1(Attn1Args A) {
     const unsigned tag = A.tag;
     if (t == 0) s_late = 0;
     // ------------------------------------------------------------ 1: q, k, v
+    // the weight rows of phases 1 and 3 are issued first: they depend on
+    // nothing, and land while x is read and normalized and the heads run
     const int q0 = A.RQ * b, nq = max(0, min(A.QR - q0, A.RQ));
+    const int o0 = A.RO * b, no = max(0, min(H - o0, A.RO));
+    auto qkv_row = [&](int j) __attribute__((always_inline)) {
+        const int gr = q0 + j;
+        const int m = gr < A.qd ? 0 : gr < A.qd + A.kvd ? 1 : 2;
+        const int lr = gr - (m == 0 ? 0 : m == 1 ? A.qd : A.qd + A.kvd);
+        return (m == 0 ? A.w[0] : m == 1 ? A.w[1] : A.w[2]) + (size_t)lr * (size_t)H;
+    };
+    mh_u4 wq1[kA1UQ][2], wo3[kA1UO][2];
+    a1_issue<kA1UQ>(qkv_row, nq, C1, wq1);
+    a1_issue<kA1UO>([&](int j) __attribute__((always_inline)) { return A.w[3] + (size_t)(o0 + j) * (size_t)A.qd; },
+                    no, C3, wo3);
     {
         float ss = 0.f;
         for (int i = t; i < H; i += kA1Threads) {
@@ -676,17 +697,13 @@ __global__ void __launch_bounds__(kA1Threads) k_attn1(Attn1Args A) {
         const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
         for (int i = t; i < H; i += kA1Threads) s_v[(i >> 5) * 33 + (i & 31)] = s_x[i] * inv * A.an[i];
         __syncthreads();
-        // the block's rows lie in q, k and v: one pass per matrix it touches
-        for (int m = 0; m < 3; ++m) {
-            const int mb = m == 0 ? 0 : m == 1 ? A.qd : A.qd + A.kvd;
-            const int me = m == 0 ? A.qd : m == 1 ? A.qd + A.kvd : A.QR;
-            const int lo = max(q0, mb), hi = min(q0 + nq, me);
-            if (lo >= hi) continue;
-            a1_rows(A.w[m], lo - mb, hi - lo, C1, s_v, red, s_out);
-            for (int j = t; j < hi - lo; j += kA1Threads) {
-                const float y = s_out[j] * A.ws[m][lo - mb + j];
-                st_tag(A.qkv + lo + j, tag, y + A.b[m][lo - mb + j]);
-            }
+        a1_math<kA1UQ>(wq1, nq, C1, s_v, red, s_out);
+        for (int j = t; j < nq; j += kA1Threads) {
+            const int gr = q0 + j;
+            const int m = gr < A.qd ? 0 : gr < A.qd + A.kvd ? 1 : 2;
+            const int lr = gr - (m == 0 ? 0 : m == 1 ? A.qd : A.qd + A.kvd);
+            const float y = s_out[j] * A.ws[m][lr];
+            st_tag(A.qkv + gr, tag, y + A.b[m][lr]);
         }
     }
     // ------------------------------------------------------------ 2: heads
@@ -967,7 +984,6 @@ __global__ void __launch_bounds__(kA1Threads) k_attn1(Attn1Args A) {
         }
     }
     // ------------------------------------------------------------ 3: o + residual
-    const int o0 = A.RO * b, no = max(0, min(H - o0, A.RO));
     if (no > 0) {
         // every word of the thread's share loaded at once, then only the
         // late ones polled again
@@ -1006,7 +1022,7 @@ __global__ void __launch_bounds__(kA1Threads) k_attn1(Attn1Args A) {
             if (t == 0) raise_err(A.err);
             return;
         }
-        a1_rows(A.w[3], o0, no, C3, s_v, red, s_out);
+        a1_math<kA1UO>(wo3, no, C3, s_v, red, s_out);
         for (int j = t; j < no; j += kA1Threads) {
             const float y = s_out[j] * A.ws[3][o0 + j] + A.b[3][o0 + j];
             A.x[o0 + j] = s_x[o0 + j] + y;
@@ -1124,7 +1140,7 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
         for (const DevWT *w : {&wq, &wk, &wv, &wo})
             ok1 = ok1 && w->dt == MH_DT_Q8R && w->scales && (uintptr_t)w->data % 16 == 0;
         ok1 = ok1 && H % 32 == 0 && H <= kA1HMax && qd % 32 == 0 && qd <= kA1QMax && ns1 >= 1 && ns3 >= 1 &&
-              RQ <= std::min(512, ns1 * kA1U) && RO <= std::min(512, ns3 * kA1U) && hd <= 256 && S1 <= kA1MaxS &&
+              RQ <= std::min(512, ns1 * kA1UQ) && RO <= std::min(512, ns3 * kA1UO) && hd <= 256 && S1 <= kA1MaxS &&
               nh * S1 <= NB;
         static int occ_dev = -1, occ = 0;
         if (ok1) {
