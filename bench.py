@@ -635,8 +635,11 @@ def reference_bench(ev, s, seconds: float = 1.0) -> dict:
 def config_probes(ev, s, seed: int, reps: int = 20) -> dict:
     """Configurations 0-2 of the measurement plan beside the headline (cfg 4)
     and the prefill (cfg 3), each with synthetic device-generated inputs:
-      cfg0  one gpt-oss expert FFN for one token: a one-layer stack of one
-            expert (top-1), through the one-launch step
+      cfg0  one gpt-oss expert FFN for one token: expert_apply with the
+            routing given (mh_stack_apply_dev on a one-expert stack: one
+            launch, no router, as the reference's own configuration times
+            the expert alone); the same expert behind a top-1 router (a
+            routed one-layer step) is reported beside it
       cfg1  one gpt-oss-20b MoE layer (32 experts, top-4), batch 1, a fresh
             hidden state per step so the routed experts differ
       cfg2  the int8 (q8r) trunk GEMVs QKV 5120x2880, O 2880x4096 and
@@ -654,20 +657,41 @@ def config_probes(ev, s, seed: int, reps: int = 20) -> dict:
         xs = DevBuf((reps + 3) * shp.hidden * 4)
         _lib.call("mh_synth_normal_dev", xs.ptr, (reps + 3) * shp.hidden, synth.hash64_int(keys.x, 5),
                   float(synth.normal_c(1.0)))
-        for i in range(3):
-            st.decode(xs.ptr + i * shp.hidden * 4, 1)
-        midge_amd.sync()
-        a, b = ev.event(), ev.event()
-        ev.record(a, s)
-        for i in range(reps):
-            st.decode(xs.ptr + (3 + i) * shp.hidden * 4, 1)
-        ev.record(b, s)
-        ms = ev.elapsed_ms(a, b) / reps
+
+        def timed(call) -> float:
+            for i in range(3):
+                call(i)
+            midge_amd.sync()
+            a, b = ev.event(), ev.event()
+            ev.record(a, s)
+            for i in range(reps):
+                call(3 + i)
+            ev.record(b, s)
+            return ev.elapsed_ms(a, b) / reps
+
+        routed_ms = timed(lambda i: st.decode(xs.ptr + i * shp.hidden * 4, 1))
+        extra = {}
+        if name == "cfg0":
+            # expert_apply: xb from the same seeded N(0, 1) stream, sel = [0],
+            # w = [1], accumulated into one output row
+            xo = DevBuf(shp.hidden * 4)
+            sd, wd = DevBuf.from_array(np.zeros(1, np.int32)), DevBuf.from_array(np.ones(1, np.float32))
+            _lib.call("mh_synth_normal_dev", xo.ptr, shp.hidden, 907, float(synth.normal_c(1.0)))
+            ms = timed(lambda i: st.apply(0, xs.ptr + i * shp.hidden * 4, sd.ptr, wd.ptr, xo.ptr))
+            extra = {"path": "expert_apply, routing given (mh_stack_apply_dev, one launch)",
+                     "routed_one_layer_us": routed_ms * 1e3}
+            for d in (xo, sd, wd):
+                d.free()
+        else:
+            ms = routed_ms
         nbytes = step_bytes(shp, 1, float(shp.top_k))
+        if name == "cfg0":
+            nbytes -= shp.n_experts * shp.hidden + 8 * shp.n_experts + 4 * shp.hidden   # no router, no norm
         out[name] = {"workload": ("one expert FFN (2880x2880 MXFP4 gate/up/down), one token" if name == "cfg0" else
                                   "one gpt-oss-20b MoE layer, 32 MXFP4 experts, top-4, batch 1"),
                      "us_per_token": ms * 1e3, "tok_per_s": 1e3 / ms, "hbm_bytes": nbytes,
-                     "GBps": nbytes / (ms * 1e-3) / 1e9, "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                     "GBps": nbytes / (ms * 1e-3) / 1e9, "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     **extra}
         xs.free()
         st.destroy()
         for d in bufs:

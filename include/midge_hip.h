@@ -234,6 +234,16 @@ int mh_stack_create(const mh_moe_layer *layers, int n_layers, int max_batch, mh_
  * usage (device u32 [n_layers][n_experts], may be NULL) is incremented per
  * routed expert as the reference's usage histogram is (midge.c:517-518). */
 int mh_stack_decode(mh_stack *s, float *x, int batch, int32_t *sel, float *w, uint32_t *usage);
+/* expert_apply (engine/midge.c:436-467) for one token with the routing
+ * given, on layer `layer` of the stack: x += w[i] * expert_{sel[i]}(xb) for
+ * the top_k slots in ascending expert order (slot order among equal ids, as
+ * the expert-major loop adds, midge.c:595-611); a slot whose expert is
+ * outside [0, n_experts) adds nothing. Device xb[hidden] (normed input, not
+ * overlapping x), sel/w[top_k], x[hidden]. mh_expert_major_dev with n = 1,
+ * in one launch where the stack's decode plan holds (the down projection
+ * then sums in another order: within 2e-6 relative of the per-layer
+ * kernels). */
+int mh_stack_apply_dev(mh_stack *s, int layer, const float *xb, const int32_t *sel, const float *w, float *x);
 int mh_stack_destroy(mh_stack *s);
 
 /* ----------------------------------------------------- decode token */

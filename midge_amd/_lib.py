@@ -105,6 +105,7 @@ _SIGS = {
     "mh_expert_major_dev": [C.POINTER(MhMoeLayer), _I, _P, _P, _P, _P],
     "mh_stack_create": [C.POINTER(MhMoeLayer), _I, _I, C.POINTER(_P)],
     "mh_stack_decode": [_P, _P, _I, _P, _P, _P],
+    "mh_stack_apply_dev": [_P, _I, _P, _P, _P, _P],
     "mh_stack_destroy": [_P],
     "mh_model_create": [C.POINTER(MhModelDesc), C.POINTER(_P)],
     "mh_forward_dev": [_P, _I, _I, _P, _P, _P, _P],

@@ -109,6 +109,11 @@ struct GrpArgs {             // k_decode_grp
     unsigned *flags;         // [gridDim.x] per-block flags: x of layer 0 read (one-layer launches)
     unsigned seq0;           // first sequence number of this launch (4 per layer)
     unsigned bank;           // the y tags' bank: the plan's count of launches of several layers, mod 2
+    // routing given (one layer, one token; null otherwise): x += w_i
+    // expert_{sel_i}(xb) over the K slots in ascending expert order
+    const float *gxb;        // [H] the normed input
+    const int32_t *gsel;     // [K]
+    const float *gw;         // [K]
 };
 
 namespace {
@@ -718,7 +723,9 @@ __device__ __forceinline__ void dn_mfma_grp(const uint8_t *sw, const uint16_t *s
 
 // ------------------------------------------------------- k_decode_grp
 
-template <int RDT>
+// GV: the routing is given (A.gxb, A.gsel, A.gw; one layer), a separate
+// instantiation so that the routed kernel's registers are unaffected.
+template <int RDT, bool GV>
 __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
     // LDS is static (capacities are checked at plan creation).
     __shared__ float s_part[16];
@@ -755,7 +762,32 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
         // sequence numbers of this layer: logits, h, y (the fourth is unused)
         const unsigned tagL = A.seq0 + 4u * (unsigned)l, tagH = tagL + 1u, tagY = tagL + 2u;
         stamp(l, 0);
-        {
+        // routing given: this thread's xb elements t + k kThreads (stored to
+        // LDS once the weight loads are issued) and, in a slot-0 block, x of
+        // its row for the combine
+        float gxv[GV ? kNG : 1];
+        float gx0 = 0.f;
+        if constexpr (GV) {
+            // expert_apply with the routing given (no norm, no router); a slot
+            // whose expert is out of range is unfilled. x is read and written
+            // only by the combine, each element by one block, so no block
+            // waits for another's reads. The selection is loaded first: the
+            // barrier then waits for it alone, and xb and x arrive while the
+            // weight loads are issued.
+            const int tk = min(t, K - 1);
+            const int ge = A.gsel[tk];
+            const float gwv = A.gw[tk];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < kNG; ++k) gxv[k] = A.gxb[min(t + k * kThreads, H - 1)];
+            if (slot == 0) gx0 = R.x[r0 + min(t, nr - 1)];
+            __builtin_amdgcn_sched_barrier(0);
+            if (t < K) {
+                s_sel[t] = ge >= 0 && ge < R.E ? ge : -1;
+                s_w[t] = gwv;
+            }
+            __syncthreads();
+        } else {
             // x (l): R.x at layer 0, else x (l - 1) + moe (l - 1) with moe =
             // sum_i w_i y_i in selection order, each product and sum rounded
             // on its own (engine/midge.c:544-548), from the y words every
@@ -826,7 +858,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
         }
         // x (0) read: the last layer's combine overwrites R.x only once every
         // block has raised this flag
-        if (l == 0 && R.n_layers == 1 && t == 0)
+        if (l == 0 && R.n_layers == 1 && t == 0 && !GV)
             __hip_atomic_store(&A.flags[b], A.seq0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         stamp(l, 2);
         const int e = s_sel[slot];   // block-uniform
@@ -851,8 +883,10 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
             const int gsl = gact ? gs : ns - 1;
             const int plast = max(np - 1, 0);
             float xr[32];
+            if constexpr (!GV) {
 #pragma unroll
-            for (int j = 0; j < 32; ++j) xr[j] = gact ? s_xbs[c * 33 + j] : 0.f;
+                for (int j = 0; j < 32; ++j) xr[j] = gact ? s_xbs[c * 33 + j] : 0.f;
+            }
             // the scales first: the block's gate, up and down scale rows are
             // three contiguous ranges, loaded as 16-byte chunks of their
             // aligned windows (mis: the range's offset in its window)
@@ -899,7 +933,18 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                 const int o = q < n0 ? q * 16 : q < n0 + n1 ? kScW + (q - n0) * 16 : 2 * kScW + (q - n0 - n1) * 16;
                 if (q < n0 + n1 + n2) *(mh_u4 *)(s_sc + o) = qs[k];
             }
+            if constexpr (GV) {
+#pragma unroll
+                for (int k = 0; k < kNG; ++k) {
+                    const int i = t + k * kThreads;
+                    if (i < H) s_xbs[(i >> 5) * 33 + (i & 31)] = gxv[k];
+                }
+            }
             __syncthreads();
+            if constexpr (GV) {
+#pragma unroll
+                for (int j = 0; j < 32; ++j) xr[j] = gact ? s_xbs[c * 33 + j] : 0.f;
+            }
             const uint16_t *scg = (const uint16_t *)(s_sc + mis0), *scu = (const uint16_t *)(s_sc + kScW + mis1);
             // gate/up math as the data arrives, each pair's math followed by
             // the next pair's loads and, once those are all issued, by the
@@ -1067,8 +1112,9 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
             auto ready = [&](uint64_t w) { return one ? tag_is(w, tagY) : ((uint32_t)w & 15u) == nibY; };
             auto load = [&]() { return one ? ld_tag(yq) : (uint64_t)ld_u32_dev(yp); };
             uint64_t yw = hasy ? load() : (one ? (uint64_t)tagY << 32 : (uint64_t)nibY);
+            const bool wflags = one && !GV;   // x (0) read by every block (routed one-layer launches)
             bool up = true;
-            if (one)
+            if (wflags)
                 for (int i = tq; i < NB; i += kThreads)
                     up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.seq0;
             for (unsigned spins = 0; !ready(yw) || !up; ++spins) {
@@ -1079,7 +1125,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                 __builtin_amdgcn_s_sleep(1);
                 if (!ready(yw)) yw = load();
                 up = true;
-                if (one)
+                if (wflags)
                     for (int i = tq; i < NB; i += kThreads)
                         up = up && __hip_atomic_load(&A.flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.seq0;
             }
@@ -1089,7 +1135,27 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                 if (t == 0) raise_err(R.err);
                 return;
             }
-            if (t < nr) {
+            if (t < nr && GV) {
+#pragma clang fp contract(off)
+                // routing given: each slot's w_i y_i added into x in ascending
+                // expert order, slot order among equal ids (the expert-major
+                // loop, engine/midge.c:595-611, with expert_apply's
+                // x_out += weight * moe, midge.c:465-466)
+                float acc = gx0;
+                int prev = -1;
+                for (int n2 = 0; n2 < K; ++n2) {
+                    int best = 0x7fffffff;
+                    for (int i = 0; i < K; ++i) {
+                        const int key = s_sel[i] * kMaxGrpK + i;
+                        if (s_sel[i] >= 0 && key > prev && key < best) best = key;
+                    }
+                    if (best == 0x7fffffff) break;
+                    prev = best;
+                    const int i = best % kMaxGrpK;
+                    acc = acc + s_w[i] * s_y[i * kRBMax + t];
+                }
+                st_dev(R.x + r0 + t, acc);
+            } else if (t < nr) {
 #pragma clang fp contract(off)
                 float moe = 0.f;
                 for (int i = 0; i < K; ++i) {
@@ -1374,10 +1440,10 @@ int launch_step(const void *k, const Args &A, int nb, hipStream_t s, int *ready_
     return hip_check(e, "decode step launch");
 }
 
-template <int RDT>
+template <int RDT, bool GV>
 int launch_grp(const GrpArgs &A, int nb, hipStream_t s) {
     static int ready_dev = -1, per_cu = 0;
-    return launch_step((const void *)k_decode_grp<RDT>, A, nb, s, &ready_dev, &per_cu);
+    return launch_step((const void *)k_decode_grp<RDT, GV>, A, nb, s, &ready_dev, &per_cu);
 }
 
 template <int RDT, int XDT>
@@ -1693,13 +1759,21 @@ int fold_stamps(const StepPlan *p, int n_layers, int nb, const Span (&spans)[NS]
 }  // namespace
 
 int step_run(StepPlan *p, const DevLayer *layers, int first, int n_layers, float *x, int32_t *sel, float *w,
-             uint32_t *usage, hipStream_t s) {
+             uint32_t *usage, hipStream_t s, const float *gxb, const int32_t *gsel, const float *gw) {
     if (!p || !p->ok) return fail(MH_E_UNSUPPORTED, "decode step: no one-launch kernel for this stack");
     if (first < 0 || n_layers < 1 || first + n_layers > p->n_layers)
         return fail(MH_E_ARG, "decode step: layers [%d, %d) outside the plan's %d", first, first + n_layers, p->n_layers);
     const DevLayer &L0 = layers[first];
     const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two kernels
     const bool grp = p->grp && !(nm && nm[0] && nm[0] != '0');
+    if (gxb) {
+        // routing given: k_decode_grp only, one layer; xb must not overlap x
+        // (the combine writes x while other blocks may still read xb)
+        if (!grp) return fail(MH_E_UNSUPPORTED, "expert apply: the expert-group kernel does not fit this stack");
+        if (n_layers != 1 || !gsel || !gw) return fail(MH_E_ARG, "expert apply: one layer with sel and w");
+        const uintptr_t xa = (uintptr_t)x, ba = (uintptr_t)gxb, nbyt = (uintptr_t)L0.hidden * 4u;
+        if (xa < ba + nbyt && ba < xa + nbyt) return fail(MH_E_UNSUPPORTED, "expert apply: xb overlaps x");
+    }
     if (!grp && !p->flat) return fail(MH_E_UNSUPPORTED, "decode step: the vector-ALU kernel does not fit this stack");
     const TagLayout tl = tag_layout(L0);
     RouteArgs R;
@@ -1754,7 +1828,13 @@ int step_run(StepPlan *p, const DevLayer *layers, int first, int n_layers, float
         A.y1 = p->tagged + tl.y1;
         A.bank = p->launches & 1u;
         if (n_layers > 1) ++p->launches;
-        rc = q8 ? launch_grp<MH_DT_Q8R>(A, nb, s) : launch_grp<MH_DT_F32>(A, nb, s);
+        A.gxb = gxb;
+        A.gsel = gsel;
+        A.gw = gw;
+        if (gxb)
+            rc = q8 ? launch_grp<MH_DT_Q8R, true>(A, nb, s) : launch_grp<MH_DT_F32, true>(A, nb, s);
+        else
+            rc = q8 ? launch_grp<MH_DT_Q8R, false>(A, nb, s) : launch_grp<MH_DT_F32, false>(A, nb, s);
     } else {
         StepArgs A;
         A.R = R;

@@ -118,9 +118,13 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out);
 void step_plan_destroy(StepPlan *p);
 bool step_plan_ok(const StepPlan *p);
 // Runs layers [first, first + n_layers) of a plan in one launch; sel, w and
-// usage are indexed from layer `first`.
+// usage are indexed from layer `first`. With gxb (then one layer, gsel and
+// gw [K]): expert_apply per slot with the routing given, x += w_i
+// expert_{sel_i}(gxb) in ascending expert order; MH_E_UNSUPPORTED if the
+// expert-group kernel cannot run it.
 int step_run(StepPlan *p, const DevLayer *layers, int first, int n_layers, float *x, int32_t *sel, float *w,
-             uint32_t *usage, hipStream_t s);
+             uint32_t *usage, hipStream_t s, const float *gxb = nullptr, const int32_t *gsel = nullptr,
+             const float *gw = nullptr);
 
 // Kernel timing (mh_profile_*): while enabled, every launch made through
 // MH_LAUNCH is bracketed by HIP events on its stream and accounted under its

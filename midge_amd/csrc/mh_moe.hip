@@ -751,6 +751,29 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
     return MH_OK;
 }
 
+int mh_stack_apply_dev(mh_stack *st, int layer, const float *xb, const int32_t *sel, const float *w, float *x) {
+    clear_error();
+    if (!st) return fail(MH_E_ARG, "mh_stack_apply_dev: NULL stack");
+    const int nl = (int)st->layers.size();
+    if (layer < 0 || layer >= nl) return fail(MH_E_ARG, "mh_stack_apply_dev: layer %d outside [0, %d)", layer, nl);
+    MH_TRY(require_init());
+    const DevLayer &L = st->layers[(size_t)layer];
+    MH_TRY(resolve_dev(xb, (uint64_t)L.hidden * 4, "mh_stack_apply_dev xb"));
+    MH_TRY(resolve_dev(sel, (uint64_t)L.top_k * 4, "mh_stack_apply_dev sel"));
+    MH_TRY(resolve_dev(w, (uint64_t)L.top_k * 4, "mh_stack_apply_dev w"));
+    MH_TRY(resolve_dev(x, (uint64_t)L.hidden * 4, "mh_stack_apply_dev x"));
+    hipStream_t s = stream();
+    const char *nf = getenv("MIDGE_HIP_NO_FUSED");   // per call, so callers can A/B the two paths
+    if (!(nf && *nf && *nf != '0') && step_plan_ok(st->plan)) {
+        int rc = step_run(st->plan, st->layers.data(), layer, 1, x, nullptr, nullptr, nullptr, s, xb, sel, w);
+        if (rc != MH_E_UNSUPPORTED) return rc;
+        clear_error();   // per-layer launches below
+    }
+    LayerBufs b;
+    MH_TRY(layer_bufs(L, 1, &b));
+    return run_expert_major(L, 1, xb, sel, w, x, b, s);
+}
+
 int mh_stack_destroy(mh_stack *st) {
     clear_error();
     if (st) {

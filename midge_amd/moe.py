@@ -182,6 +182,11 @@ class Stack:
         _lib.call("mh_stack_decode", self.handle, int(x), int(batch), int(sel or 0), int(w or 0),
                   int(usage or 0))
 
+    def apply(self, layer: int, xb, sel, w, x) -> None:
+        """expert_apply for one token with the routing given (device xb,
+        sel, w, x): x += w_i expert_{sel_i}(xb) in ascending expert order."""
+        _lib.call("mh_stack_apply_dev", self.handle, int(layer), int(xb), int(sel), int(w), int(x))
+
     def destroy(self) -> None:
         if self.handle:
             _lib.call("mh_stack_destroy", self.handle)

@@ -389,6 +389,61 @@ def test_stack_fused_step_vs_per_layer_and_oracle(mh, shape, layers):
         x = xo
 
 
+@pytest.mark.parametrize("shape", [
+    MoEShape(hidden=2880, ffn=2880, n_experts=1, top_k=1),
+    MoEShape(hidden=256, ffn=192, n_experts=16, top_k=4),
+    MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4),
+], ids=["one_expert", "mid", "gptoss20b"])
+def test_stack_apply_vs_expert_major_and_oracle(mh, shape):
+    """expert_apply with the routing given (mh_stack_apply_dev, engine/
+    midge.c:436-467 per slot in the expert-major loop's order, 595-611): the
+    one-launch kernel against the per-layer expert-major kernels (SPLIT_TOL)
+    and the oracle's expert-major loop (TOL), over slot orders that are not
+    ascending, a repeated expert and unfilled slots, three calls in a row on
+    one stack."""
+    import os
+    say(f"stack apply {shape.hidden}x{shape.ffn} E={shape.n_experts} k={shape.top_k}")
+    keys = Keys(91)
+    ex = synth.host_layer_experts(shape, keys, 0)
+    w, s, b, nw = synth.host_router(shape, keys, 0)
+    lay = MoELayer.host(shape, ex, w, s, b, nw)
+    _LIVE.append(lay)
+    L = po.layer_struct(shape, ex, w, s, b, nw)
+    st = Stack([lay], max_batch=1)
+    k, E = shape.top_k, shape.n_experts
+    rng = np.random.default_rng(5)
+    sels = [[0], [0], [-1]] if k == 1 else [[E - 1, 2, 7, 0], [3, 3, 1, -1], [5, -1, -1, 5]]
+    for sel in sels:
+        sel = np.array(sel, np.int32)
+        wv = rng.uniform(0.05, 1.0, k).astype(np.float32)
+        xb = rng.standard_normal(shape.hidden).astype(np.float32)
+        x0 = rng.standard_normal(shape.hidden).astype(np.float32)
+        out = {}
+        for mode in ("fused", "per_layer"):
+            if mode == "per_layer":
+                os.environ["MIDGE_HIP_NO_FUSED"] = "1"
+            try:
+                bufs = [DevBuf.from_array(a) for a in (xb, sel, wv, x0)]
+                st.apply(0, *bufs)
+                mh.sync()
+                out[mode] = bufs[3].download(np.float32, (shape.hidden,))
+                for d in bufs:
+                    d.free()
+            finally:
+                os.environ.pop("MIDGE_HIP_NO_FUSED", None)
+        want = po.expert_major_apply(L, xb[None], sel[None], wv[None], x0[None])[0]
+        if (sel < 0).all():
+            assert np.array_equal(out["fused"], x0) and np.array_equal(out["per_layer"], x0)
+            continue
+        # the one-launch kernel's down sums in another order: its result is
+        # not bit-identical to the per-layer kernels' (so it did run)
+        assert not np.array_equal(out["fused"], out["per_layer"])
+        assert rel_l2(out["fused"], out["per_layer"]) < SPLIT_TOL, sel
+        assert rel_l2(out["fused"], want) < TOL, sel
+        assert rel_l2(out["per_layer"], want) < TOL, sel
+    st.destroy()
+
+
 FUSED_VARIANTS = {
     "softmax_all_logits": dict(router_norm=0),
     "plain_silu": dict(act_plain=1),
