@@ -50,6 +50,7 @@
 #include <vector>
 
 #include "mh_gemv.cuh"
+#include "mh_mfma16.cuh"
 #include "mh_xchg.cuh"
 
 namespace mh {
@@ -647,27 +648,6 @@ __device__ __forceinline__ bool route_layer(const RouteArgs &R, const RouterPref
 // The weights cannot be loaded in this lane layout directly (16 rows x 64 B
 // per instruction streams from HBM ~25% slower than whole rows), so they are
 // loaded as whole rows and staged through LDS.
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v2h __attribute__((ext_vector_type(2)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v8h fp4x8_f16(uint32_t w, float s) {
-    const v2h a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0);
-    const v2h b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1);
-    const v2h c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2);
-    const v2h d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3);
-    return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3),
-                                   0, 1, 2, 3, 4, 5, 6, 7);
-}
-__device__ __forceinline__ uint32_t dword_of(const mh_u4 &q, int j) {
-    return j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
-}
-// v of lane + K within the lane's row of 16 (0 past the row's end)
-template <int K>
-__device__ __forceinline__ float dpp_shl(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + K, 0xF, 0xF, false));
-}
-
 // One wave's share of the down projection: the K steps q = kQ wave .. +kQ
 // (128 columns each) of the block's down rows [0, rows), staged in LDS at a
 // stride of SD chunks (sw; their f16 scales ss at a stride of CF), times the
@@ -1396,17 +1376,18 @@ __global__ void k_fill_u32(unsigned *p, int n, unsigned v) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
 }
 
-// Flags a down-projection MXFP4 scale that the MFMA path cannot apply
-// exactly in f16: it must be zero or a power of two in [2^-23, 2^13], so that
-// every e2m1 value times it is an f16.
-__global__ void k_scan_scales(const uint8_t *experts, uint64_t stride, uint64_t od, int n, unsigned *bad) {
+// Flags (bit) an MXFP4 scale that the f16 matrix-core paths cannot apply
+// exactly: it must be zero or a power of two in [2^-23, 2^13], so that every
+// e2m1 value times it is an f16.
+__global__ void k_scan_scales(const uint8_t *experts, uint64_t stride, uint64_t od, int n, unsigned *bad,
+                              unsigned bit) {
     const uint16_t *d = (const uint16_t *)(experts + (uint64_t)blockIdx.y * stride + od);
     bool ok = true;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         const unsigned v = d[i], e = (v >> 10) & 31u, mn = v & 1023u;
         ok = ok && ((v & 0x7FFFu) == 0 || (e == 0 && mn >= 2 && (mn & (mn - 1)) == 0) || (e != 0 && e <= 28 && mn == 0));
     }
-    if (!ok) atomicOr(bad, 1u);
+    if (!ok) atomicOr(bad, bit);
 }
 
 // Launch of a one-launch step: nb blocks of kThreads. Every block must be
@@ -1480,6 +1461,7 @@ struct StepPlan {
     int grp = 0;                   // 1 = k_decode_grp can run the stack
     int G = 0, PB = 0, RB = 0;     // k_decode_grp's shape (grid G * K)
     int ok = 0;                    // 1 = one of the kernels is eligible
+    int few = 0;                   // 1 = every MXFP4 scale is f16-exact (the few-token expert kernels)
     char why[160] = {0};
     std::vector<std::pair<void *, uint64_t>> mem;   // device allocations (counted)
 };
@@ -1634,22 +1616,29 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     MH_TRY(plan_alloc(p, &p->tagged, sizeof(uint64_t) * p->tagged_words, "decode plan exchange words"));
     MH_HIP(hipMemset(p->tagged, 0, sizeof(uint64_t) * p->tagged_words));
     MH_TRY(plan_alloc(p, &p->h, sizeof(float) * (size_t)L0.top_k * (size_t)L0.ffn, "decode plan h"));
-    if (p->grp) {
+    if (L0.expert_dt == MH_DT_MXFP4) {
+        // down scales (bit 1: the expert-group kernel), gate and up scales
+        // (bit 2: with bit 1, the few-token expert kernels of batches 2-16)
         unsigned *bad = nullptr;
         MH_TRY(dev_alloc((void **)&bad, sizeof(unsigned), "decode plan scale scan"));
         MH_HIP(hipMemset(bad, 0, sizeof(unsigned)));
-        const int n_dn = (int)(L0.hidden * (L0.ffn / 32));
+        const int n_dn = (int)(L0.hidden * (L0.ffn / 32)), n_gu = (int)(L0.ffn * (L0.hidden / 32));
         for (int l = 0; l < n_layers; l++) {
             const DevLayer &L = layers[l];
             hipLaunchKernelGGL(k_scan_scales, dim3(16, (unsigned)L.n_experts), dim3(256), 0, 0, L.experts,
-                               L.expert_stride, L.off[7], n_dn, bad);
+                               L.expert_stride, L.off[7], n_dn, bad, 1u);
+            hipLaunchKernelGGL(k_scan_scales, dim3(16, (unsigned)L.n_experts), dim3(256), 0, 0, L.experts,
+                               L.expert_stride, L.off[1], n_gu, bad, 2u);
+            hipLaunchKernelGGL(k_scan_scales, dim3(16, (unsigned)L.n_experts), dim3(256), 0, 0, L.experts,
+                               L.expert_stride, L.off[4], n_gu, bad, 2u);
         }
         unsigned hb = 0;
         const hipError_t le = hipGetLastError();
         const hipError_t ce = le != hipSuccess ? le : hipMemcpy(&hb, bad, sizeof(unsigned), hipMemcpyDeviceToHost);
         dev_release(bad, sizeof(unsigned));
         MH_HIP(ce);
-        if (hb) p->grp = 0;   // the vector-ALU kernel handles any f16 scale
+        if (hb & 1u) p->grp = 0;   // the vector-ALU kernel handles any f16 scale
+        p->few = hb == 0u;
     }
     MH_HIP(hipMemset(p->flags, 0, sizeof(unsigned) * (size_t)flag_words(nb)));
     MH_HIP(hipDeviceSynchronize());
@@ -1668,6 +1657,7 @@ void step_plan_destroy(StepPlan *p) {
 }
 
 bool step_plan_ok(const StepPlan *p) { return p && p->ok; }
+bool step_plan_few(const StepPlan *p) { return p && p->few; }
 
 namespace {
 

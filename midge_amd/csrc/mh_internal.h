@@ -117,6 +117,15 @@ struct StepPlan;
 int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out);
 void step_plan_destroy(StepPlan *p);
 bool step_plan_ok(const StepPlan *p);
+// 1 if every MXFP4 scale of the plan's layers is f16-exact (the few-token
+// expert kernels may run them).
+bool step_plan_few(const StepPlan *p);
+// The expert FFN of a decode step of 2-16 tokens on the f16 matrix cores
+// (mh_fewtok.hip): h from xb, then ye, walking the top-k kernel's
+// expert-sorted order. fewtok_ok: the layer and token count fit.
+bool fewtok_ok(const DevLayer &L, int n);
+int launch_fewtok(const DevLayer &L, int n, const int32_t *order, const float *xb, float *h, float *ye,
+                  hipStream_t s);
 // Runs layers [first, first + n_layers) of a plan in one launch; sel, w and
 // usage are indexed from layer `first`. With gxb (then one layer, gsel and
 // gw [K]): expert_apply per slot with the routing given, x += w_i

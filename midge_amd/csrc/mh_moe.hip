@@ -442,9 +442,19 @@ int run_router(const DevLayer &L, const float *x, int n, int unfilled, const Lay
                        s);
 }
 
-int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uint32_t *usage, hipStream_t s) {
+// few: the layer's MXFP4 scales are known to be f16-exact (a stack's plan
+// scanned them), so 2-16 tokens may take the few-token matrix-core kernels
+// when MIDGE_HIP_FEW=1 (opt-in: at 16 tokens of gpt-oss-120b they are
+// slower than the per-assignment GEMVs, 7.3 vs 6.05 ms per step, being
+// bound by the e2m1 -> f16 conversion at one wave per SIMD).
+int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uint32_t *usage, hipStream_t s,
+                     bool few = false) {
     MH_TRY(run_router(L, x, n, -1, b, usage, b.order, s));
-    MH_TRY(launch_experts(L, n * L.top_k, b.sel, b.order, b.xb, b.h, b.ye, s));
+    const char *fe = getenv("MIDGE_HIP_FEW");
+    if (few && b.order && fe && *fe && *fe != '0' && fewtok_ok(L, n))
+        MH_TRY(launch_fewtok(L, n, b.order, b.xb, b.h, b.ye, s));
+    else
+        MH_TRY(launch_experts(L, n * L.top_k, b.sel, b.order, b.xb, b.h, b.ye, s));
     MH_LAUNCH("combine_decode", k_combine_decode, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s, x,
                        b.ye, b.w, L.hidden, L.top_k);
     return hip_check(hipGetLastError(), "combine launch");
@@ -746,7 +756,7 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
         if (sel) bl.sel = sel + (size_t)l * batch * k;
         if (w) bl.w = w + (size_t)l * batch * k;
         MH_TRY(run_decode_layer(st->layers[(size_t)l], x, batch, bl,
-                                usage ? usage + (size_t)l * L0.n_experts : nullptr, s));
+                                usage ? usage + (size_t)l * L0.n_experts : nullptr, s, step_plan_few(st->plan)));
     }
     return MH_OK;
 }

@@ -444,6 +444,84 @@ def test_stack_apply_vs_expert_major_and_oracle(mh, shape):
     st.destroy()
 
 
+def _composed_decode(shape, arrays, L, x):
+    """moe() for one token composed from the oracle's pieces (router, stable
+    top-k, weights, each filled slot's expert FFN, the combine in selection
+    order), which also covers unfilled slots (expert -1, skipped)."""
+    ex, w, s, b, nw = arrays
+    xb = po.rmsnorm(x, nw, shape.norm_eps)
+    rl = po.matvec(shape.router_dt, w, s, xb, shape.n_experts, shape.hidden) + b
+    sel, val = po.topk(rl, shape.top_k, decode=True)
+    wr = po.router_weights(rl, val, 1)
+    moe = np.zeros(shape.hidden, np.float32)
+    for i, e in enumerate(np.asarray(sel)):
+        if e >= 0:
+            moe = moe + np.float32(wr[i]) * po.expert_ffn(L, int(e), xb)
+    return x + moe, np.asarray(sel)
+
+
+@pytest.mark.parametrize("shape,batch,case", [
+    (MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4), 2, "random"),
+    (MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4), 7, "random"),
+    (MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4), 16, "random"),
+    (MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4), 16, "same"),
+    (MoEShape(hidden=256, ffn=192, n_experts=16, top_k=4), 16, "random"),
+    (MoEShape(hidden=256, ffn=192, n_experts=16, top_k=4), 9, "unfilled"),
+], ids=["20b-b2", "20b-b7", "20b-b16", "20b-b16-one-run", "mid-b16", "mid-b9-unfilled"])
+def test_stack_batch_few_token_kernels(mh, shape, batch, case):
+    """Decode of 2-16 tokens through a stack: the few-token matrix-core
+    kernels (MIDGE_HIP_FEW=1; assignments grouped by expert, groups of up to
+    4) against the per-assignment GEMVs (the default) within SPLIT_TOL and
+    the oracle within TOL per token, with identical selections. "same": every token
+    equal, so each routed expert has a run of `batch` assignments (groups of
+    4 and a remainder); "unfilled": only two experts can be routed, so two
+    slots per token are unfilled (their y is 0)."""
+    import os
+    say(f"few-token {shape.hidden}x{shape.ffn} E={shape.n_experts} batch={batch} {case}")
+    keys = Keys(64)
+    ex = synth.host_layer_experts(shape, keys, 0)
+    w, s, b, nw = synth.host_router(shape, keys, 0)
+    if case == "unfilled":
+        b = np.full_like(b, -1e31)
+        b[[2, 11]] = 0.0
+    lay = MoELayer.host(shape, ex, w, s, b, nw)
+    _LIVE.append(lay)
+    L = po.layer_struct(shape, ex, w, s, b, nw)
+    st = Stack([lay], max_batch=16)
+    k = shape.top_k
+    x0 = synth.host_x(shape, keys, batch, step=3)
+    if case == "same":
+        x0 = np.ascontiguousarray(np.repeat(x0[:1], batch, axis=0))
+    out = {}
+    for mode in ("few", "gemv"):
+        if mode == "few":
+            os.environ["MIDGE_HIP_FEW"] = "1"
+        try:
+            xd, sd = DevBuf.from_array(x0), DevBuf(batch * k * 4)
+            st.decode(xd, batch, sd)
+            mh.sync()
+            out[mode] = (xd.download(np.float32, x0.shape), sd.download(np.int32, (batch, k)))
+            xd.free()
+            sd.free()
+        finally:
+            os.environ.pop("MIDGE_HIP_FEW", None)
+    st.destroy()
+    xf, sf = out["few"]
+    xg, sg = out["gemv"]
+    assert (sf == sg).all()
+    # the two paths sum in different orders: not bit-identical (so the
+    # matrix-core path ran), within SPLIT_TOL per token
+    assert not np.array_equal(xf, xg)
+    for t in range(batch):
+        assert rel_l2(xf[t], xg[t]) < SPLIT_TOL, t
+    for t in sorted({0, batch // 2, batch - 1}):
+        want, selr = _composed_decode(shape, (ex, w, s, b, nw), L, x0[t])
+        assert (sf[t] == selr).all(), (t, sf[t], selr)
+        assert rel_l2(xf[t], want) < TOL, t
+    if case == "unfilled":
+        assert (sf[:, 2:] == -1).all()
+
+
 FUSED_VARIANTS = {
     "softmax_all_logits": dict(router_norm=0),
     "plain_silu": dict(act_plain=1),
