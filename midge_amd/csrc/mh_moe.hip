@@ -293,6 +293,35 @@ k_combine_decode(float *__restrict__ x, const float *__restrict__ ye, const floa
     x[(size_t)t * H + r] = x[(size_t)t * H + r] + moe;
 }
 
+// The decode combine of one layer and the next layer's RMSNorm in one
+// launch (one block of 1024 threads per token): x += moe exactly as
+// k_combine_decode, then xb = x * inv * w exactly as k_rmsnorm (the same
+// per-thread order of the squares and the same reductions), so the fused
+// pair is bit-identical to the two launches.
+__global__ void __launch_bounds__(1024)
+k_combine_norm(float *__restrict__ x, const float *__restrict__ ye, const float *__restrict__ w, int64_t H, int k,
+               const float *__restrict__ nw, float eps, float *__restrict__ xb) {
+#pragma clang fp contract(off)
+    __shared__ float part[16];
+    const int t = blockIdx.x;
+    float *xt = x + (size_t)t * H;
+    float s = 0.f;
+    for (int64_t r = threadIdx.x; r < H; r += blockDim.x) {
+        float moe = 0.f;
+        for (int i = 0; i < k; ++i) moe = moe + w[(size_t)t * k + i] * ye[((size_t)t * k + i) * H + r];
+        const float v = xt[r] + moe;
+        xt[r] = v;
+        s = __builtin_fmaf(v, v, s);
+    }
+    s = mh_wave_sum(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float ss = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) ss += part[i];
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int64_t r = threadIdx.x; r < H; r += blockDim.x) xb[(size_t)t * H + r] = xt[r] * inv * nw[r];
+}
+
 // Prefill combine (engine/midge.c:595-611, 465-466): each token's
 // contributions are added straight into its residual in ascending expert
 // order (slot order among equal ids, as the reference's loops give).
@@ -434,9 +463,10 @@ int layer_bufs(const DevLayer &L, int n, LayerBufs *b) {
 
 // Router (rmsnorm, logits, top-k) for n tokens into b->xb / b->sel / b->w
 // (and the expert-sorted order into `order` when it is not null).
+// x null: b.xb already holds rmsnorm(x) of this layer (k_combine_norm).
 int run_router(const DevLayer &L, const float *x, int n, int unfilled, const LayerBufs &b, uint32_t *usage,
                int32_t *order, hipStream_t s) {
-    MH_TRY(launch_rmsnorm(x, L.mlp_norm, b.xb, L.hidden, L.norm_eps, n, s));
+    if (x) MH_TRY(launch_rmsnorm(x, L.mlp_norm, b.xb, L.hidden, L.norm_eps, n, s));
     MH_TRY(launch_gemv(L.router, b.xb, b.rl, n, s));
     return launch_topk(b.rl, L.router_b, n, L.n_experts, L.top_k, L.router_norm, unfilled, b.sel, b.w, usage, order,
                        s);
@@ -447,16 +477,23 @@ int run_router(const DevLayer &L, const float *x, int n, int unfilled, const Lay
 // when MIDGE_HIP_FEW=1 (opt-in: at 16 tokens of gpt-oss-120b they are
 // slower than the per-assignment GEMVs, 7.3 vs 6.05 ms per step, being
 // bound by the e2m1 -> f16 conversion at one wave per SIMD).
+// have_xb: b.xb holds this layer's normed input already; next: the next
+// layer, whose RMSNorm is fused into this layer's combine (or null).
 int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uint32_t *usage, hipStream_t s,
-                     bool few = false) {
-    MH_TRY(run_router(L, x, n, -1, b, usage, b.order, s));
+                     bool few = false, bool have_xb = false, const DevLayer *next = nullptr) {
+    MH_TRY(run_router(L, have_xb ? nullptr : x, n, -1, b, usage, b.order, s));
     const char *fe = getenv("MIDGE_HIP_FEW");
     if (few && b.order && fe && *fe && *fe != '0' && fewtok_ok(L, n))
         MH_TRY(launch_fewtok(L, n, b.order, b.xb, b.h, b.ye, s));
     else
         MH_TRY(launch_experts(L, n * L.top_k, b.sel, b.order, b.xb, b.h, b.ye, s));
-    MH_LAUNCH("combine_decode", k_combine_decode, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s, x,
-                       b.ye, b.w, L.hidden, L.top_k);
+    if (next) {
+        MH_LAUNCH("combine_norm", k_combine_norm, dim3((unsigned)n), dim3(1024), 0, s, x, b.ye, b.w, L.hidden, L.top_k,
+                  next->mlp_norm, next->norm_eps, b.xb);
+    } else {
+        MH_LAUNCH("combine_decode", k_combine_decode, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256),
+                  0, s, x, b.ye, b.w, L.hidden, L.top_k);
+    }
     return hip_check(hipGetLastError(), "combine launch");
 }
 
@@ -755,8 +792,11 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
         LayerBufs bl = b;
         if (sel) bl.sel = sel + (size_t)l * batch * k;
         if (w) bl.w = w + (size_t)l * batch * k;
+        // every layer after the first takes its normed input from the
+        // previous layer's combine
         MH_TRY(run_decode_layer(st->layers[(size_t)l], x, batch, bl,
-                                usage ? usage + (size_t)l * L0.n_experts : nullptr, s, step_plan_few(st->plan)));
+                                usage ? usage + (size_t)l * L0.n_experts : nullptr, s, step_plan_few(st->plan), l > 0,
+                                l + 1 < nl ? &st->layers[(size_t)l + 1] : nullptr));
     }
     return MH_OK;
 }
