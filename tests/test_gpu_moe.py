@@ -512,6 +512,8 @@ def test_stack_batch_few_token_kernels(mh, shape, batch, case):
     # the two paths sum in different orders: not bit-identical (so the
     # matrix-core path ran), within SPLIT_TOL per token
     assert not np.array_equal(xf, xg)
+    worst = max(rel_l2(xf[t], xg[t]) for t in range(batch))
+    say(f"few-token vs GEMV: worst per-token rel L2 {worst:.3g}")
     for t in range(batch):
         assert rel_l2(xf[t], xg[t]) < SPLIT_TOL, t
     for t in sorted({0, batch // 2, batch - 1}):
