@@ -60,6 +60,9 @@ def test_null_and_range_arguments():
     out = np.zeros(32, np.float32)
     assert _rc("mh_row", C.byref(t), 4, out.ctypes.data) == _lib.MH_E_RANGE
     assert _rc("mh_row", C.byref(t), -1, out.ctypes.data) == _lib.MH_E_RANGE
+    # stack entry points: a NULL stack is refused before any device work
+    assert _rc("mh_stack_apply_dev", None, 0, 1, 1, 1, 1) == _lib.MH_E_ARG
+    assert _rc("mh_stack_decode", None, 1, 1, None, None, None) == _lib.MH_E_ARG
 
 
 def _layer(**kw) -> _lib.MhMoeLayer:

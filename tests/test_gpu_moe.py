@@ -441,6 +441,20 @@ def test_stack_apply_vs_expert_major_and_oracle(mh, shape):
         assert rel_l2(out["fused"], out["per_layer"]) < SPLIT_TOL, sel
         assert rel_l2(out["fused"], want) < TOL, sel
         assert rel_l2(out["per_layer"], want) < TOL, sel
+    # xb aliasing x: the one-launch kernel would read xb while other blocks
+    # write x, so the call falls back to the per-layer kernels (x += w
+    # expert(x)); against the oracle with the same aliasing
+    sel = np.array(sels[0], np.int32)
+    wv = np.full(k, 0.5, np.float32)
+    x0 = rng.standard_normal(shape.hidden).astype(np.float32)
+    bufs = [DevBuf.from_array(a) for a in (x0, sel, wv)]
+    st.apply(0, bufs[0], bufs[1], bufs[2], bufs[0])
+    mh.sync()
+    got = bufs[0].download(np.float32, (shape.hidden,))
+    for d in bufs:
+        d.free()
+    want = po.expert_major_apply(L, x0[None], sel[None], wv[None], x0[None])[0]
+    assert rel_l2(got, want) < TOL
     st.destroy()
 
 
