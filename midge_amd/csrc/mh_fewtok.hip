@@ -89,9 +89,6 @@ __host__ __device__ inline FewLds few_lds(int K) {
 __device__ __forceinline__ mh_u4 few_ld16(mh_rsrc r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kGemvNT);
 }
-__device__ __forceinline__ float few_ldf(mh_rsrc r, uint32_t off) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-}
 
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
