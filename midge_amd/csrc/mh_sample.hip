@@ -164,7 +164,14 @@ __device__ MaxIdx block_max(MaxIdx m) {
 }
 
 // e of one logit: every kernel evaluates this same expression
-__device__ __forceinline__ float samp_e(float l, float mx, float temp) { return expf((l - mx) / temp); }
+// expf((l - max) / temp) of the reference, the argument formed in f32 as
+// there, the exponential correctly rounded (f64 rounded once to f32):
+// glibc's expf is within 0.502 ulp, so the two differ only where glibc's own
+// result is not the nearest float. (A last-bit difference can reorder two
+// tokens of nearly equal p, and with them a draw that falls between.)
+__device__ __forceinline__ float samp_e(float l, float mx, float temp) {
+    return (float)exp((double)((l - mx) / temp));
+}
 
 // Scans over the block (all threads get the block total). The f64 scan
 // returns the inclusive sum and sets *excl to the exclusive one, computed
