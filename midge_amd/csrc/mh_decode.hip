@@ -15,11 +15,12 @@
 //        rmsnorm(x) * w in LDS; blocks b < E compute router logit b and
 //        publish it in kLR copies;
 //     R  every block's first wave gathers the logits and ranks them itself
-//        (stable top-k, ties to the lower index): all blocks reach the same
-//        selection and weights and nothing is broadcast;
-//     B  the block issues every weight load of its share at once, the
-//        gate/up pairs first and the down rows behind them, so the layer's
-//        weights stream as one transfer; the gate/up math runs as the data
+//        (stable top-k, ties to the lower index) up to its own slot: all
+//        blocks reach the same selection and nothing is broadcast;
+//     B  the block issues its weight loads, the gate/up pairs first and the
+//        down rows behind them, so the layer's weights stream as one
+//        transfer; the first wave then ranks the remaining slots and forms
+//        the weights while the loads fly; the gate/up math runs as the data
 //        arrives; bias + clamped SwiGLU give h, published as tagged words
 //        (h as two f16 terms) to the slot's group;
 //     C  the down rows are staged in LDS; each wave polls only the part of
@@ -327,11 +328,13 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // remaining value, lowest index among equals"; only values > -1e30
 // qualify, unfilled slots get -1 (engine/midge.c:476-486). Lane i < k ends
 // with slot i's expert in *sel and its logit in *val (-1e30 if unfilled).
-__device__ __forceinline__ void wave_topk(float *v, int k, int *sel, float *val) {
+__device__ __forceinline__ void wave_topk(float *v, int k, int *sel, float *val, int i0 = 0) {
     const int lane = threadIdx.x & 63;
-    *sel = -1;
-    *val = -1e30f;
-    for (int i = 0; i < k; ++i) {
+    if (i0 == 0) {
+        *sel = -1;
+        *val = -1e30f;
+    }
+    for (int i = i0; i < k; ++i) {
         float lm = -INFINITY;
 #pragma unroll
         for (int j = 0; j < kEL; ++j) lm = fmaxf(lm, v[j]);
@@ -502,6 +505,37 @@ __device__ __forceinline__ bool gather_x_tagged(const RouteArgs &R, int l, uint6
     return true;
 }
 
+// The ranking wave's state between route_layer (ranked up to a given slot)
+// and route_finish (the remaining slots, the weights and the records).
+struct RankState {
+    float v[kEL], v0[kEL];
+    int sel;
+    float val;
+};
+
+// The rest of layer l's routing after a route_layer that ranked slots
+// [0, from] (wave 0): slots from + 1 .. K - 1, the weights into S.sel / S.w,
+// block 0's records. The caller's next block barrier publishes them.
+__device__ __forceinline__ void route_finish(const RouteArgs &R, int l, const RouteLds &S, RankState &rs, int from) {
+    const int E = R.E, K = R.K, t = threadIdx.x;
+    if (t >= 64) return;
+    const int lane = t;
+    wave_topk(rs.v, K, &rs.sel, &rs.val, from + 1);
+    const float my_w = wave_weight(rs.v0, K, R.router_norm, rs.val);
+    if (lane < K) {
+        const int ln = opaque(lane);
+        S.sel[ln] = rs.sel;
+        S.w[ln] = my_w;
+        if (blockIdx.x == 0) {
+            if (R.sel) R.sel[(size_t)l * K + ln] = rs.sel;
+            if (R.w) R.w[(size_t)l * K + ln] = my_w;
+            if (R.usage && rs.sel >= 0)
+                __hip_atomic_fetch_add(&R.usage[(size_t)l * E + rs.sel], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 // Phase A and the routing of layer l, common to both kernels.
 //  - x: getx(xv) fills this thread's elements t + k kThreads of x (0 past H)
 //    and returns false if a wait timed out (gather_x_tagged, or k_decode_grp's
@@ -518,11 +552,15 @@ __device__ __forceinline__ bool gather_x_tagged(const RouteArgs &R, int l, uint6
 //    ranks them (wave_topk: the reference's insertion order, ties to the
 //    lower index) and computes the weights; block 0 records sel, w and the
 //    usage counts. The block's other waves wait at the closing barrier.
+//    With `split` (k_decode_grp) the wave ranks slots 0 .. upto only, the
+//    block's own expert, and leaves the rest to route_finish: a block needs
+//    only its slot's expert to issue its weight loads.
 // Returns false, with the error flag raised, if a wait timed out (every
 // thread of the block returns the same value).
 template <int RDT, class GetX>
 __device__ __forceinline__ bool route_layer(const RouteArgs &R, const RouterPref &pf, int l, GetX getx,
-                                            unsigned ltag, const RouteLds &S, const Stamper &stamp) {
+                                            unsigned ltag, const RouteLds &S, const Stamper &stamp,
+                                            RankState *split = nullptr, int upto = 0) {
     const int H = R.H, E = R.E, K = R.K;
     const int NB = gridDim.x, b = blockIdx.x, t = threadIdx.x;
     const StepLayer Ly = R.layers[l];
@@ -607,11 +645,24 @@ __device__ __forceinline__ bool route_layer(const RouteArgs &R, const RouterPref
         }
         int my_sel;
         float my_val;
-        wave_topk(v, K, &my_sel, &my_val);
+        if (split) {
+            // slots 0 .. upto only: the block's own expert (S.sel[upto]); the
+            // rest after the caller has issued its weight loads
+            wave_topk(v, upto + 1, &my_sel, &my_val);
+            if (lane == upto) S.sel[opaque(lane)] = my_sel;
+#pragma unroll
+            for (int j = 0; j < kEL; ++j) {
+                split->v[j] = v[j];
+                split->v0[j] = v0[j];
+            }
+            split->sel = my_sel;
+            split->val = my_val;
+        }
+        if (!split) wave_topk(v, K, &my_sel, &my_val);
         if (b == 0) stamp(l, 17);
-        const float my_w = wave_weight(v0, K, R.router_norm, my_val);
+        const float my_w = split ? 0.f : wave_weight(v0, K, R.router_norm, my_val);
         if (b == 0) stamp(l, 18);
-        if (lane < K) {
+        if (lane < K && !split) {
             // (addresses from an opaque lane: recomputed here, not hoisted
             // out of the layer loop and spilled)
             const int ln = opaque(lane);
@@ -742,6 +793,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
         // sequence numbers of this layer: logits, h, y (the fourth is unused)
         const unsigned tagL = A.seq0 + 4u * (unsigned)l, tagH = tagL + 1u, tagY = tagL + 2u;
         stamp(l, 0);
+        RankState rks;   // the ranking wave's state (routed launches)
         // routing given: this thread's xb elements t + k kThreads (stored to
         // LDS once the weight loads are issued) and, in a slot-0 block, x of
         // its row for the combine
@@ -834,7 +886,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
             // the router row's loads are issued here and land while x is on
             // its way (held across the layer they would cost 18 registers)
             const RouterPref pf = prefetch_router<RDT>(R, l);
-            if (!route_layer<RDT>(R, pf, l, getx, tagL, S, stamp)) return;
+            if (!route_layer<RDT>(R, pf, l, getx, tagL, S, stamp, &rks, slot)) return;
         }
         // x (0) read: the last layer's combine overwrites R.x only once every
         // block has raised this flag
@@ -862,11 +914,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
             const bool gact = gs < ns;
             const int gsl = gact ? gs : ns - 1;
             const int plast = max(np - 1, 0);
-            float xr[32];
-            if constexpr (!GV) {
-#pragma unroll
-                for (int j = 0; j < 32; ++j) xr[j] = gact ? s_xbs[c * 33 + j] : 0.f;
-            }
+            float xr[32];   // this thread's chunk of xb (read from LDS once the loads are issued)
             // the scales first: the block's gate, up and down scale rows are
             // three contiguous ranges, loaded as 16-byte chunks of their
             // aligned windows (mis: the range's offset in its window)
@@ -905,6 +953,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
             const float bu = ld_f(rex, eo + (uint32_t)A.off[5] + pb4);
             __builtin_amdgcn_sched_barrier(0);
             stamp(l, 9);
+            // the other slots' experts and the weights, while the loads fly
+            if constexpr (!GV) route_finish(R, l, S, rks, slot);
             // the scale windows into LDS (their loads were issued first, so
             // they complete first)
 #pragma unroll
@@ -921,10 +971,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                 }
             }
             __syncthreads();
-            if constexpr (GV) {
 #pragma unroll
-                for (int j = 0; j < 32; ++j) xr[j] = gact ? s_xbs[c * 33 + j] : 0.f;
-            }
+            for (int j = 0; j < 32; ++j) xr[j] = gact ? s_xbs[c * 33 + j] : 0.f;
             const uint16_t *scg = (const uint16_t *)(s_sc + mis0), *scu = (const uint16_t *)(s_sc + kScW + mis1);
             // gate/up math as the data arrives, each pair's math followed by
             // the next pair's loads and, once those are all issued, by the
@@ -1057,6 +1105,9 @@ __global__ void __launch_bounds__(kThreads) k_decode_grp(GrpArgs A) {
                 for (int w = 0; w < kThreads / 64; ++w) sum += s_dred[w * kRBMax + t];
                 y = sum + s_bd[t];   // the matvec, then wk_addbias (engine/midge.c:539-541)
             }
+        } else if constexpr (!GV) {
+            route_finish(R, l, S, rks, slot);
+            __syncthreads();   // the selection and weights before any later read
         }
         // -------------------------------------- D: y
         // every block publishes its rows of its slot's y (0 for a slot with
