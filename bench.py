@@ -736,7 +736,7 @@ def prefill_probe(ev, s, seed: int, n: int = 512, reps: int = 10) -> dict:
     scaled-MFMA GEMM path and, for comparison, the per-assignment GEMV path.
     Timed with HIP events over `reps` calls of mh_expert_major_dev."""
     import midge_amd
-    from midge_amd import DevBuf, _lib, synth
+    from midge_amd import DevBuf, _lib, set_switch, synth
     from midge_amd.device import profile_enable, profile_query, profile_reset
     from midge_amd.moe import Stack, expert_major_dev, topk_dev
     from midge_amd.synth import MoEShape
@@ -757,7 +757,7 @@ def prefill_probe(ev, s, seed: int, n: int = 512, reps: int = 10) -> dict:
     useful_flops = 2.0 * n * k * 3 * shape.hidden * shape.ffn
     for path in ("mfma", "gemv"):
         if path == "gemv":
-            os.environ["MIDGE_HIP_NO_MFMA"] = "1"
+            set_switch("NO_MFMA", True)
         try:
             r = reps if path == "mfma" else 2
             expert_major_dev(lay, n, xb, sel, w, x)
@@ -789,7 +789,7 @@ def prefill_probe(ev, s, seed: int, n: int = 512, reps: int = 10) -> dict:
                             if gemm_us else None})
             out[path] = res
         finally:
-            os.environ.pop("MIDGE_HIP_NO_MFMA", None)
+            set_switch("NO_MFMA", False)
     out["speedup_mfma_vs_gemv"] = out["gemv"]["ms"] / out["mfma"]["ms"]
     for d in (logits, xb, x, sel, w):
         d.free()

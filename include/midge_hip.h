@@ -88,6 +88,17 @@ int mh_set_stream(void *stream);
 void *mh_get_stream(void);
 /* Wait for all work on the library stream. */
 int mh_sync(void);
+/* Path switches for comparisons (tests, benchmarks), all off by default.
+ * mh_init reads each from the environment once (MIDGE_HIP_<name> set and not
+ * "0"); this call changes one at run time: "NO_MFMA" (no matrix-core
+ * kernels in the batched int8 GEMV, the prefill and the decode step),
+ * "NO_FUSED" (stack decode as per-layer launches), "ATTN_SPLIT" (attention
+ * as four launches), "COOP" (the one-launch decode step launched
+ * cooperatively), "Q8_NO_ROWS" (long batched int8 GEMVs on the
+ * register-operand kernel). MH_E_ARG for an unknown name. No counterpart in
+ * the reference: its only comparable knob is MIDGE_NO_SIMD, read once at
+ * start-up (engine/mkern.h:75-93). */
+int mh_set_switch(const char *name, int on);
 
 /* Kernel timing. While enabled, every kernel launch is bracketed by HIP
  * events on its stream and accounted under its kernel name ("gemv",
@@ -178,7 +189,8 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos);
 int mh_sample_dev(const float *logits, int64_t V, float temp, float topp, float u, int32_t *out);
 
 /* mh_sample_dev on a fixed workspace that the library holds on each GPU
- * from mh_init() until the process ends (about 1.05 MB): the call allocates
+ * from mh_init() until the process ends (1,252,096 bytes: a 203,520-byte
+ * head of counters, histograms and candidates, and 2^18 floats): the call allocates
  * nothing (no hipMalloc, hipFree or event), for callers that cannot
  * allocate: code under HIP graph capture, tight serving loops, harnesses
  * that forbid allocation. No counterpart in the reference. V is limited to

@@ -7,8 +7,8 @@ wk_row), moe (engine/midge.c's moe / route_topk / expert-major prefill),
 layout (engine/mten.h's expert layout) and synth (seeded inputs).
 """
 from ._lib import (DT_F32, DT_MXFP4, DT_Q4G32, DT_Q8R, LIB_PATH, MidgeHipError, load)
-from .device import DevBuf, Region, init, shutdown, stream, sync
+from .device import DevBuf, Region, init, set_switch, shutdown, stream, switch, sync
 from .layout import ExpertLayout
 
 __all__ = ["DT_F32", "DT_Q8R", "DT_Q4G32", "DT_MXFP4", "LIB_PATH", "MidgeHipError", "load", "DevBuf",
-           "Region", "init", "shutdown", "stream", "sync", "ExpertLayout"]
+           "Region", "init", "set_switch", "shutdown", "stream", "switch", "sync", "ExpertLayout"]

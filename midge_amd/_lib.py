@@ -78,6 +78,7 @@ _SIGS = {
     "mh_shutdown": [],
     "mh_last_error": [],
     "mh_set_stream": [_P],
+    "mh_set_switch": [C.c_char_p, _I],
     "mh_get_stream": [],
     "mh_sync": [],
     "mh_profile_enable": [_I],

@@ -961,6 +961,8 @@ __global__ void __launch_bounds__(kA1Threads) k_attn1(Attn1Args A) {
                 for (int q = 0; q < A.S; ++q) den += s_l[q] * expf(s_m[q] - M);
                 if (A.sinks) den += expf(sinkv - M);
                 const float inv = 1.0f / den;
+                // the head's output into ob (its partials were read above),
+                // published only once every split's words have arrived
                 for (int dm = i; dm < hd; dm += T) {
                     float o = 0.f;
                     for (int q = 0; q < A.S; ++q) {
@@ -976,7 +978,15 @@ __global__ void __launch_bounds__(kA1Threads) k_attn1(Attn1Args A) {
                         }
                         o += tag_val(wo) * expf(s_m[q] - M);
                     }
-                    const float ov = o * inv;
+                    ob[dm] = o * inv;
+                }
+                __syncthreads();
+                if (s_late) {
+                    if (t == 0) raise_err(A.err);
+                    return;
+                }
+                for (int dm = i; dm < hd; dm += T) {
+                    const float ov = ob[dm];
 #pragma unroll
                     for (int cp = 0; cp < kAR; ++cp) st_tag(A.ao + (size_t)cp * A.aos + (size_t)h * hd + dm, tag, ov);
                 }
@@ -1112,14 +1122,14 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
     const int Smax = (cap + kSplitT * kSplitP - 1) / (kSplitT * kSplitP);
     const size_t total_max = total + (size_t)nh * (Smax - S) * (hd + 2) * 4 + 256;
     void *p;
-    MH_TRY(scratch(S_ATTN, total_max, &p));
-    static void *cleared = nullptr;
-    static int cleared_nh = 0;
+    bool fresh = false;
+    MH_TRY(scratch(S_ATTN, total_max, &p, &fresh));
+    static int cleared_nh = 0;   // heads whose counters the slot holds zeroed (0 after a (re)allocation)
+    if (fresh) cleared_nh = 0;
     uint8_t *b8 = (uint8_t *)p;
     unsigned *cnt = (unsigned *)(b8 + oc);
-    if (p != cleared || nh > cleared_nh) {
+    if (nh > cleared_nh) {
         MH_LAUNCH("attn_clear", k_attn_clear, dim3(1), dim3(256), 0, stream(), cnt, nh);
-        cleared = p;
         cleared_nh = nh;
     }
     float *xb = (float *)(b8 + ox), *q = (float *)(b8 + oq), *k = (float *)(b8 + ok), *v = (float *)(b8 + ov);
@@ -1128,15 +1138,14 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
     {
         // the one-launch kernel when its limits hold (int8 projections, the
         // LDS capacities, every head's splits in the grid, one block per CU
-        // resident); MIDGE_HIP_ATTN_SPLIT=1 (read per call) keeps the
-        // separate launches, so callers can compare the two
-        const char *sp = getenv("MIDGE_HIP_ATTN_SPLIT");
+        // resident); the ATTN_SPLIT switch keeps the separate launches, so
+        // callers can compare the two
         const int cus = device_cus(), QR = qd + 2 * kvd;
         const int RQ = (QR + cus - 1) / cus, NB = (QR + RQ - 1) / RQ;
         const int C1 = (int)(H / 32), C3 = qd / 32;
         const int ns1 = C1 >= 1 ? kA1Threads / C1 : 0, ns3 = C3 >= 1 ? kA1Threads / C3 : 0;
         const int RO = (int)((H + NB - 1) / NB), S1 = (nctx + kA1P - 1) / kA1P;
-        bool ok1 = !(sp && sp[0] == '1');
+        bool ok1 = !sw(SW_ATTN_SPLIT);
         for (const DevWT *w : {&wq, &wk, &wv, &wo})
             ok1 = ok1 && w->dt == MH_DT_Q8R && w->scales && (uintptr_t)w->data % 16 == 0;
         ok1 = ok1 && H % 32 == 0 && H <= kA1HMax && qd % 32 == 0 && qd <= kA1QMax && ns1 >= 1 && ns3 >= 1 &&
@@ -1153,13 +1162,8 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
             ok1 = occ >= 1;
         }
         if (ok1) {
-            static unsigned *err = nullptr, *err_dev = nullptr;
-            if (!err) {
-                MH_HIP(hipHostMalloc((void **)&err, sizeof(unsigned), hipHostMallocMapped));
-                *err = 0;
-                MH_HIP(hipHostGetDevicePointer((void **)&err_dev, err, 0));
-                watch_async_error(err, "attention: an exchange timed out (blocks not co-resident)");
-            }
+            unsigned *err_dev = nullptr;
+            MH_TRY(async_flag(F_ATTN1, "attention: an exchange timed out (blocks not co-resident)", &err_dev));
             // exchange words: q/k/v rows, the splits' partials, kAR copies of
             // the attention output (zeroed when the slot is (re)allocated: a
             // launch's tag is never 0 and never repeats)
@@ -1168,15 +1172,20 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos) {
             const size_t words = wqkv + wpart + kAR * aos;
             const size_t words_max = words;
             void *p1;
-            MH_TRY(scratch(S_ATTN1, words_max * 8, &p1));
-            static void *zeroed = nullptr;
+            bool fresh1 = false;
+            MH_TRY(scratch(S_ATTN1, words_max * 8, &p1, &fresh1));
+            // launch tags count up from 1 over words zeroed when the slot is
+            // (re)allocated or grows; before the count could wrap to 0 the
+            // words are zeroed again and the count restarts (a word left
+            // from an older launch then never matches a later tag)
             static size_t zeroed_words = 0;
-            if (p1 != zeroed || words > zeroed_words) {
-                MH_LAUNCH("attn_clear", k_attn_clear, dim3(64), dim3(256), 0, s, (unsigned *)p1, (int)(2 * words_max));
-                zeroed = p1;
-                zeroed_words = words_max;
-            }
             static unsigned tag = 0;
+            if (fresh1) zeroed_words = 0;
+            if (words > zeroed_words || tag >= 0xF0000000u) {
+                MH_LAUNCH("attn_clear", k_attn_clear, dim3(64), dim3(256), 0, s, (unsigned *)p1, (int)(2 * words_max));
+                zeroed_words = words_max;
+                tag = 0;
+            }
             Attn1Args A;
             A.w[0] = (const int8_t *)wq.data;
             A.w[1] = (const int8_t *)wk.data;

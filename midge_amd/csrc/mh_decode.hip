@@ -1445,7 +1445,7 @@ __global__ void k_scan_scales(const uint8_t *experts, uint64_t stride, uint64_t 
 // resident at once (the blocks wait on each other): the plan sizes the grid
 // to at most one block per CU, and the occupancy is checked here (the query
 // once per device and kernel: it costs host time comparable to a small
-// step). A plain launch is the default; MIDGE_HIP_COOP=1 makes it a
+// step). A plain launch is the default; the COOP switch makes it a
 // cooperative launch, whose runtime check of co-residency costs ~18 us of
 // device time per call. A block that were not resident would make the grid's
 // bounded waits time out and report an error through mh_sync, never hang.
@@ -1462,9 +1462,8 @@ int launch_step(const void *k, const Args &A, int nb, hipStream_t s, int *ready_
     void *args[] = {&a};
     const bool prof = profiling();
     if (prof) prof_begin("decode_step", s);
-    const char *coop = getenv("MIDGE_HIP_COOP");
     hipError_t e;
-    if (coop && coop[0] == '1')
+    if (sw(SW_COOP))
         e = hipLaunchCooperativeKernel(k, dim3(nb), dim3(kThreads), args, 0u, s);
     else
         e = hipLaunchKernel(k, dim3(nb), dim3(kThreads), args, 0u, s);
@@ -1805,8 +1804,7 @@ int step_run(StepPlan *p, const DevLayer *layers, int first, int n_layers, float
     if (first < 0 || n_layers < 1 || first + n_layers > p->n_layers)
         return fail(MH_E_ARG, "decode step: layers [%d, %d) outside the plan's %d", first, first + n_layers, p->n_layers);
     const DevLayer &L0 = layers[first];
-    const char *nm = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two kernels
-    const bool grp = p->grp && !(nm && nm[0] && nm[0] != '0');
+    const bool grp = p->grp && !sw(SW_NO_MFMA);
     if (gxb) {
         // routing given: k_decode_grp only, one layer; xb must not overlap x
         // (the combine writes x while other blocks may still read xb)

@@ -532,8 +532,7 @@ int launch_gemm_q8r(const DevWT &w, const float *x, float *y, int batch, hipStre
     if (w.dt != MH_DT_Q8R || batch < 2 || R < 1 || K < 64 || K % 64 != 0 || K > kQ8MaxK || R > (int64_t)INT32_MAX - 4096 ||
         (uintptr_t)w.data % 16 != 0)
         return MH_OK;
-    const char *off = getenv("MIDGE_HIP_NO_MFMA");   // per call, so callers can A/B the two paths
-    if (off && *off && *off != '0') return MH_OK;
+    if (sw(SW_NO_MFMA)) return MH_OK;
     const int groups = (batch + kQ8Cols - 1) / kQ8Cols;
     const int NT = batch > 16 ? 2 : 1;
     const uint64_t qbytes = (uint64_t)groups * (K / 64) * 3 * NT * 1024;
@@ -554,8 +553,7 @@ int launch_gemm_q8r(const DevWT &w, const float *x, float *y, int batch, hipStre
         MH_LAUNCH("gemm_q8r", kern, dim3((unsigned)nb, (unsigned)groups), dim3(threads), 0, s,
                   (const int8_t *)w.data, (const float *)w.scales, xq, sh, x, y, (int)R, (int)K, batch);
     };
-    const char *nl = getenv("MIDGE_HIP_Q8_NO_ROWS");   // per call: A/B against the register-operand kernel
-    if (longm && !(nl && *nl && *nl != '0')) {
+    if (longm && !sw(SW_Q8_NO_ROWS)) {
         // two blocks of 4 waves per CU, each wave 32-row tiles
         const int64_t nb = std::min<int64_t>((R + 31) / 32 / kQ8RowWaves + 1, 2 * (int64_t)device_cus());
         auto go2 = [&](auto kern) {

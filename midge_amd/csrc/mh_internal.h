@@ -54,10 +54,36 @@ void register_owner(void *key, void (*release)(void *));
 void unregister_owner(void *key);
 
 // Library-owned device scratch that grows on demand (slot = purpose id).
-// Contents are not preserved across growth.
+// Contents are not preserved across growth; *fresh (optional) tells whether
+// this call (re)allocated the slot (its contents are then undefined, also
+// when the new allocation lands at an address the slot had before).
 enum Scratch { S_X = 0, S_Y, S_XB, S_H, S_YE, S_RL, S_SEL, S_W, S_PLAN, S_MISC, S_LIST, S_Q, S_XQ, S_ORD, S_SAMPLE, S_ATTN,
                S_ATTN1, S_COUNT };
-int scratch(Scratch slot, uint64_t bytes, void **p);
+int scratch(Scratch slot, uint64_t bytes, void **p, bool *fresh = nullptr);
+
+// Host-mapped error flags owned by the runtime, one per purpose: allocated
+// (zeroed) and watched by mh_sync on first use after mh_init, freed by
+// mh_shutdown. *dev is the device address kernels raise.
+enum AsyncFlag { F_ATTN1 = 0, F_PREFILL_SCALE, F_COUNT };
+int async_flag(AsyncFlag id, const char *msg, unsigned **dev);
+
+// Path switches for comparisons (tests, benchmarks): read once from the
+// environment by mh_init (MIDGE_HIP_<name> set and not "0"), changed at run
+// time by mh_set_switch. Off by default.
+//   NO_MFMA     batched int8 GEMVs, the prefill and the decode step without
+//               the matrix-core kernels
+//   NO_FUSED    stack decode / expert apply as per-layer launches
+//   ATTN_SPLIT  attention as four launches instead of k_attn1
+//   COOP        the one-launch decode step as a cooperative launch
+//   Q8_NO_ROWS  long batched int8 GEMVs on the register-operand kernel
+//   FEW         decode steps of 2-16 tokens on the few-token kernels
+enum Switch { SW_NO_MFMA = 0, SW_NO_FUSED, SW_ATTN_SPLIT, SW_COOP, SW_Q8_NO_ROWS, SW_FEW, SW_COUNT };
+bool sw(Switch s);
+
+// The number of successful mh_init calls so far (never reset): state that a
+// function caches per initialisation (kernel attributes) keeps the value it
+// was set under and redoes its set-up when it differs.
+uint64_t init_epoch();
 
 // Bytes per element class for a tensor view.
 int wt_bytes(int dt, int64_t rows, int64_t cols, uint64_t *data_bytes, uint64_t *scale_bytes);

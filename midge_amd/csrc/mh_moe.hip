@@ -474,7 +474,7 @@ int run_router(const DevLayer &L, const float *x, int n, int unfilled, const Lay
 
 // few: the layer's MXFP4 scales are known to be f16-exact (a stack's plan
 // scanned them), so 2-16 tokens may take the few-token matrix-core kernels
-// when MIDGE_HIP_FEW=1 (opt-in: at 16 tokens of gpt-oss-120b they are
+// under the FEW switch (opt-in: at 16 tokens of gpt-oss-120b they are
 // slower than the per-assignment GEMVs, 7.3 vs 6.05 ms per step, being
 // bound by the e2m1 -> f16 conversion at one wave per SIMD).
 // have_xb: b.xb holds this layer's normed input already; next: the next
@@ -482,8 +482,7 @@ int run_router(const DevLayer &L, const float *x, int n, int unfilled, const Lay
 int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uint32_t *usage, hipStream_t s,
                      bool few = false, bool have_xb = false, const DevLayer *next = nullptr) {
     MH_TRY(run_router(L, have_xb ? nullptr : x, n, -1, b, usage, b.order, s));
-    const char *fe = getenv("MIDGE_HIP_FEW");
-    if (few && b.order && fe && *fe && *fe != '0' && fewtok_ok(L, n))
+    if (few && b.order && sw(SW_FEW) && fewtok_ok(L, n))
         MH_TRY(launch_fewtok(L, n, b.order, b.xb, b.h, b.ye, s));
     else
         MH_TRY(launch_experts(L, n * L.top_k, b.sel, b.order, b.xb, b.h, b.ye, s));
@@ -603,8 +602,7 @@ namespace mh {
 // usage (device [E]) are this layer's rows, or null.
 int stack_decode_layer(mh_stack *st, int l, float *x, int32_t *sel, float *w, uint32_t *usage) {
     hipStream_t s = stream();
-    const char *nf = getenv("MIDGE_HIP_NO_FUSED");
-    if (!(nf && *nf && *nf != '0') && step_plan_ok(st->plan)) {
+    if (!sw(SW_NO_FUSED) && step_plan_ok(st->plan)) {
         int rc = step_run(st->plan, st->layers.data(), l, 1, x, sel, w, usage, s);
         if (rc != MH_E_UNSUPPORTED) return rc;
         clear_error();
@@ -780,8 +778,7 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
     if (w) MH_TRY(resolve_dev(w, (uint64_t)nl * batch * k * 4, "mh_stack_decode w"));
     if (usage) MH_TRY(resolve_dev(usage, (uint64_t)nl * L0.n_experts * 4, "mh_stack_decode usage"));
     hipStream_t s = stream();
-    const char *nf = getenv("MIDGE_HIP_NO_FUSED");   // per call, so callers can A/B the two paths
-    if (batch == 1 && !(nf && *nf && *nf != '0') && step_plan_ok(st->plan)) {
+    if (batch == 1 && !sw(SW_NO_FUSED) && step_plan_ok(st->plan)) {
         int rc = step_run(st->plan, st->layers.data(), 0, nl, x, sel, w, usage, s);
         if (rc != MH_E_UNSUPPORTED) return rc;
         clear_error();   // shape this device cannot run in one launch: per-layer launches below
@@ -813,8 +810,7 @@ int mh_stack_apply_dev(mh_stack *st, int layer, const float *xb, const int32_t *
     MH_TRY(resolve_dev(w, (uint64_t)L.top_k * 4, "mh_stack_apply_dev w"));
     MH_TRY(resolve_dev(x, (uint64_t)L.hidden * 4, "mh_stack_apply_dev x"));
     hipStream_t s = stream();
-    const char *nf = getenv("MIDGE_HIP_NO_FUSED");   // per call, so callers can A/B the two paths
-    if (!(nf && *nf && *nf != '0') && step_plan_ok(st->plan)) {
+    if (!sw(SW_NO_FUSED) && step_plan_ok(st->plan)) {
         int rc = step_run(st->plan, st->layers.data(), layer, 1, x, nullptr, nullptr, nullptr, s, xb, sel, w);
         if (rc != MH_E_UNSUPPORTED) return rc;
         clear_error();   // per-layer launches below

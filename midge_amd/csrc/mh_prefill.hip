@@ -515,9 +515,6 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
     if (bad) atomicOr(A.err, 1u);
 }
 
-unsigned *g_scale_err = nullptr;       // host-mapped flag
-unsigned *g_scale_err_dev = nullptr;
-
 }  // namespace
 
 // Assignments grouped by expert (offsets[E + 1], token and slot of each list
@@ -537,8 +534,7 @@ int launch_expert_lists(const int32_t *sel, int N, int E, int k, ExpertLists *ou
 // True when the scaled-MFMA path handles this layer (MXFP4 experts, shapes
 // that tile by 64 along K and 32 along rows, whose scales fit the GEMM's LDS).
 bool prefill_mfma_ok(const DevLayer &L) {
-    const char *off = getenv("MIDGE_HIP_NO_MFMA");
-    if (off && off[0] && off[0] != '0') return false;
+    if (sw(SW_NO_MFMA)) return false;
     return L.expert_dt == MH_DT_MXFP4 && L.hidden % 64 == 0 && L.ffn % 64 == 0 && L.top_k >= 1 &&
            L.n_experts <= kPlistMaxE && L.hidden <= INT32_MAX && L.ffn <= INT32_MAX &&
            gemm_lds((int)L.hidden, 2).total <= kLdsMax && gemm_lds((int)L.ffn, 1).total <= kLdsMax;
@@ -553,18 +549,15 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
     const int H = (int)L.hidden, F = (int)L.ffn;
     if (!prefill_mfma_ok(L)) return fail(MH_E_UNSUPPORTED, "prefill: layer shape not handled by the MFMA path");
     const size_t lds_gu = gemm_lds(H, 2).total, lds_dn = gemm_lds(F, 1).total;
-    static bool lds_set = false;
-    if (!lds_set) {
+    static uint64_t lds_epoch = 0;   // the initialisation the LDS attribute was set under
+    if (lds_epoch != init_epoch()) {
         MH_HIP(hipFuncSetAttribute((const void *)k_moe_gemm<0>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax));
         MH_HIP(hipFuncSetAttribute((const void *)k_moe_gemm<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax));
-        lds_set = true;
+        lds_epoch = init_epoch();
     }
-    if (!g_scale_err) {
-        MH_HIP(hipHostMalloc((void **)&g_scale_err, sizeof(unsigned), hipHostMallocMapped));
-        *g_scale_err = 0;
-        MH_HIP(hipHostGetDevicePointer((void **)&g_scale_err_dev, g_scale_err, 0));
-        watch_async_error(g_scale_err, "prefill: an MXFP4 scale is not a positive power of two (e8m0 cannot hold it)");
-    }
+    unsigned *scale_err_dev = nullptr;
+    MH_TRY(async_flag(F_PREFILL_SCALE, "prefill: an MXFP4 scale is not a positive power of two (e8m0 cannot hold it)",
+                      &scale_err_dev));
     ExpertLists lists;
     MH_TRY(launch_expert_lists(sel, N, E, k, &lists, s));
     const int *offs = lists.offs, *list_tok = lists.list_tok, *slot_of = lists.slot_of;
@@ -594,7 +587,7 @@ int run_expert_major_mfma(const DevLayer &L, int n, const float *xb, const int32
     A.slot_of = slot_of;
     A.hbuf = hbuf;
     A.ye = ye;
-    A.err = g_scale_err_dev;
+    A.err = scale_err_dev;
 
     // gate/up over the quantized tokens
     {

@@ -45,9 +45,24 @@ struct State {
     uint64_t cap = 0;                       // 0 = no cap
     void *scratch[S_COUNT] = {};
     uint64_t scratch_bytes[S_COUNT] = {};
+    unsigned *flag_host[F_COUNT] = {};      // async_flag: host-mapped pinned words
+    unsigned *flag_dev[F_COUNT] = {};
 };
 
 State g;
+uint64_t g_epoch = 0;   // successful mh_init calls
+
+// Path switches (sw, mh_set_switch), read from the environment by mh_init.
+const char *const kSwitchNames[SW_COUNT] = {"NO_MFMA", "NO_FUSED", "ATTN_SPLIT", "COOP", "Q8_NO_ROWS", "FEW"};
+bool g_sw[SW_COUNT] = {};
+void read_switches() {
+    char name[64];
+    for (int i = 0; i < SW_COUNT; i++) {
+        snprintf(name, sizeof(name), "MIDGE_HIP_%s", kSwitchNames[i]);
+        const char *v = getenv(name);
+        g_sw[i] = v && v[0] && v[0] != '0';
+    }
+}
 
 // Host-mapped error flags of asynchronous work (checked by mh_sync).
 std::vector<std::pair<unsigned *, const char *>> g_async;
@@ -280,11 +295,35 @@ int resolve_wt(const mh_wt *t, DevWT *out, const char *what) {
     return MH_OK;
 }
 
-int scratch(Scratch slot, uint64_t bytes, void **p) {
+uint64_t init_epoch() { return g_epoch; }
+
+bool sw(Switch s) { return g_sw[s]; }
+
+int async_flag(AsyncFlag id, const char *msg, unsigned **dev) {
+    if (!g.flag_host[id]) {
+        unsigned *h = nullptr, *d = nullptr;
+        MH_HIP(hipHostMalloc((void **)&h, sizeof(unsigned), hipHostMallocMapped));
+        *h = 0;
+        const hipError_t e = hipHostGetDevicePointer((void **)&d, h, 0);
+        if (e != hipSuccess) {
+            (void)hipHostFree(h);
+            return hip_check(e, "hipHostGetDevicePointer (error flag)");
+        }
+        g.flag_host[id] = h;
+        g.flag_dev[id] = d;
+        watch_async_error(h, msg);
+    }
+    *dev = g.flag_dev[id];
+    return MH_OK;
+}
+
+int scratch(Scratch slot, uint64_t bytes, void **p, bool *fresh) {
+    if (fresh) *fresh = false;
     if (bytes <= g.scratch_bytes[slot] && g.scratch[slot]) {
         *p = g.scratch[slot];
         return MH_OK;
     }
+    if (fresh) *fresh = true;
     if (g.scratch[slot]) {
         MH_HIP(hipStreamSynchronize(g.cur));
         MH_HIP(hipFree(g.scratch[slot]));
@@ -332,6 +371,8 @@ int mh_init(int device) {
     g.cus = prop.multiProcessorCount;
     g.cap = env_cap();
     g.inited = true;
+    ++g_epoch;
+    read_switches();
     const int rc = sample_static_setup(device);
     if (rc) {
         (void)hipStreamDestroy(g.own);
@@ -352,6 +393,8 @@ int mh_shutdown(void) {
         o.release(o.key);
     }
     g_async.clear();
+    for (int i = 0; i < F_COUNT; i++)
+        if (g.flag_host[i]) (void)hipHostFree(g.flag_host[i]);
     for (auto &r : g.regions) (void)hipFree(r.second.dev);
     g.regions.clear();
     g.region_dev.clear();
@@ -392,6 +435,17 @@ int mh_profile_query(const char *name, double *total_ms, uint64_t *launches) {
     *total_ms = it == g_prof_done.end() ? 0.0 : it->second.first;
     *launches = it == g_prof_done.end() ? 0 : it->second.second;
     return MH_OK;
+}
+
+int mh_set_switch(const char *name, int on) {
+    clear_error();
+    if (!name) return fail(MH_E_ARG, "mh_set_switch: NULL name");
+    for (int i = 0; i < SW_COUNT; i++)
+        if (strcmp(name, kSwitchNames[i]) == 0) {
+            g_sw[i] = on != 0;
+            return MH_OK;
+        }
+    return fail(MH_E_ARG, "mh_set_switch: unknown switch '%s'", name);
 }
 
 int mh_set_stream(void *s) {

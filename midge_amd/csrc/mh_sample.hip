@@ -96,6 +96,7 @@ struct SampWs {
     alignas(16) float p[4];         // [V] (only when radix; 16-byte aligned for the block scans)
 };
 constexpr uint64_t kWsHead = offsetof(SampWs, p);
+static_assert(kWsHead == 203520, "the workspace head size the headers state");
 
 // device-scope stores and loads of data that other blocks of the same
 // launch read (no cache on the way can hold a stale copy)
@@ -960,12 +961,11 @@ __global__ void k_samp_clear(uint32_t *w, int n) {
 // (re)allocated (a fill kernel, so that a caller's graph capture records no
 // memset node).
 int sample_scratch(uint64_t bytes, void **ws) {
-    static void *cleared = nullptr;
-    MH_TRY(scratch(S_SAMPLE, bytes, ws));
-    if (*ws != cleared) {
+    bool fresh = false;
+    MH_TRY(scratch(S_SAMPLE, bytes, ws, &fresh));
+    if (fresh) {
         MH_LAUNCH("sample_clear", k_samp_clear, dim3(8), dim3(256), 0, stream(), (uint32_t *)*ws, (int)(kWsHead / 4));
         MH_TRY(hip_check(hipGetLastError(), "sample workspace clear"));
-        cleared = *ws;
     }
     return MH_OK;
 }
@@ -1002,7 +1002,9 @@ int sample_launch(const float *logits, int V, float temp, float topp, float u, v
 // ------------------------------------------ the fixed, allocation-free workspace
 
 // Vocabularies up to 2^18 tokens (gpt-oss: 201088) fit the fixed workspace:
-// about 1.05 MB of device memory per GPU, held until the process ends.
+// 1,252,096 bytes of device memory per GPU (the 203,520-byte head: block
+// maxima, f64 sums, two 64 x 328 histograms, counters and 8192 candidates;
+// then 2^18 floats of p), held until the process ends.
 constexpr int64_t kStaticMaxV = 1 << 18;
 static __device__ __align__(256) uint8_t samp_static_ws[kWsHead + kStaticMaxV * 4];
 

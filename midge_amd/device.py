@@ -32,6 +32,27 @@ def stream() -> int:
     return _lib.raw("mh_get_stream")() or 0
 
 
+def set_switch(name: str, on: bool) -> None:
+    """mh_set_switch: a path switch ("NO_MFMA", "NO_FUSED", "ATTN_SPLIT",
+    "COOP", "Q8_NO_ROWS") on or off for the calls that follow."""
+    _lib.call("mh_set_switch", name.encode(), 1 if on else 0)
+
+
+class switch:
+    """`with switch("NO_FUSED"):` runs the block with a path switch on."""
+
+    def __init__(self, name: str, on: bool = True):
+        self.name, self.on = name, on
+
+    def __enter__(self):
+        set_switch(self.name, self.on)
+        return self
+
+    def __exit__(self, *exc):
+        set_switch(self.name, not self.on)
+        return False
+
+
 def profile_enable(on: bool = True) -> None:
     _lib.call("mh_profile_enable", 1 if on else 0)
 

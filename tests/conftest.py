@@ -25,6 +25,22 @@ def mh():
     midge_amd.sync()
 
 
+@pytest.fixture
+def path_switch(mh):
+    """set(name, on): a library path switch (mh_set_switch) for this test;
+    every switch it touched is turned off again at teardown."""
+    from midge_amd import set_switch
+    used = []
+
+    def set_(name: str, on: bool = True) -> None:
+        set_switch(name, on)
+        used.append(name)
+
+    yield set_
+    for n in used:
+        set_switch(n, False)
+
+
 def rel_l2(a, b) -> float:
     a = np.asarray(a, np.float64).ravel()
     b = np.asarray(b, np.float64).ravel()

@@ -2,7 +2,7 @@
 oracle: exact dequantization, GEMVs of every dtype, batched GEMVs, the
 fallback path, and the device synthetic generators."""
 import ctypes as C
-
+import os
 import zlib
 
 import numpy as np
@@ -10,7 +10,7 @@ import pytest
 
 import make_golden as mg
 from conftest import rel_l2, say
-from midge_amd import DT_F32, DT_MXFP4, DT_Q4G32, DT_Q8R, DevBuf, synth
+from midge_amd import DT_F32, DT_MXFP4, DT_Q4G32, DT_Q8R, DevBuf, switch, synth
 from midge_amd.kern import WT, dequant_dev, matvec_dev, rmsnorm_dev, wk_matvec, wk_row
 from oracle import pyoracle as po
 from test_oracle_kernels import closed_form_dequant, make_tensor, pow2_f16
@@ -173,8 +173,8 @@ def test_matvec_dev_q8r_batched_nonfinite(mh):
             assert rel_l2(Y[b][fin], want[fin]) < 1e-5, b
 
 
-def test_matvec_dev_q8r_batched_paths_agree(mh, monkeypatch):
-    # the matrix-core path and the per-column GEMV (MIDGE_HIP_NO_MFMA=1)
+def test_matvec_dev_q8r_batched_paths_agree(mh):
+    # the matrix-core path and the per-column GEMV (the NO_MFMA switch)
     rows, cols, batch = 4096, 2880, 8
     say(f"matvec_dev q8r batched vs per-column {rows}x{cols} batch={batch}")
     data, sc = make_tensor(DT_Q8R, rows, cols, rng=RNG)
@@ -183,8 +183,8 @@ def test_matvec_dev_q8r_batched_paths_agree(mh, monkeypatch):
     xd, y1, y2 = DevBuf.from_array(X), DevBuf(batch * rows * 4), DevBuf(batch * rows * 4)
     t = WT(DT_Q8R, rows, cols, wd.ptr, sd.ptr)
     matvec_dev(t, xd, y1, batch)
-    monkeypatch.setenv("MIDGE_HIP_NO_MFMA", "1")
-    matvec_dev(t, xd, y2, batch)
+    with switch("NO_MFMA"):
+        matvec_dev(t, xd, y2, batch)
     a, b = y1.download(np.float32, (batch, rows)), y2.download(np.float32, (batch, rows))
     for d in (wd, sd, xd, y1, y2):
         d.free()
@@ -453,52 +453,23 @@ LONG_ATTN_SHAPES = {
 
 @pytest.mark.parametrize("path", ["one_launch", "split"])
 @pytest.mark.parametrize("name", ["small_sliding_sinks", "small_full_qknorm", "gpt_oss", *LONG_ATTN_SHAPES])
-def test_attention_dev_vs_oracle(mh, name, path, monkeypatch):
+def test_attention_dev_vs_oracle(mh, name, path, path_switch):
     # attention() for a run of decode positions (past the sliding window, so
     # the ring wraps): the device x and f16 caches against the oracle's
     # (bit-exact with the reference's scalar attention on the CPU), through
     # the one-launch kernel (int8 projections) and the separate launches
-    # (MIDGE_HIP_ATTN_SPLIT=1)
+    # (the ATTN_SPLIT switch)
     import ctypes
-    if path == "split":
-        monkeypatch.setenv("MIDGE_HIP_ATTN_SPLIT", "1")
-    else:
-        monkeypatch.delenv("MIDGE_HIP_ATTN_SPLIT", raising=False)
+    path_switch("ATTN_SPLIT", path == "split")
     from test_oracle_kernels import ATTN_DIV_FIXTURE, ATTN_SHAPES, GPT_OSS_ATTN, GPT_OSS_ROPE, AttnHost
     from midge_amd import _lib
     cfgs = dict(ATTN_SHAPES, gpt_oss=GPT_OSS_ATTN, **LONG_ATTN_SHAPES)
     cfg = cfgs[name]
     say(f"attention_dev {name}")
     host = AttnHost(**cfg, seed=13, rope=GPT_OSS_ROPE if name == "gpt_oss" else None)
-    L = host.L
-    bufs = []
-
-    def dev(ptr, nbytes):
-        a = np.ctypeslib.as_array(ctypes.cast(ptr, ctypes.POINTER(ctypes.c_uint8)), (nbytes,)).copy()
-        d = DevBuf.from_array(a)
-        bufs.append(d)
-        return d.ptr
-
-    H, nh, nkv, hd = cfg["hidden"], cfg["nh"], cfg["nkv"], cfg["hd"]
-    qd, kvd = nh * hd, nkv * hd
-    D = _lib.MhAttnLayer()
-    for f, _ in po.MhAttnLayer._fields_:
-        if f not in ("wq", "wk", "wv", "wo"):
-            setattr(D, f, getattr(L, f))
-    for f in ("wq", "wk", "wv", "wo"):
-        w = getattr(L, f)
-        setattr(D, f, _lib.MhWT(w.dt, w.rows, w.cols, dev(w.data, w.rows * w.cols), dev(w.scales, w.rows * 4)))
-    for f, n in (("bq", qd), ("bk", kvd), ("bv", kvd), ("bo", H), ("attn_norm", H)):
-        setattr(D, f, dev(getattr(L, f), n * 4))
-    if cfg["qk_norm"]:
-        D.qn, D.kn = dev(L.qn, hd * 4), dev(L.kn, hd * 4)
-    if cfg["sinks"]:
-        D.sink = dev(L.sink, nh * 4)
-    D.rope_cos, D.rope_sin = dev(L.rope_cos, host.co.nbytes), dev(L.rope_sin, host.si.nbytes)
-    kc_d = DevBuf.from_array(np.zeros_like(host.kc))
-    vc_d = DevBuf.from_array(np.zeros_like(host.vc))
-    bufs += [kc_d, vc_d]
-    D.kc, D.vc = kc_d.ptr, vc_d.ptr
+    from attn_dev import attn_device_layer
+    H = cfg["hidden"]
+    D, bufs, kc_d, vc_d = attn_device_layer(host, cfg)
     rng = np.random.default_rng(14)
     xd = DevBuf(H * 4)
     bufs.append(xd)
@@ -557,3 +528,18 @@ def test_attention_dev_vs_oracle(mh, name, path, monkeypatch):
             <= 2.0 ** -10 * np.abs(w.view(np.float16).astype(np.float32)).max()
     for d in bufs:
         d.free()
+
+
+def test_reinit_attention_and_sampling():
+    # mh_shutdown then mh_init: attention's exchange words and error flag and
+    # the sampler's workspace counters are set up again for the new
+    # initialisation (the scratch can come back at the same address). In a
+    # child process: this session's library holds live buffers.
+    import subprocess
+    import sys
+    say("reinit: attention and sampling across mh_shutdown / mh_init (child process)")
+    r = subprocess.run([sys.executable, "-u", os.path.join(os.path.dirname(os.path.abspath(__file__)), "reinit_case.py")],
+                       capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "reinit ok" in r.stdout
+

@@ -6,7 +6,7 @@ import pytest
 
 import make_golden as mg
 from conftest import rel_l2, say
-from midge_amd import DevBuf, _lib, synth
+from midge_amd import DevBuf, _lib, set_switch, synth
 from midge_amd.moe import MoELayer, Stack, expert_major_dev, moe, moe_dev, moe_prefill, moe_prefill_dev, topk_dev
 from midge_amd.synth import Keys, MoEShape
 from oracle import pyoracle as po
@@ -37,15 +37,13 @@ _LIVE: list = []
 
 
 @pytest.fixture(params=["mfma", "gemv"])
-def prefill_path(request, monkeypatch):
+def prefill_path(request, mh):
     """The expert-major prefill runs the scaled-MFMA grouped GEMM for MXFP4
-    experts; MIDGE_HIP_NO_MFMA=1 selects the per-assignment GEMV kernels.
+    experts; the NO_MFMA switch selects the per-assignment GEMV kernels.
     Both must match the oracle."""
-    if request.param == "gemv":
-        monkeypatch.setenv("MIDGE_HIP_NO_MFMA", "1")
-    else:
-        monkeypatch.delenv("MIDGE_HIP_NO_MFMA", raising=False)
-    return request.param
+    set_switch("NO_MFMA", request.param == "gemv")
+    yield request.param
+    set_switch("NO_MFMA", False)
 
 
 @pytest.fixture(autouse=True)
@@ -339,7 +337,7 @@ def test_stack_fused_step_vs_per_layer_and_oracle(mh, shape, layers):
         out = {}
         for mode in ("fused", "per_layer"):
             if mode == "per_layer":
-                os.environ["MIDGE_HIP_NO_FUSED"] = "1"
+                set_switch("NO_FUSED", True)
             try:
                 xd = DevBuf.from_array(x0)
                 sd = DevBuf(layers * k * 4)
@@ -351,7 +349,7 @@ def test_stack_fused_step_vs_per_layer_and_oracle(mh, shape, layers):
                 for d in (xd, sd, ud):
                     d.free()
             finally:
-                os.environ.pop("MIDGE_HIP_NO_FUSED", None)
+                set_switch("NO_FUSED", False)
         xf, sf, uf = out["fused"]
         xp, sp, up = out["per_layer"]
         assert (sf == sp).all(), (sf, sp)
@@ -371,7 +369,7 @@ def test_stack_fused_step_vs_per_layer_and_oracle(mh, shape, layers):
         got = {}
         for mode in ("fused", "per_layer"):
             if mode == "per_layer":
-                os.environ["MIDGE_HIP_NO_FUSED"] = "1"
+                set_switch("NO_FUSED", True)
             try:
                 xd, sd = DevBuf.from_array(x[None, :]), DevBuf(k * 4)
                 one.decode(xd, 1, sd)
@@ -380,13 +378,54 @@ def test_stack_fused_step_vs_per_layer_and_oracle(mh, shape, layers):
                 xd.free()
                 sd.free()
             finally:
-                os.environ.pop("MIDGE_HIP_NO_FUSED", None)
+                set_switch("NO_FUSED", False)
         one.destroy()
         for mode, (xg, sg) in got.items():
             assert (sg == selr).all(), (l, mode, sg, selr)
         assert rel_l2(got["fused"][0], got["per_layer"][0]) < SPLIT_TOL, l
         assert rel_l2(got["fused"][0], xo) < TOL, l
         x = xo
+
+
+@pytest.mark.parametrize("n_experts", [32, 128], ids=["gptoss20b", "gptoss120b"])
+def test_stack_multilayer_launch_y_words(mh, n_experts):
+    """A launch of several layers passes y between its blocks as 32-bit
+    words: the f32 rounded to a multiple of 16 units in the last place
+    (within 2^-20 relative) with a 4-bit tag in the low bits, both inside
+    the launch and into the last layer's combine. One-layer launches, which
+    the per-layer bar SPLIT_TOL holds elsewhere, pass full f32 words. Here a
+    2-layer launch (device-generated experts at the gpt-oss shape) against
+    the per-layer kernels (full f32 everywhere) on the same inputs: the same
+    experts in both layers, and x after the two layers within twice the
+    per-layer bar widened by the words' own rounding, 2 (SPLIT_TOL + 2^-20)
+    (measured: up to 4.7e-6 at 128 experts)."""
+    shape = MoEShape(hidden=2880, ffn=2880, n_experts=n_experts, top_k=4, n_layers=2)
+    say(f"2-layer launch vs per-layer kernels, E={n_experts}")
+    st, bufs, keys = Stack.synthetic(shape, 91 + n_experts, 1)
+    k = shape.top_k
+    worst = 0.0
+    for step in range(8):
+        x0 = synth.host_x(shape, keys, 1, step=step)
+        out = {}
+        for mode in ("fused", "per_layer"):
+            set_switch("NO_FUSED", mode == "per_layer")
+            try:
+                xd, sd = DevBuf.from_array(x0), DevBuf(2 * k * 4)
+                st.decode(xd, 1, sd)
+                mh.sync()
+                out[mode] = (xd.download(np.float32, x0.shape)[0], sd.download(np.int32, (2, k)))
+                xd.free()
+                sd.free()
+            finally:
+                set_switch("NO_FUSED", False)
+        assert (out["fused"][1] == out["per_layer"][1]).all(), (step, out["fused"][1], out["per_layer"][1])
+        err = rel_l2(out["fused"][0], out["per_layer"][0])
+        worst = max(worst, err)
+        assert err < 2 * (SPLIT_TOL + 2.0 ** -20), (step, err)
+    say(f"2-layer launch E={n_experts}: worst rel L2 {worst:.3g} against the per-layer kernels")
+    st.destroy()
+    for d in bufs:
+        d.free()
 
 
 @pytest.mark.parametrize("shape", [
@@ -421,7 +460,7 @@ def test_stack_apply_vs_expert_major_and_oracle(mh, shape):
         out = {}
         for mode in ("fused", "per_layer"):
             if mode == "per_layer":
-                os.environ["MIDGE_HIP_NO_FUSED"] = "1"
+                set_switch("NO_FUSED", True)
             try:
                 bufs = [DevBuf.from_array(a) for a in (xb, sel, wv, x0)]
                 st.apply(0, *bufs)
@@ -430,7 +469,7 @@ def test_stack_apply_vs_expert_major_and_oracle(mh, shape):
                 for d in bufs:
                     d.free()
             finally:
-                os.environ.pop("MIDGE_HIP_NO_FUSED", None)
+                set_switch("NO_FUSED", False)
         want = po.expert_major_apply(L, xb[None], sel[None], wv[None], x0[None])[0]
         if (sel < 0).all():
             assert np.array_equal(out["fused"], x0) and np.array_equal(out["per_layer"], x0)
@@ -509,7 +548,7 @@ def test_stack_batch_few_token_kernels(mh, shape, batch, case):
     out = {}
     for mode in ("few", "gemv"):
         if mode == "few":
-            os.environ["MIDGE_HIP_FEW"] = "1"
+            set_switch("FEW", True)
         try:
             xd, sd = DevBuf.from_array(x0), DevBuf(batch * k * 4)
             st.decode(xd, batch, sd)
@@ -518,7 +557,7 @@ def test_stack_batch_few_token_kernels(mh, shape, batch, case):
             xd.free()
             sd.free()
         finally:
-            os.environ.pop("MIDGE_HIP_FEW", None)
+            set_switch("FEW", False)
     st.destroy()
     xf, sf = out["few"]
     xg, sg = out["gemv"]
@@ -570,7 +609,7 @@ def test_stack_fused_step_variants(mh, variant, path):
         _LIVE.append(lays[-1])
         structs.append(po.layer_struct(shape, ex, w, s, b, nw))
     if path == "valu":
-        os.environ["MIDGE_HIP_NO_MFMA"] = "1"
+        set_switch("NO_MFMA", True)
     try:
         st = Stack(lays, max_batch=1)
         k = shape.top_k
@@ -591,7 +630,7 @@ def test_stack_fused_step_variants(mh, variant, path):
             assert rel_l2(xf, x) < TOL, (step, rel_l2(xf, x))
         st.destroy()
     finally:
-        os.environ.pop("MIDGE_HIP_NO_MFMA", None)
+        set_switch("NO_MFMA", False)
 
 
 def test_stack_fused_step_ties_and_unfilled_slots(mh):
@@ -623,7 +662,7 @@ def test_stack_fused_step_ties_and_unfilled_slots(mh):
     out = {}
     for mode in ("fused", "per_layer"):
         if mode == "per_layer":
-            os.environ["MIDGE_HIP_NO_FUSED"] = "1"
+            set_switch("NO_FUSED", True)
         try:
             xd = DevBuf.from_array(x0)
             sd, wd = DevBuf(3 * k * 4), DevBuf(3 * k * 4)
@@ -634,7 +673,7 @@ def test_stack_fused_step_ties_and_unfilled_slots(mh):
             for d in (xd, sd, wd):
                 d.free()
         finally:
-            os.environ.pop("MIDGE_HIP_NO_FUSED", None)
+            set_switch("NO_FUSED", False)
     st.destroy()
     xf, sf, wf = out["fused"]
     xp, sp, wp = out["per_layer"]

@@ -1,7 +1,12 @@
 """mh_sample_dev_static (the allocation-free sampling entry point) against
 mh_sample_dev through the C ABI: two calls in a row, the second over a
 smaller vocabulary, on every selection path (greedy, the candidate sort,
-the radix select over the whole vocabulary)."""
+the radix select over the whole vocabulary); and, in a fresh process, that
+it allocates nothing when it runs before anything else has sampled."""
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 
@@ -29,3 +34,14 @@ def test_sample_static_matches_sample_dev(mh, spread):
         ld.free()
     out_a.free()
     out_b.free()
+
+
+def test_sample_static_allocates_nothing():
+    # a child process: a fresh initialisation, the static entry point first,
+    # under a one-byte allocation cap
+    say("sample_dev_static first in a fresh process under MIDGE_HIP_MAX_BYTES=1")
+    r = subprocess.run([sys.executable, "-u", os.path.join(os.path.dirname(os.path.abspath(__file__)), "no_alloc_case.py")],
+                       capture_output=True, text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "no-alloc ok" in r.stdout
+
