@@ -216,6 +216,8 @@ def run_gpu(args, shape):
         extra["lm_head_sample"] = lm_head_sample_probe(ev, s)
         extra["attention"] = attention_probe(ev, s)
         extra["full_token"] = full_token_probe(ev, s, st, shape)
+    if not args.no_engine:
+        extra["engine_host"] = engine_host_probe()
     for b in bufs:
         b.free()
     st.destroy()
@@ -632,6 +634,61 @@ def reference_bench(ev, s, seconds: float = 1.0) -> dict:
     return out
 
 
+def engine_host_probe(n_gen: int = 384) -> dict:
+    """The reference engine's own host (its protocol, forward, forward_batch,
+    sample; engine/midge.c:552-622, 654-679, 790-831), built from its sources
+    three ways, decoding on a 4-layer model at gpt-oss's layer shapes (32
+    MXFP4 experts 2880x2880, int8 attention and router, vocab 8192) written
+    to a temporary directory by the tests' model writer:
+      cpu          oracle/_ref/midged: the engine on its CPU kernels
+      kernel_level oracle/_ref/midged_hip: every wk_matvec / wk_row through
+                   the drop-in header (host activations, a GEMV round trip
+                   per projection)
+      layer_level  oracle/_ref/midged_hip_layer: the containers resident in
+                   HBM, forward() one mh_forward_dev call per token (device
+                   attention, the one-launch MoE kernel per layer, lm_head),
+                   sample() on the device logits
+    Greedy decode tok/s from the engine's own DONE line (its timer around the
+    gen loop), after a 16-token prefill; the layer level also at temperature
+    0.8 / top-p 0.9 (set: ... seed 5)."""
+    import shutil
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import engine_model as em
+    out = {"workload": "4-layer gpt-oss-shaped model (32 MXFP4 experts, int8 attention/router, vocab 8192), "
+                       f"16-token prefill then {n_gen} generated tokens; tok/s from the engine's DONE line"}
+    d = tempfile.mkdtemp(prefix="midge_engine_")
+    try:
+        sp = em.write_model(d, n_layers=4)
+        ids = " ".join(map(str, em.prompt(16, sp["vocab"], seed=9)))
+        greedy = f"ids: {ids}\ngen: {n_gen}\nquit\n"
+        sampled = f"set: 0.8 0.9 5\nids: {ids}\ngen: {n_gen}\nquit\n"
+        runs = [("cpu", "midged", greedy), ("kernel_level", "midged_hip", greedy),
+                ("layer_level", "midged_hip_layer", greedy), ("layer_level_sampled", "midged_hip_layer", sampled),
+                ("cpu_sampled", "midged", sampled)]
+        toks = {}
+        for key, exe, script in runs:
+            path = os.path.join(ROOT, "oracle", "_ref", exe)
+            if not os.path.exists(path):
+                out[key] = None
+                continue
+            log(f"engine host: {key}")
+            _, t, done, _ = em.run_engine(path, d, script, ctx=512, timeout=300)
+            gen = [x for x in done if x[1] > 0]
+            toks[key] = t
+            out[key] = {"tok_per_s": gen[-1][1] / gen[-1][2], "generated": int(gen[-1][1]),
+                        "seconds": gen[-1][2]} if gen else {"error": "no DONE line"}
+        if "cpu" in toks and "layer_level" in toks:
+            out["greedy_tokens_equal"] = toks["cpu"] == toks["layer_level"] == toks.get("kernel_level", toks["cpu"])
+        if "cpu_sampled" in toks and "layer_level_sampled" in toks:
+            out["sampled_tokens_equal"] = toks["cpu_sampled"] == toks["layer_level_sampled"]
+        if out.get("cpu") and out.get("layer_level"):
+            out["layer_level_vs_cpu"] = out["layer_level"]["tok_per_s"] / out["cpu"]["tok_per_s"]
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return out
+
+
 def config_probes(ev, s, seed: int, reps: int = 20) -> dict:
     """Configurations 0-2 of the measurement plan beside the headline (cfg 4)
     and the prefill (cfg 3), each with synthetic device-generated inputs:
@@ -895,6 +952,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the expert-major prefill measurement")
     ap.add_argument("--no-refbench", action="store_true", help="skip the reference's run_bench figure")
     ap.add_argument("--no-configs", action="store_true", help="skip the configuration 0-2 measurements")
+    ap.add_argument("--no-engine", action="store_true", help="skip the reference engine's host on the library")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device twice (byte-counter calibration)")

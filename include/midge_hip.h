@@ -206,11 +206,15 @@ int mh_sample_dev_static(const float *logits, int64_t V, float temp, float topp,
  * router, stable top-k, routing weights, the routed experts' clamped-SwiGLU
  * FFNs, weighted sum in selection order and the residual add. Replaces
  * moe() (engine/midge.c:469-549). sel[top_k] / w[top_k] (host, may be NULL)
- * receive the routing for the caller's usage bookkeeping (midge.c:517-518). */
+ * receive the routing for the caller's usage bookkeeping (midge.c:517-518).
+ * The layer runs as one launch of the decode-step kernel where a one-layer
+ * plan fits it (made on the layer's first call and kept, keyed by its
+ * tensors, until mh_shutdown), else as the per-layer launches. */
 int mh_moe(const mh_moe_layer *L, float *x, int32_t *sel, float *w);
 
 /* moe() for `batch` independent tokens on device x[batch][hidden], in place.
- * sel/w (device, [batch][top_k], may be NULL). */
+ * sel/w (device, [batch][top_k], may be NULL). At batch 1 the one-launch
+ * kernel as for mh_moe. */
 int mh_moe_dev(const mh_moe_layer *L, float *x, int batch, int32_t *sel, float *w);
 
 /* The MoE half of forward_batch() (engine/midge.c:591-611) for n tokens on

@@ -615,6 +615,70 @@ int stack_decode_layer(mh_stack *st, int l, float *x, int32_t *sel, float *w, ui
     return run_decode_layer(L, x, 1, b, usage, s);
 }
 
+// One-layer plans of the one-launch decode kernel for the layers that
+// mh_moe and mh_moe_dev see at batch 1, keyed by the resolved layer (its
+// device pointers and parameters): made on a layer's first call (the plan
+// scans the layer's down scales once), kept until mh_shutdown releases them
+// (the cache is dropped when the initialisation changes) or the cache is
+// full (then its oldest plan goes). A layer no plan can run keeps a null
+// entry and takes the per-layer launches.
+struct LayerPlanKey {
+    const void *experts, *router, *router_s, *router_b, *norm;
+    int64_t hidden, ffn;
+    int E, k, rdt, edt, act_plain, router_norm;
+    float alpha, limit, eps;
+    uint64_t stride;
+    bool operator==(const LayerPlanKey &o) const {
+        return experts == o.experts && router == o.router && router_s == o.router_s && router_b == o.router_b &&
+               norm == o.norm && hidden == o.hidden && ffn == o.ffn && E == o.E && k == o.k && rdt == o.rdt &&
+               edt == o.edt && act_plain == o.act_plain && router_norm == o.router_norm && alpha == o.alpha &&
+               limit == o.limit && eps == o.eps && stride == o.stride;
+    }
+};
+struct LayerPlans {
+    uint64_t epoch = 0;
+    std::vector<std::pair<LayerPlanKey, StepPlan *>> plans;
+};
+LayerPlans g_lplans;
+constexpr size_t kLayerPlans = 256;
+
+StepPlan *layer_plan(const DevLayer &L) {
+    if (g_lplans.epoch != init_epoch()) {
+        // plans of an earlier initialisation: mh_shutdown released their memory
+        for (auto &e : g_lplans.plans) step_plan_destroy(e.second);
+        g_lplans.plans.clear();
+        g_lplans.epoch = init_epoch();
+    }
+    const LayerPlanKey key{L.experts,    L.router.data, L.router.scales, L.router_b, L.mlp_norm,
+                           L.hidden,     L.ffn,         L.n_experts,     L.top_k,    L.router.dt,
+                           L.expert_dt,  L.act_plain,   L.router_norm,   L.alpha,    L.limit,
+                           L.norm_eps,   L.expert_stride};
+    for (auto &e : g_lplans.plans)
+        if (e.first == key) return e.second;
+    StepPlan *p = nullptr;
+    if (step_plan_create(&L, 1, &p) != MH_OK || !step_plan_ok(p)) {
+        clear_error();
+        if (p) step_plan_destroy(p);
+        p = nullptr;
+    }
+    if (g_lplans.plans.size() >= kLayerPlans) {
+        step_plan_destroy(g_lplans.plans.front().second);
+        g_lplans.plans.erase(g_lplans.plans.begin());
+    }
+    g_lplans.plans.push_back({key, p});
+    return p;
+}
+
+// moe() for one token on device x through the layer's one-launch plan:
+// MH_E_UNSUPPORTED (error cleared) when no plan runs this layer.
+int one_launch_layer(const DevLayer &L, float *x, int32_t *sel, float *w, hipStream_t s) {
+    StepPlan *p = sw(SW_NO_FUSED) ? nullptr : layer_plan(L);
+    if (!p) return MH_E_UNSUPPORTED;
+    const int rc = step_run(p, &L, 0, 1, x, sel, w, nullptr, s);
+    if (rc == MH_E_UNSUPPORTED) clear_error();
+    return rc;
+}
+
 }  // namespace mh
 
 using namespace mh;
@@ -634,6 +698,10 @@ int mh_moe_dev(const mh_moe_layer *Lh, float *x, int batch, int32_t *sel, float 
     LayerBufs b;
     MH_TRY(layer_bufs(L, batch, &b));
     hipStream_t s = stream();
+    if (batch == 1) {   // the one-launch kernel when a plan runs the layer
+        const int rc = one_launch_layer(L, x, sel ? sel : b.sel, w ? w : b.w, s);
+        if (rc != MH_E_UNSUPPORTED) return rc;
+    }
     MH_TRY(run_decode_layer(L, x, batch, b, nullptr, s));
     if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, (size_t)batch * L.top_k * 4, hipMemcpyDeviceToDevice, s));
     if (w) MH_HIP(hipMemcpyAsync(w, b.w, (size_t)batch * L.top_k * 4, hipMemcpyDeviceToDevice, s));
@@ -653,7 +721,10 @@ int mh_moe(const mh_moe_layer *Lh, float *x, int32_t *sel, float *w) {
     MH_TRY(layer_bufs(L, 1, &b));
     hipStream_t s = stream();
     MH_HIP(hipMemcpyAsync(dx, x, (size_t)L.hidden * 4, hipMemcpyHostToDevice, s));
-    MH_TRY(run_decode_layer(L, (float *)dx, 1, b, nullptr, s));
+    // the one-launch kernel when a plan runs the layer, else the per-layer launches
+    const int rc = one_launch_layer(L, (float *)dx, b.sel, b.w, s);
+    if (rc == MH_E_UNSUPPORTED) MH_TRY(run_decode_layer(L, (float *)dx, 1, b, nullptr, s));
+    else if (rc) return rc;
     MH_HIP(hipMemcpyAsync(x, dx, (size_t)L.hidden * 4, hipMemcpyDeviceToHost, s));
     if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, (size_t)L.top_k * 4, hipMemcpyDeviceToHost, s));
     if (w) MH_HIP(hipMemcpyAsync(w, b.w, (size_t)L.top_k * 4, hipMemcpyDeviceToHost, s));

@@ -1,4 +1,4 @@
-"""Build step: the reference engine's source with three static functions
+"""Build step: the reference engine's source with six static functions
 replaced by the layer-level GPU versions in include/midge_hip_layer.inc.
 
     python oracle/mk_layer_engine.py <midge checkout>/engine/midge.c _ref/midge_layer.c
@@ -17,6 +17,9 @@ FUNCS = [
     ("static void preload_hot(Model *m, double gb) {", 1),
     ("static void moe(Model *m, int layer) {", 2),
     ("static void forward_batch(Model *m, const int *toks, int n, int tfall,", 3),
+    ("static void forward(Model *m, int token, int want_logits) {", 4),
+    ("static int sample(Model *m, float temp, float topp) {", 5),
+    ("static void print_logits(Model *m) {", 6),
 ]
 
 

