@@ -189,7 +189,7 @@ int mh_attention_dev(const mh_attn_layer *L, float *x, int pos);
 int mh_sample_dev(const float *logits, int64_t V, float temp, float topp, float u, int32_t *out);
 
 /* mh_sample_dev on a fixed workspace that the library holds on each GPU
- * from mh_init() until the process ends (1,252,096 bytes: a 203,520-byte
+ * from mh_init() until the process ends (1,273,888 bytes: a 225,312-byte
  * head of counters, histograms and candidates, and 2^18 floats): the call allocates
  * nothing (no hipMalloc, hipFree or event), for callers that cannot
  * allocate: code under HIP graph capture, tight serving loops, harnesses

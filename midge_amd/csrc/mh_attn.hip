@@ -510,12 +510,21 @@ __global__ void __launch_bounds__(T) k_attn_split(SplitArgs A) {
     // ---------------------------------------------------------- combine
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (i == 0)
-        s_last = __hip_atomic_fetch_add(&A.cnt[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)A.S - 1u;
+    if (i == 0) {
+        // one thread's acquire serves the block: its invalidation covers the
+        // CU's cache and the L2 every wave reads through, and the barrier
+        // orders the other waves' loads after it
+        const bool last =
+            __hip_atomic_fetch_add(&A.cnt[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)A.S - 1u;
+        if (last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __builtin_amdgcn_s_waitcnt(0);
+            __hip_atomic_store(&A.cnt[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_last = last;
+    }
     __syncthreads();
     if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (i == 0) __hip_atomic_store(&A.cnt[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // after the acquire, plain loads in one round: every split's m and l
     // into LDS, then each thread's o values
     const float *ph = A.part + (size_t)h * A.S * (hd + 2);

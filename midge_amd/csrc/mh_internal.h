@@ -64,7 +64,7 @@ int scratch(Scratch slot, uint64_t bytes, void **p, bool *fresh = nullptr);
 // Host-mapped error flags owned by the runtime, one per purpose: allocated
 // (zeroed) and watched by mh_sync on first use after mh_init, freed by
 // mh_shutdown. *dev is the device address kernels raise.
-enum AsyncFlag { F_ATTN1 = 0, F_PREFILL_SCALE, F_COUNT };
+enum AsyncFlag { F_ATTN1 = 0, F_PREFILL_SCALE, F_SAMPLE, F_COUNT };
 int async_flag(AsyncFlag id, const char *msg, unsigned **dev);
 
 // Path switches for comparisons (tests, benchmarks): read once from the

@@ -72,10 +72,24 @@ constexpr int kHB = 1024 - kHLo;
 constexpr int kCap = 8192;         // candidates the one-block sort takes
 constexpr int kCapF = 1024;        // candidates the fast path ranks (one per thread)
 constexpr int kRadixBins = 256;    // bins per radix level (8 bits)
+constexpr const char *kSampleTimeout = "sampling: a radix-select barrier timed out (blocks not co-resident)";
 
 struct MaxIdx {
     float v;
     int i;
+};
+
+// The radix select on the grid: per slot (one level of one select), the
+// blocks' histograms summed by device atomics, and the blocks' arrivals.
+// Slot 0 is level 0 (the same for every select); the nucleus select's
+// levels 1-3 are slots 1-3, the draw's 4-6. The last arrival counter is the
+// id search's, with its per-block match counts.
+constexpr int kRSlots = 7;
+struct SampRadix {
+    double hm[kRSlots][kRadixBins];    // mass per bin
+    unsigned hc[kRSlots][kRadixBins];  // tokens per bin
+    unsigned arrive[kRSlots + 1];
+    unsigned gcnt[kSelBlocks];
 };
 
 // The workspace of one sample call (device memory): a fixed head, then p
@@ -92,11 +106,12 @@ struct SampWs {
     unsigned ncand;                 // tokens with e >= tc (the fast list)
     unsigned nsel;                  // tokens with p >= T (the select launch's list)
     unsigned pad[56];
+    SampRadix rx;                   // the radix select on the grid (zeroed by the top-p launch)
     int cand[kCap];                 // the fast list (the first kCapF), then the select launch's (the first kCap)
     alignas(16) float p[4];         // [V] (only when radix; 16-byte aligned for the block scans)
 };
 constexpr uint64_t kWsHead = offsetof(SampWs, p);
-static_assert(kWsHead == 203520, "the workspace head size the headers state");
+static_assert(kWsHead == 225312, "the workspace head size the headers state");
 
 // device-scope stores and loads of data that other blocks of the same
 // launch read (no cache on the way can hold a stale copy)
@@ -112,18 +127,25 @@ __device__ __forceinline__ T ld_agent(const T *p) {
 // True in the launch's last block to get here. Every thread's stores have
 // completed before its block counts itself in; the last block then drops
 // what its caches hold (acquire), resets the counter for the next call and
-// goes on alone.
+// goes on alone. One thread's acquire serves the block: its invalidation
+// covers the CU's cache and the L2 that every wave of the block reads
+// through, and the block barrier orders the other waves' loads after it
+// (an invalidation per wave costs microseconds).
 __device__ bool last_block(unsigned *done) {
     __shared__ bool s_last;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    if (threadIdx.x == 0) {
+        const bool last = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+        if (last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __builtin_amdgcn_s_waitcnt(0);
+            st_agent(done, 0u);
+        }
+        s_last = last;
+    }
     __syncthreads();
-    if (!s_last) return false;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (threadIdx.x == 0) st_agent(done, 0u);
-    return true;
+    return s_last;
 }
 
 // the reference loop's order: a larger value wins, equal values go to the
@@ -320,9 +342,56 @@ struct Select {
     int above, ties;
     double above_mass, total;
 };
-__device__ Select radix_select(const Probs &P, int V, double X, SelLds &L) {
+// One level of a radix select from its per-bin sums: thread t holds bin
+// bb = nb-1-t's mass m and count c (bb < 0: none). The running sums'
+// intervals (lo, hi] from the top tile (above_mass, total], so exactly one
+// bin holds X if any does. Appends the bin to *prefix and updates r (the
+// tokens above it, their mass, the bin's count); false when X lies beyond
+// the total at level 0 (r.total then holds it).
+__device__ bool level_choose(double m, int c, int bb, int lv, int kw, double X, Select &r, uint32_t *prefix) {
     __shared__ int s_b, s_above, s_low, s_ties;
     __shared__ double s_mass, s_total;
+    if (threadIdx.x == 0) {
+        s_b = -1;
+        s_low = INT32_MAX;
+    }
+    double tot, ex;
+    const double in = block_scan_f64(m, &ex, &tot);   // (its barriers order the reset above)
+    int ctot;
+    const int cin = block_scan_int(c, &ctot);
+    const double lo = r.above_mass + ex, hi = r.above_mass + in;
+    if (bb >= 0 && c > 0 && lo < X && X <= hi) {
+        s_b = bb;
+        s_mass = lo;
+        s_above = r.above + cin - c;
+    }
+    if (bb >= 0 && c > 0) atomicMin(&s_low, bb);
+    if (threadIdx.x == 0) s_total = r.above_mass + tot;
+    __syncthreads();
+    if (s_b < 0 && lv == 0) {   // X beyond the total
+        r.total = s_total;
+        __syncthreads();
+        return false;
+    }
+    if (s_b < 0 && bb == s_low) {
+        // X past this prefix's sum by a rounding (its mass at the level
+        // above was summed in another order): the prefix's last bin
+        s_b = bb;
+        s_mass = r.above_mass + (tot - m);
+        s_above = r.above + ctot - c;
+    }
+    __syncthreads();
+    if (bb >= 0 && bb == s_b) s_ties = c;
+    __syncthreads();
+    r.above_mass = s_mass;
+    r.above = s_above;
+    r.ties = s_ties;
+    *prefix = (*prefix << kw) | (uint32_t)s_b;
+    __syncthreads();
+    return true;
+}
+
+__device__ Select radix_select(const Probs &P, int V, double X, SelLds &L) {
     const int t = threadIdx.x, w = t >> 6;
     Select r{false, 0u, 0, 0, 0.0, 0.0};
     uint32_t prefix = 0;
@@ -332,10 +401,6 @@ __device__ Select radix_select(const Probs &P, int V, double X, SelLds &L) {
         for (int j = t; j < (kSelThreads / 64) * kRadixBins; j += kSelThreads) {
             (&L.hist.cnt[0][0])[j] = 0;
             (&L.hist.mass[0][0])[j] = 0.0;
-        }
-        if (t == 0) {
-            s_b = -1;
-            s_low = INT32_MAX;
         }
         __syncthreads();
         scan_p(P, V, [&](int, float p, bool ok) {
@@ -347,9 +412,7 @@ __device__ Select radix_select(const Probs &P, int V, double X, SelLds &L) {
             }
         });
         __syncthreads();
-        // thread t < nb takes bin nb-1-t (the waves' copies added in order);
-        // the running sums' intervals (lo, hi] tile (above_mass, total], so
-        // exactly one bin holds X if any does
+        // thread t < nb takes bin nb-1-t (the waves' copies added in order)
         const int b = nb - 1 - t;
         double m = 0;
         int c = 0;
@@ -359,38 +422,7 @@ __device__ Select radix_select(const Probs &P, int V, double X, SelLds &L) {
                 c += (int)L.hist.cnt[q][b];
             }
         }
-        double tot, ex;
-        const double in = block_scan_f64(m, &ex, &tot);
-        int ctot;
-        const int cin = block_scan_int(c, &ctot);
-        const double lo = r.above_mass + ex, hi = r.above_mass + in;
-        if (b >= 0 && c > 0 && lo < X && X <= hi) {
-            s_b = b;
-            s_mass = lo;
-            s_above = r.above + cin - c;
-        }
-        if (b >= 0 && c > 0) atomicMin(&s_low, b);
-        if (t == 0) s_total = r.above_mass + tot;
-        __syncthreads();
-        if (s_b < 0 && lv == 0) {   // X beyond the total
-            r.total = s_total;
-            return r;
-        }
-        if (s_b < 0 && b == s_low) {
-            // X past this prefix's sum by a rounding (its mass at the level
-            // above was summed in another order): the prefix's last bin
-            s_b = b;
-            s_mass = r.above_mass + (tot - m);
-            s_above = r.above + ctot - c;
-        }
-        __syncthreads();
-        if (b >= 0 && b == s_b) s_ties = c;
-        __syncthreads();
-        r.above_mass = s_mass;
-        r.above = s_above;
-        r.ties = s_ties;
-        prefix = (prefix << kw) | (uint32_t)s_b;
-        __syncthreads();
+        if (!level_choose(m, c, b, lv, kw, X, r, &prefix)) return r;
     }
     r.found = true;
     r.key = prefix;
@@ -630,6 +662,292 @@ __device__ void pick_radix(const Probs &P, int V, float topp, float u, SelLds &L
     if (threadIdx.x == 0) *out = id >= 0 ? id : 0;   // (id >= 0: every pass counts the same tokens)
 }
 
+// ------------------------------------------------ the radix select on the grid
+//
+// When the nucleus is too wide for the one-block sort, the select launch's
+// blocks run the radix select together instead of one block alone. Each
+// block takes a contiguous slice of the vocabulary: it stores p of its
+// slice, and per level it histograms its slice (per-wave copies added in
+// wave order), adds the histogram to the level's slot with device atomics
+// and arrives; once every block has arrived, every block reads the slot's
+// sums and makes the same choice. Level 0 (no prefix yet) is histogrammed
+// as p is stored and serves every select of the call; a later select whose
+// prefix at a level equals the nucleus select's reads that select's slot.
+// The id of the k-th token of a key in index order: each block counts its
+// slice's matches, every block finds the slice that holds the k-th, and
+// that block finds the token.
+static_assert(kSelBlocks <= 64, "the id search's per-block counts: one lane each");
+
+struct GridSel {
+    SampRadix *rx;
+    const float *ps;      // the stored p
+    unsigned *err;        // raised when an arrival wait times out
+    int lo, hi;           // this block's slice
+    uint32_t pre0[4];     // the nucleus select's prefix at each level
+    int lv0;              // levels whose slot the nucleus select filled
+};
+
+// This block's slice [lo, hi) of V tokens (64-token aligned).
+__device__ __forceinline__ void slice_of(int V, int *lo, int *hi) {
+    const int seg = ((V + (int)gridDim.x - 1) / (int)gridDim.x + 63) & ~63;
+    *lo = min((int)blockIdx.x * seg, V);
+    *hi = min(*lo + seg, V);
+}
+
+// Arrive at counter *cnt once this block's atomics and stores are done, and
+// wait (bounded) until every block of the launch has; false in every thread
+// of the block if the wait timed out, with *err raised. One thread's acquire
+// serves the block, as in last_block.
+__device__ bool arrive_wait(unsigned *cnt, unsigned *err) {
+    __shared__ int s_ok;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int ok = 1;
+        unsigned spins = 0;
+        while (ld_agent(cnt) < gridDim.x) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > (1u << 20)) {   // ~1 s: the blocks were not co-resident
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                ok = 0;
+                break;
+            }
+        }
+        if (ok) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        s_ok = ok;
+    }
+    __syncthreads();
+    return s_ok != 0;
+}
+
+__device__ __forceinline__ void hist_clear(SelLds &L) {
+    for (int j = threadIdx.x; j < (kSelThreads / 64) * kRadixBins; j += kSelThreads) {
+        (&L.hist.cnt[0][0])[j] = 0;
+        (&L.hist.mass[0][0])[j] = 0.0;
+    }
+}
+
+// The block's histogram (its waves' copies added in wave order) into the
+// slot's sums, then the arrival.
+__device__ bool hist_publish(GridSel &g, int slot, int nb, SelLds &L) {
+    __syncthreads();
+    for (int j = threadIdx.x; j < nb; j += kSelThreads) {
+        double m = 0;
+        unsigned c = 0;
+        for (int q = 0; q < kSelThreads / 64; ++q) {
+            m += L.hist.mass[q][j];
+            c += L.hist.cnt[q][j];
+        }
+        if (c) {
+            unsafeAtomicAdd(&g.rx->hm[slot][j], m);
+            __hip_atomic_fetch_add(&g.rx->hc[slot][j], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    return arrive_wait(&g.rx->arrive[slot], g.err);
+}
+
+// radix_select over the stored p, by every block of the launch (s: 0 the
+// nucleus select, 1 the draw's); every block returns the same Select (ok
+// false: a wait timed out). Slot 0 holds level 0 already.
+__device__ Select gselect(GridSel &g, int s, double X, SelLds &L, bool *ok) {
+    const int t = threadIdx.x, w = t >> 6;
+    Select r{false, 0u, 0, 0, 0.0, 0.0};
+    uint32_t prefix = 0;
+    for (int lv = 0; lv < 4; ++lv) {
+        const int kw = lv < 3 ? 8 : 7, sh = lv < 3 ? 23 - 8 * lv : 0, nb = 1 << kw;
+        int slot = 0;
+        if (lv > 0) {
+            if (s > 0 && lv < g.lv0 && prefix == g.pre0[lv]) {
+                slot = lv;   // the nucleus select's histogram of the same prefix
+            } else {
+                slot = 3 * s + lv;
+                hist_clear(L);
+                __syncthreads();
+                for (int i0 = g.lo + t; i0 < g.hi; i0 += 4 * kSelThreads) {
+                    float v[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int i = i0 + u * kSelThreads;
+                        v[u] = i < g.hi ? g.ps[i] : 0.f;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const uint32_t k = __float_as_uint(v[u]);
+                        if (i0 + u * kSelThreads < g.hi && (k >> (sh + kw)) == prefix) {
+                            const int b = (int)((k >> sh) & (uint32_t)(nb - 1));
+                            atomicAdd(&L.hist.cnt[w][b], 1u);
+                            atomicAdd(&L.hist.mass[w][b], (double)v[u]);
+                        }
+                    }
+                }
+                if (!hist_publish(g, slot, nb, L)) {
+                    *ok = false;
+                    return r;
+                }
+            }
+        }
+        if (s == 0) {
+            g.pre0[lv] = prefix;
+            g.lv0 = lv + 1;
+        }
+        // thread t takes bin nb-1-t of the slot
+        const int bb = nb - 1 - t;
+        double m = 0;
+        int c = 0;
+        if (bb >= 0) {
+            m = ld_agent(&g.rx->hm[slot][bb]);
+            c = (int)ld_agent(&g.rx->hc[slot][bb]);
+        }
+        if (!level_choose(m, c, bb, lv, kw, X, r, &prefix)) return r;
+    }
+    r.found = true;
+    r.key = prefix;
+    return r;
+}
+
+// *out = the id of the (rank + 1)-th token in index order whose stored p has
+// the bits key, by every block (the block whose slice holds it writes it).
+// False if the wait timed out.
+__device__ bool gid_of(GridSel &g, uint32_t key, int rank, int32_t *out) {
+    __shared__ int s_cnt[kSelThreads / 64];
+    __shared__ int s_owner, s_local;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    constexpr int nw = kSelThreads / 64;
+    // the slice in parts of seg2 tokens, one per wave
+    const int seg2 = ((g.hi - g.lo + nw - 1) / nw + 63) & ~63;
+    const int plo = min(g.lo + w * seg2, g.hi), phi = min(plo + seg2, g.hi);
+    int cw = 0;
+    for (int i = plo; i < phi; i += 64) {
+        const int j = i + lane;
+        cw += __popcll(__ballot(j < phi && __float_as_uint(g.ps[j]) == key));
+    }
+    if (lane == 0) s_cnt[w] = cw;
+    __syncthreads();
+    if (t == 0) {
+        int n = 0;
+        for (int q = 0; q < nw; ++q) n += s_cnt[q];
+        st_agent(&g.rx->gcnt[blockIdx.x], (unsigned)n);
+    }
+    if (!arrive_wait(&g.rx->arrive[kRSlots], g.err)) return false;
+    if (w == 0) {
+        // lane q holds block q's count: the block where the running count passes rank
+        const int n = lane < (int)gridDim.x ? (int)ld_agent(&g.rx->gcnt[lane]) : 0;
+        int incl = n;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        const unsigned long long past = __ballot(incl > rank);
+        if (lane == 0) s_owner = past ? __ffsll((long long)past) - 1 : -1;
+        const int owner = past ? __ffsll((long long)past) - 1 : -1;
+        if (owner >= 0 && lane == owner) s_local = rank - (incl - n);
+    }
+    __syncthreads();
+    if (s_owner < 0) {   // (never: every pass counts the same tokens)
+        if (blockIdx.x == 0 && t == 0) *out = 0;
+        return true;
+    }
+    if ((int)blockIdx.x != s_owner) return true;
+    int before = 0;
+    for (int q = 0; q < w; ++q) before += s_cnt[q];
+    const int k0 = s_local;
+    if (k0 >= before && k0 < before + cw) {
+        int k = k0 - before;
+        for (int i = plo; i < phi; i += 64) {
+            const unsigned long long bal = __ballot(i + lane < phi && __float_as_uint(g.ps[i + lane]) == key);
+            const int n = __popcll(bal);
+            if (k < n) {
+                unsigned long long m = bal;
+                for (int j = 0; j < k; ++j) m &= m - 1;   // drop the k lowest matches
+                if (lane == 0) *out = i + (__ffsll((long long)m) - 1);
+                break;
+            }
+            k -= n;
+        }
+    }
+    return true;
+}
+
+// pick_radix by every block of the launch: p of this block's slice stored
+// with its level-0 histogram, then the selects.
+__device__ void gpick_radix(const Probs &P0, int V, float topp, float u, SelLds &L, SampWs *ws, unsigned *err,
+                            int32_t *out) {
+    const int t = threadIdx.x, w = t >> 6;
+    GridSel g;
+    g.rx = &ws->rx;
+    g.ps = ws->p;
+    g.err = err;
+    g.lv0 = 0;
+    slice_of(V, &g.lo, &g.hi);
+    hist_clear(L);
+    __syncthreads();
+    for (int i0 = g.lo + t; i0 < g.hi; i0 += 4 * kSelThreads) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = i0 + q * kSelThreads;
+            v[q] = i < g.hi ? P0.lg[i] : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = i0 + q * kSelThreads;
+            if (i < g.hi) {
+                const float p = P0.of(v[q]);
+                ws->p[i] = p;
+                const int b = (int)((__float_as_uint(p) >> 23) & (kRadixBins - 1));
+                atomicAdd(&L.hist.cnt[w][b], 1u);
+                atomicAdd(&L.hist.mass[w][b], (double)p);
+            }
+        }
+    }
+    if (!hist_publish(g, 0, kRadixBins, L)) return;
+    const Probs P{P0.lg, ws->p, P0.mx, P0.temp, P0.den};
+    bool ok = true;
+    const Select sn = gselect(g, 0, (double)topp, L, &ok);
+    if (!ok) return;
+    int n, jn = 0;
+    double cum;
+    if (sn.found) {
+        jn = tie_place(sn.above_mass, __uint_as_float(sn.key), sn.ties, (double)topp);
+        n = sn.above + jn;
+        cum = sn.above_mass + (double)jn * (double)__uint_as_float(sn.key);
+    } else {
+        n = V;
+        cum = sn.total;
+    }
+    const float r = u * (float)cum;
+    if (r <= 0.f) {
+        // the first token of the order: the largest p, the lowest id
+        const Select s0 = gselect(g, 1, 1e-300, L, &ok);   // (a target below the largest p)
+        if (ok) (void)gid_of(g, s0.key, 0, out);
+        return;
+    }
+    const Select sp = gselect(g, 1, (double)r, L, &ok);
+    if (!ok) return;
+    if (sp.found) {
+        const int jp = tie_place(sp.above_mass, __uint_as_float(sp.key), sp.ties, (double)r);
+        if (sp.above + jp <= n) {
+            (void)gid_of(g, sp.key, jp - 1, out);
+            return;
+        }
+    }
+    // past the nucleus: its last token
+    if (sn.found) {
+        (void)gid_of(g, sn.key, jn - 1, out);
+        return;
+    }
+    if (blockIdx.x == 0) {   // (a total below topp by a rounding: the order's last token; block 0 alone)
+        const int id = last_in_order(P, V);
+        if (t == 0) *out = id >= 0 ? id : 0;
+    }
+}
+
 // The fast candidates' threshold: tokens with e >= tc go on the fast list.
 // Any tc gives exact picks (the fast path checks that what it orders is a
 // head of the whole order and holds the nucleus); with tc = (1 - topp) / 2V
@@ -774,6 +1092,9 @@ __global__ void __launch_bounds__(kSelThreads) k_samp_topp(const float *__restri
         s_mass[b] = 0.f;
     }
     if (t == 0) s_n = 0;
+    // the radix select's slots start at zero in every call
+    for (int j = blockIdx.x * kSelThreads + t; j < (int)(sizeof(SampRadix) / 4); j += gridDim.x * kSelThreads)
+        ((unsigned *)&ws->rx)[j] = 0u;
     const float mx = ws->mx;
     const float tc = fast_tc(topp, V);
     __syncthreads();
@@ -865,10 +1186,11 @@ __global__ void __launch_bounds__(kSelThreads) k_samp_topp(const float *__restri
 // holds every token of those bins (division is monotone). Then, over its
 // share of the tokens, the ids with p >= T (gathered in LDS, one counter add
 // per block; the first kCap), or, when the candidates cannot fit, p itself.
-// The last block: the sort and the pick, or the radix select.
+// The last block: the sort and the pick; or, when the nucleus is too wide
+// for the sort, the radix select on the grid.
 __global__ void __launch_bounds__(kSelThreads) k_samp_select(const float *__restrict__ lg, int V, float temp,
                                                              float topp, float u, SampWs *ws,
-                                                             int32_t *__restrict__ out) {
+                                                             int32_t *__restrict__ out, unsigned *err) {
     __shared__ SelLds L;
     __shared__ int s_hit, s_n, s_fb;
     if (ws->fast) return;
@@ -914,13 +1236,13 @@ __global__ void __launch_bounds__(kSelThreads) k_samp_select(const float *__rest
     // candidates (every token when no bin reaches the target)
     const float tp = hit == INT32_MAX ? 0.f : __uint_as_float((uint32_t)(kHLo + kHB - 1 - hit) << 20) / den;
     const bool radix = (hit == INT32_MAX ? V : nc) > kCap;
+    if (radix) {
+        gpick_radix(P, V, topp, u, L, ws, err, out);
+        return;
+    }
     const int Vr = (V + 63) & ~63;
     for (int i = blockIdx.x * kSelThreads + t; i < Vr; i += gridDim.x * kSelThreads) {
         const float p = i < V ? P(i) : 0.f;
-        if (radix) {
-            if (i < V) st_agent(&ws->p[i], p);
-            continue;
-        }
         const bool inc = i < V && p >= tp;
         const unsigned long long bal = __ballot(inc);
         if (!bal) continue;
@@ -932,7 +1254,7 @@ __global__ void __launch_bounds__(kSelThreads) k_samp_select(const float *__rest
         if (inc && pos < kCap) L.sort.id[pos] = i;
     }
     __syncthreads();
-    if (!radix) {
+    {
         const int nb = s_n;
         if (t == 0) s_fb = nb ? (int)atomicAdd(&ws->nsel, (unsigned)nb) : 0;
         __syncthreads();
@@ -941,15 +1263,13 @@ __global__ void __launch_bounds__(kSelThreads) k_samp_select(const float *__rest
     }
     if (!last_block(&ws->done[2])) return;
     const int cnt = (int)ld_agent(&ws->nsel);
-    if (!radix && cnt >= 1 && cnt <= kCap) {
+    if (cnt >= 1 && cnt <= kCap) {
         for (int j = t; j < cnt; j += kSelThreads) L.sort.id[j] = ld_agent(&ws->cand[j]);
         __syncthreads();
         if (pick_sorted(P, cnt, V, topp, u, L, out, false)) return;
         __syncthreads();
-        pick_radix(P, V, topp, u, L, out);   // (the histogram fell short: recomputed p)
-        return;
     }
-    pick_radix(radix ? Probs{lg, ws->p, mx, temp, den} : P, V, topp, u, L, out);
+    pick_radix(P, V, topp, u, L, out);   // (the histogram fell short: p recomputed, one block)
 }
 
 // zeroes the workspace head (counters, histogram) of a fresh workspace
@@ -982,6 +1302,8 @@ uint64_t sample_ws_bytes(int64_t V) { return kWsHead + (uint64_t)V * 4; }
 // not for it).
 int sample_launch(const float *logits, int V, float temp, float topp, float u, void *ws_dev, int32_t *out,
                   hipStream_t s, bool prof) {
+    unsigned *err = nullptr;   // (made at initialisation: the static entry point allocates nothing)
+    MH_TRY(async_flag(F_SAMPLE, kSampleTimeout, &err));
     SampWs *ws = (SampWs *)ws_dev;
     const bool greedy = temp <= 0.f;
 #define SAMP_LAUNCH(name, kernel, grid, block, ...)                                  \
@@ -994,7 +1316,7 @@ int sample_launch(const float *logits, int V, float temp, float topp, float u, v
     if (greedy) return hip_check(hipGetLastError(), "sample launch");
     SAMP_LAUNCH("sample_topp", k_samp_topp, dim3(kSelBlocks), dim3(kSelThreads), logits, V, temp, topp, u, ws, out);
     SAMP_LAUNCH("sample_select", k_samp_select, dim3(kSelBlocks), dim3(kSelThreads), logits, V, temp, topp, u, ws,
-                out);
+                out, err);
 #undef SAMP_LAUNCH
     return hip_check(hipGetLastError(), "sample launch");
 }
@@ -1002,7 +1324,7 @@ int sample_launch(const float *logits, int V, float temp, float topp, float u, v
 // ------------------------------------------ the fixed, allocation-free workspace
 
 // Vocabularies up to 2^18 tokens (gpt-oss: 201088) fit the fixed workspace:
-// 1,252,096 bytes of device memory per GPU (the 203,520-byte head: block
+// 1,273,888 bytes of device memory per GPU (the 225,312-byte head: block
 // maxima, f64 sums, two 64 x 328 histograms, counters and 8192 candidates;
 // then 2^18 floats of p), held until the process ends.
 constexpr int64_t kStaticMaxV = 1 << 18;
@@ -1014,6 +1336,8 @@ constexpr int kMaxDevices = 64;
 static void *g_static_ws[kMaxDevices];
 
 int sample_static_setup(int device) {
+    unsigned *err = nullptr;   // the radix select's error flag, made here so that no call allocates it
+    MH_TRY(async_flag(F_SAMPLE, kSampleTimeout, &err));
     if (device < 0 || device >= kMaxDevices) return fail(MH_E_ARG, "device %d beyond the static workspace table", device);
     void *p = nullptr;
     MH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(samp_static_ws)));
