@@ -69,6 +69,15 @@ class HipEvents:
         return float(ms.value)
 
 
+def gu_bytes_grouped(shape, assignments: int, unique: float) -> float:
+    """Algorithmic bytes of one expert-grouped gate/up launch: the gate and
+    up data + f16 scales + f32 biases of each routed expert once, the normed
+    inputs and the activations written per assignment."""
+    L = shape.layout
+    per_mat = L.rows[0] * L.cols[0] // 2 + L.rows[0] * (L.cols[0] // 32) * 2 + L.rows[0] * 4
+    return unique * 2 * per_mat + assignments * (shape.ffn * 4 + shape.hidden * 4)
+
+
 def gu_bytes_per_launch(shape, assignments: int) -> int:
     """Algorithmic bytes of one expert gate/up launch: per routed (token,
     expert) pair the gate and up data + f16 scales + f32 bias, the normed input
@@ -183,7 +192,8 @@ def run_gpu(args, shape):
         f"decode_step/t{st:02d}.{w}" for st in (0, 15, 1, 16, 17, 18, 2, 9, 19, 20, 10, 21, 22, 11, 3, 4, 5, 12, 13,
                                                 14, 6, 7)
         for w in ("first", "last"))
-    for name in ("decode_step", "expert_gu", "expert_down", "gemv", "topk", "rmsnorm", "combine_decode") + phases:
+    for name in ("decode_step", "grouped_gu", "grouped_down", "expert_gu", "expert_down", "gemv", "topk", "rmsnorm",
+                 "combine_norm", "combine_decode") + phases:
         tot, n = profile_query(name)
         if n:
             kern[name] = {"avg_us": 1e3 * tot / n, "launches": n}
@@ -201,6 +211,10 @@ def run_gpu(args, shape):
             with open(tpath) as f:
                 dom["traffic"] = json.load(f)["traffic_bytes"]
             dom["traffic_source"] = "profiles/decode_step_120b_b1_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE)"
+    elif "grouped_gu" in kern:
+        # each routed expert's gate/up read once per group of its tokens
+        dom = {"name": "k_grouped<0> (expert-grouped gate/up on the f16 matrix cores + clamped SwiGLU)",
+               "bytes": gu_bytes_grouped(shape, args.batch * k, unique), "avg_us": kern["grouped_gu"]["avg_us"]}
     else:
         dom = {"name": "expert_gu (fused gate/up MXFP4 GEMV + clamped SwiGLU)",
                "bytes": gu_bytes_per_launch(shape, args.batch * k), "avg_us": kern["expert_gu"]["avg_us"]}

@@ -21,7 +21,7 @@ ORACLE = os.path.join(ROOT, "oracle")
 REFERENCE = os.environ.get("MIDGE_REFERENCE", "/root/reference")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["mh_runtime.hip", "mh_gemv.hip", "mh_moe.hip", "mh_decode.hip", "mh_prefill.hip", "mh_fewtok.hip", "mh_synth.hip",
+SOURCES = ["mh_runtime.hip", "mh_gemv.hip", "mh_moe.hip", "mh_decode.hip", "mh_prefill.hip", "mh_grouped.hip", "mh_synth.hip",
            "mh_sample.hip", "mh_attn.hip", "mh_forward.hip"]
 HIPFLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",

@@ -1511,7 +1511,7 @@ struct StepPlan {
     int grp = 0;                   // 1 = k_decode_grp can run the stack
     int G = 0, PB = 0, RB = 0;     // k_decode_grp's shape (grid G * K)
     int ok = 0;                    // 1 = one of the kernels is eligible
-    int few = 0;                   // 1 = every MXFP4 scale is f16-exact (the few-token expert kernels)
+    int few = 0;                   // 1 = every MXFP4 scale is f16-exact (the expert-grouped kernels)
     char why[160] = {0};
     std::vector<std::pair<void *, uint64_t>> mem;   // device allocations (counted)
 };
@@ -1668,7 +1668,7 @@ int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out) {
     MH_TRY(plan_alloc(p, &p->h, sizeof(float) * (size_t)L0.top_k * (size_t)L0.ffn, "decode plan h"));
     if (L0.expert_dt == MH_DT_MXFP4) {
         // down scales (bit 1: the expert-group kernel), gate and up scales
-        // (bit 2: with bit 1, the few-token expert kernels of batches 2-16)
+        // (bit 2: with bit 1, the expert-grouped kernels of batches 2-16)
         unsigned *bad = nullptr;
         MH_TRY(dev_alloc((void **)&bad, sizeof(unsigned), "decode plan scale scan"));
         MH_HIP(hipMemset(bad, 0, sizeof(unsigned)));

@@ -76,8 +76,9 @@ int async_flag(AsyncFlag id, const char *msg, unsigned **dev);
 //   ATTN_SPLIT  attention as four launches instead of k_attn1
 //   COOP        the one-launch decode step as a cooperative launch
 //   Q8_NO_ROWS  long batched int8 GEMVs on the register-operand kernel
-//   FEW         decode steps of 2-16 tokens on the few-token kernels
-enum Switch { SW_NO_MFMA = 0, SW_NO_FUSED, SW_ATTN_SPLIT, SW_COOP, SW_Q8_NO_ROWS, SW_FEW, SW_COUNT };
+//   BATCH_GEMV  decode steps of 2-16 tokens on the per-assignment GEMVs
+//               instead of the expert-grouped matrix-core kernels
+enum Switch { SW_NO_MFMA = 0, SW_NO_FUSED, SW_ATTN_SPLIT, SW_COOP, SW_Q8_NO_ROWS, SW_BATCH_GEMV, SW_COUNT };
 bool sw(Switch s);
 
 // The number of successful mh_init calls so far (never reset): state that a
@@ -143,15 +144,16 @@ struct StepPlan;
 int step_plan_create(const DevLayer *layers, int n_layers, StepPlan **out);
 void step_plan_destroy(StepPlan *p);
 bool step_plan_ok(const StepPlan *p);
-// 1 if every MXFP4 scale of the plan's layers is f16-exact (the few-token
-// expert kernels may run them).
+// 1 if every MXFP4 scale of the plan's layers is f16-exact (the expert-
+// grouped matrix-core kernels may run them).
 bool step_plan_few(const StepPlan *p);
-// The expert FFN of a decode step of 2-16 tokens on the f16 matrix cores
-// (mh_fewtok.hip): h from xb, then ye, walking the top-k kernel's
-// expert-sorted order. fewtok_ok: the layer and token count fit.
-bool fewtok_ok(const DevLayer &L, int n);
-int launch_fewtok(const DevLayer &L, int n, const int32_t *order, const float *xb, float *h, float *ye,
-                  hipStream_t s);
+// The expert FFN of a decode step of 2-16 tokens on the f16 matrix cores,
+// each routed expert's weights read once for its tokens (mh_grouped.hip): h
+// from xb, then ye, from the top-k kernel's expert-sorted order.
+// grouped_ok: the layer and token count fit.
+bool grouped_ok(const DevLayer &L, int n);
+int launch_grouped(const DevLayer &L, int n, const int32_t *order, const float *xb, float *h, float *ye,
+                   hipStream_t s);
 // Runs layers [first, first + n_layers) of a plan in one launch; sel, w and
 // usage are indexed from layer `first`. With gxb (then one layer, gsel and
 // gw [K]): expert_apply per slot with the routing given, x += w_i

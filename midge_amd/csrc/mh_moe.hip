@@ -473,17 +473,16 @@ int run_router(const DevLayer &L, const float *x, int n, int unfilled, const Lay
 }
 
 // few: the layer's MXFP4 scales are known to be f16-exact (a stack's plan
-// scanned them), so 2-16 tokens may take the few-token matrix-core kernels
-// under the FEW switch (opt-in: at 16 tokens of gpt-oss-120b they are
-// slower than the per-assignment GEMVs, 7.3 vs 6.05 ms per step, being
-// bound by the e2m1 -> f16 conversion at one wave per SIMD).
+// scanned them), so 2-16 tokens take the expert-grouped matrix-core kernels
+// (each routed expert read once for its tokens); the BATCH_GEMV switch, or
+// a layer they cannot run, keeps the per-assignment GEMVs.
 // have_xb: b.xb holds this layer's normed input already; next: the next
 // layer, whose RMSNorm is fused into this layer's combine (or null).
 int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uint32_t *usage, hipStream_t s,
                      bool few = false, bool have_xb = false, const DevLayer *next = nullptr) {
     MH_TRY(run_router(L, have_xb ? nullptr : x, n, -1, b, usage, b.order, s));
-    if (few && b.order && sw(SW_FEW) && fewtok_ok(L, n))
-        MH_TRY(launch_fewtok(L, n, b.order, b.xb, b.h, b.ye, s));
+    if (few && b.order && !sw(SW_BATCH_GEMV) && grouped_ok(L, n))
+        MH_TRY(launch_grouped(L, n, b.order, b.xb, b.h, b.ye, s));
     else
         MH_TRY(launch_experts(L, n * L.top_k, b.sel, b.order, b.xb, b.h, b.ye, s));
     if (next) {

@@ -521,16 +521,16 @@ def _composed_decode(shape, arrays, L, x):
     (MoEShape(hidden=256, ffn=192, n_experts=16, top_k=4), 16, "random"),
     (MoEShape(hidden=256, ffn=192, n_experts=16, top_k=4), 9, "unfilled"),
 ], ids=["20b-b2", "20b-b7", "20b-b16", "20b-b16-one-run", "mid-b16", "mid-b9-unfilled"])
-def test_stack_batch_few_token_kernels(mh, shape, batch, case):
-    """Decode of 2-16 tokens through a stack: the few-token matrix-core
-    kernels (MIDGE_HIP_FEW=1; assignments grouped by expert, groups of up to
-    4) against the per-assignment GEMVs (the default) within SPLIT_TOL and
-    the oracle within TOL per token, with identical selections. "same": every token
-    equal, so each routed expert has a run of `batch` assignments (groups of
-    4 and a remainder); "unfilled": only two experts can be routed, so two
-    slots per token are unfilled (their y is 0)."""
-    import os
-    say(f"few-token {shape.hidden}x{shape.ffn} E={shape.n_experts} batch={batch} {case}")
+def test_stack_batch_grouped_kernels(mh, shape, batch, case):
+    """Decode of 2-16 tokens through a stack: the expert-grouped matrix-core
+    kernels (the default; assignments grouped by expert, groups of up to 4,
+    each routed expert's weights read once per group) against the
+    per-assignment GEMVs (the BATCH_GEMV switch) within SPLIT_TOL and the
+    oracle within TOL per token, with identical selections. "same": every
+    token equal, so each routed expert has a run of `batch` assignments
+    (groups of 4 and a remainder); "unfilled": only two experts can be
+    routed, so two slots per token are unfilled (their y is 0)."""
+    say(f"grouped {shape.hidden}x{shape.ffn} E={shape.n_experts} batch={batch} {case}")
     keys = Keys(64)
     ex = synth.host_layer_experts(shape, keys, 0)
     w, s, b, nw = synth.host_router(shape, keys, 0)
@@ -546,9 +546,9 @@ def test_stack_batch_few_token_kernels(mh, shape, batch, case):
     if case == "same":
         x0 = np.ascontiguousarray(np.repeat(x0[:1], batch, axis=0))
     out = {}
-    for mode in ("few", "gemv"):
-        if mode == "few":
-            set_switch("FEW", True)
+    for mode in ("grouped", "gemv"):
+        if mode == "gemv":
+            set_switch("BATCH_GEMV", True)
         try:
             xd, sd = DevBuf.from_array(x0), DevBuf(batch * k * 4)
             st.decode(xd, batch, sd)
@@ -557,16 +557,16 @@ def test_stack_batch_few_token_kernels(mh, shape, batch, case):
             xd.free()
             sd.free()
         finally:
-            set_switch("FEW", False)
+            set_switch("BATCH_GEMV", False)
     st.destroy()
-    xf, sf = out["few"]
+    xf, sf = out["grouped"]
     xg, sg = out["gemv"]
     assert (sf == sg).all()
     # the two paths sum in different orders: not bit-identical (so the
     # matrix-core path ran), within SPLIT_TOL per token
     assert not np.array_equal(xf, xg)
     worst = max(rel_l2(xf[t], xg[t]) for t in range(batch))
-    say(f"few-token vs GEMV: worst per-token rel L2 {worst:.3g}")
+    say(f"grouped vs GEMV: worst per-token rel L2 {worst:.3g}")
     for t in range(batch):
         assert rel_l2(xf[t], xg[t]) < SPLIT_TOL, t
     for t in sorted({0, batch // 2, batch - 1}):
