@@ -192,8 +192,8 @@ def run_gpu(args, shape):
         f"decode_step/t{st:02d}.{w}" for st in (0, 15, 1, 16, 17, 18, 2, 9, 19, 20, 10, 21, 22, 11, 3, 4, 5, 12, 13,
                                                 14, 6, 7)
         for w in ("first", "last"))
-    for name in ("decode_step", "grouped_gu", "grouped_down", "expert_gu", "expert_down", "gemv", "topk", "rmsnorm",
-                 "combine_norm", "combine_decode") + phases:
+    for name in ("decode_step", "grouped_gu", "grouped_down", "expert_gu", "expert_down", "combine_route", "gemv",
+                 "topk", "rmsnorm", "combine_norm", "combine_decode") + phases:
         tot, n = profile_query(name)
         if n:
             kern[name] = {"avg_us": 1e3 * tot / n, "launches": n}

@@ -58,7 +58,7 @@ void unregister_owner(void *key);
 // this call (re)allocated the slot (its contents are then undefined, also
 // when the new allocation lands at an address the slot had before).
 enum Scratch { S_X = 0, S_Y, S_XB, S_H, S_YE, S_RL, S_SEL, S_W, S_PLAN, S_MISC, S_LIST, S_Q, S_XQ, S_ORD, S_SAMPLE, S_ATTN,
-               S_ATTN1, S_COUNT };
+               S_ATTN1, S_CROUTE, S_COUNT };
 int scratch(Scratch slot, uint64_t bytes, void **p, bool *fresh = nullptr);
 
 // Host-mapped error flags owned by the runtime, one per purpose: allocated
@@ -78,7 +78,9 @@ int async_flag(AsyncFlag id, const char *msg, unsigned **dev);
 //   Q8_NO_ROWS  long batched int8 GEMVs on the register-operand kernel
 //   BATCH_GEMV  decode steps of 2-16 tokens on the per-assignment GEMVs
 //               instead of the expert-grouped matrix-core kernels
-enum Switch { SW_NO_MFMA = 0, SW_NO_FUSED, SW_ATTN_SPLIT, SW_COOP, SW_Q8_NO_ROWS, SW_BATCH_GEMV, SW_COUNT };
+//   SPLIT_ROUTE a stack decode's layer boundary (combine, norm, router,
+//               top-k) as three launches instead of k_combine_route
+enum Switch { SW_NO_MFMA = 0, SW_NO_FUSED, SW_ATTN_SPLIT, SW_COOP, SW_Q8_NO_ROWS, SW_BATCH_GEMV, SW_SPLIT_ROUTE, SW_COUNT };
 bool sw(Switch s);
 
 // The number of successful mh_init calls so far (never reset): state that a

@@ -322,6 +322,179 @@ k_combine_norm(float *__restrict__ x, const float *__restrict__ ye, const float 
     for (int64_t r = threadIdx.x; r < H; r += blockDim.x) xb[(size_t)t * H + r] = xt[r] * inv * nw[r];
 }
 
+// The boundary between two layers of a decode of 2-16 tokens, in one launch:
+// the previous layer's combine x += sum_i w_i y_i (as k_combine_norm; none
+// before the first layer), this layer's RMSNorm (xb, as k_rmsnorm), its
+// router logits, and per token the top-k and weights (wave_topk_token, as
+// k_topk); the launch's last token sorts the assignments by expert.
+//   Block (t, g) forms token t's x and xb itself (the same arithmetic in
+//   every block of the token, bit-identical to the separate kernels) and
+//   computes router rows [kCRRows g, +kCRRows), one per wave, the row's loads
+//   issued first. The token's last block to arrive ranks the token and
+//   writes its x back (every block of the token has read it by then); the
+//   launch's last ranked token writes the order. Counters are left at zero.
+constexpr int kCRRows = 16;       // router rows per block (one per wave)
+constexpr int kCRChunks = 12;     // 16-byte router chunks per lane
+constexpr int kCRMaxH = 3072;     // hidden (3 elements per thread)
+
+struct CombineRouteArgs {
+    float *x;              // [n][H] residual (combined in place)
+    const float *ye;       // [n k][H] the previous layer's expert outputs, or null
+    const float *wprev;    // [n k] their weights
+    int64_t H;
+    int k;
+    const float *nw;       // this layer's norm weights
+    float eps;
+    float *xb;             // [n][H] out
+    const uint8_t *rw;     // router rows [E][H] (int8 or f32)
+    const float *rs;       // int8 row scales [E]
+    const float *rb;       // router bias [E] or null
+    int E, router_norm, unfilled, n;
+    float *rl;             // [n][E] logits (scratch)
+    int32_t *sel;          // [n][k] out
+    float *w;              // [n][k] out
+    uint32_t *usage;       // [E] or null
+    int32_t *order;        // [2 n k] out
+    unsigned *cnt;         // [n + 1] arrival counters
+};
+
+template <int DT, int PER>
+__global__ void __launch_bounds__(1024) k_combine_route(CombineRouteArgs A) {
+#pragma clang fp contract(off)
+    __shared__ float part[16];
+    __shared__ __attribute__((aligned(16))) float s_xb[kCRMaxH];
+    __shared__ int s_last;
+    __shared__ int skey[kMaxOrder];
+    constexpr int CE = mh_chunk<DT>::E;
+    constexpr int kV = kCRMaxH / 1024;
+    const int t = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t H = A.H;
+    const int C = (int)(H / CE), E = A.E, k = A.k;
+    // this wave's router row: its loads first (they wait for nothing)
+    const int e = g * kCRRows + wave;
+    const bool has_row = e < E;   // wave-uniform
+    const mh_rsrc rr = gemv_rsrc(A.rw, (uint32_t)E * (uint32_t)C * 16u);
+    const int er = min(e, E - 1);
+    mh_u4 q[kCRChunks];
+#pragma unroll
+    for (int j = 0; j < kCRChunks; ++j) {
+        const int c = min(lane + 64 * j, C - 1);   // past the row: the last chunk again, not used
+        q[j] = __builtin_amdgcn_raw_buffer_load_b128(rr, (uint32_t)(er * C + c) * 16u, 0, 0);
+    }
+    // x (combined) and the sum of its squares, as k_combine_norm / k_rmsnorm
+    float *xt = A.x + (size_t)t * H;
+    float v[kV];
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < kV; ++u) {
+        const int64_t r = tid + 1024 * u;
+        v[u] = 0.f;
+        if (r < H) {
+            if (A.ye) {
+                float moe = 0.f;
+                for (int i = 0; i < k; ++i) moe = moe + A.wprev[(size_t)t * k + i] * A.ye[((size_t)t * k + i) * H + r];
+                v[u] = xt[r] + moe;
+            } else {
+                v[u] = xt[r];
+            }
+            s = __builtin_fmaf(v[u], v[u], s);
+        }
+    }
+    s = mh_wave_sum(s);
+    if (lane == 0) part[wave] = s;
+    __syncthreads();
+    float ss = 0.f;
+    for (int i = 0; i < 16; ++i) ss += part[i];
+    const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+#pragma unroll
+    for (int u = 0; u < kV; ++u) {
+        const int64_t r = tid + 1024 * u;
+        if (r < H) {
+            const float xbv = v[u] * inv * A.nw[r];
+            s_xb[r] = xbv;
+            if (g == 0) A.xb[(size_t)t * H + r] = xbv;
+        }
+    }
+    __syncthreads();
+    // router row e of token t
+    if (has_row) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < kCRChunks; ++j) {
+            const int c = lane + 64 * j;
+            if (c < C) acc += mh_dot_chunk<DT>(q[j], s_xb + c * CE);
+        }
+        acc = mh_wave_sum(acc);
+        if (lane == 0) {
+            float p = acc;
+            if constexpr (DT == MH_DT_Q8R) p *= A.rs[e];
+            __hip_atomic_store(&A.rl[(size_t)t * E + e], p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // the token's blocks count themselves in; the last ranks the token (one
+    // thread's acquire serves the block: its invalidation covers the CU's
+    // cache and the L2 that every wave reads through)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const bool last = __hip_atomic_fetch_add(&A.cnt[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                          gridDim.y - 1;
+        if (last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __builtin_amdgcn_s_waitcnt(0);
+            __hip_atomic_store(&A.cnt[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_last = last ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (A.ye) {
+#pragma unroll
+        for (int u = 0; u < kV; ++u) {
+            const int64_t r = tid + 1024 * u;
+            if (r < H) xt[r] = v[u];
+        }
+    }
+    if (wave == 0)
+        wave_topk_token<PER>(A.rl + (size_t)t * E, A.rb, E, k, A.router_norm, A.unfilled, A.sel + (size_t)t * k,
+                             A.w + (size_t)t * k, A.usage);
+    // the launch's last ranked token sorts the assignments (as k_topk)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const bool last =
+            __hip_atomic_fetch_add(&A.cnt[A.n], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)A.n - 1u;
+        if (last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __builtin_amdgcn_s_waitcnt(0);
+            __hip_atomic_store(&A.cnt[A.n], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_last = last ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const int N = A.n * k;
+    for (int i = tid; i < N; i += 1024) {
+        const int se = A.sel[i];
+        skey[i] = (se >= 0 && se < E ? se : E) * N + i;   // distinct keys
+    }
+    __syncthreads();
+    for (int i = tid; i < N; i += 1024) {
+        const int ki = skey[i];
+        int r = 0;
+        for (int j = 0; j < N; ++j) r += skey[j] < ki;
+        A.order[r] = i;
+        A.order[N + r] = ki / N < E ? ki / N : -1;
+    }
+}
+
+// zeroes n words (a fill kernel: no memset node in a caller's graph)
+__global__ void k_zero_u32(uint32_t *p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
 // Prefill combine (engine/midge.c:595-611, 465-466): each token's
 // contributions are added straight into its residual in ascending expert
 // order (slot order among equal ids, as the reference's loops give).
@@ -429,6 +602,64 @@ int launch_topk(const float *rl, const float *bias, int n, int E, int k, int rou
         MH_LAUNCH("topk", k_topk<kMaxExperts / 64>, grid, block, 0, s, rl, bias, n, E, k, router_norm, unfilled, sel,
                   w, usage, order);
     return hip_check(hipGetLastError(), "topk launch");
+}
+
+// The layer boundary of a decode of 2-16 tokens in one launch
+// (k_combine_route): MH_E_UNSUPPORTED (error cleared) for shapes it does not
+// take. ye / wprev null: the first layer (no combine).
+bool combine_route_ok(const DevLayer &L, int n) {
+    const int CE = L.router.dt == MH_DT_Q8R ? 16 : 4;
+    return (L.router.dt == MH_DT_Q8R || L.router.dt == MH_DT_F32) && n >= 1 && n <= 16 &&
+           n * L.top_k <= kMaxOrder && L.hidden <= kCRMaxH && L.hidden % CE == 0 &&
+           L.hidden / CE <= 64 * kCRChunks && L.n_experts <= kMaxExperts && (uintptr_t)L.router.data % 16 == 0 &&
+           (uint64_t)L.n_experts * (uint64_t)L.hidden * (L.router.dt == MH_DT_Q8R ? 1u : 4u) < (1ull << 32);
+}
+
+int launch_combine_route(const DevLayer &L, float *x, const float *ye, const float *wprev, int n, float *xb,
+                         float *rl, int32_t *sel, float *w, uint32_t *usage, int32_t *order, hipStream_t s) {
+    if (!combine_route_ok(L, n)) return MH_E_UNSUPPORTED;
+    void *cp = nullptr;
+    bool fresh = false;
+    MH_TRY(scratch(S_CROUTE, sizeof(unsigned) * 17, &cp, &fresh));
+    if (fresh) {
+        MH_LAUNCH("zero_counters", k_zero_u32, dim3(1), dim3(64), 0, s, (uint32_t *)cp, 17);
+        MH_TRY(hip_check(hipGetLastError(), "counter clear"));
+    }
+    CombineRouteArgs A;
+    A.x = x;
+    A.ye = ye;
+    A.wprev = wprev;
+    A.H = L.hidden;
+    A.k = L.top_k;
+    A.nw = L.mlp_norm;
+    A.eps = L.norm_eps;
+    A.xb = xb;
+    A.rw = L.router.data;
+    A.rs = (const float *)L.router.scales;
+    A.rb = L.router_b;
+    A.E = L.n_experts;
+    A.router_norm = L.router_norm;
+    A.unfilled = -1;
+    A.n = n;
+    A.rl = rl;
+    A.sel = sel;
+    A.w = w;
+    A.usage = usage;
+    A.order = order;
+    A.cnt = (unsigned *)cp;
+    const dim3 grid((unsigned)n, (unsigned)((L.n_experts + kCRRows - 1) / kCRRows));
+#define CR_LAUNCH(DT, PER) MH_LAUNCH("combine_route", (k_combine_route<DT, PER>), grid, dim3(1024), 0, s, A)
+    if (L.router.dt == MH_DT_Q8R) {
+        if (L.n_experts <= 128) CR_LAUNCH(MH_DT_Q8R, 2);
+        else if (L.n_experts <= 256) CR_LAUNCH(MH_DT_Q8R, 4);
+        else CR_LAUNCH(MH_DT_Q8R, kMaxExperts / 64);
+    } else {
+        if (L.n_experts <= 128) CR_LAUNCH(MH_DT_F32, 2);
+        else if (L.n_experts <= 256) CR_LAUNCH(MH_DT_F32, 4);
+        else CR_LAUNCH(MH_DT_F32, kMaxExperts / 64);
+    }
+#undef CR_LAUNCH
+    return hip_check(hipGetLastError(), "combine/route launch");
 }
 
 // Scratch for a layer call of n tokens.
@@ -855,6 +1086,36 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
     }
     LayerBufs b;
     MH_TRY(layer_bufs(L0, batch, &b));
+    const bool few = step_plan_few(st->plan);
+    bool fuse = b.order != nullptr && !sw(SW_SPLIT_ROUTE);
+    for (int l = 0; l < nl && fuse; l++) fuse = combine_route_ok(st->layers[(size_t)l], batch);
+    if (fuse) {
+        // each layer boundary (the previous layer's combine, this layer's
+        // norm, router and top-k) in one launch; the sel / w of a layer in
+        // the caller's rows or, without them, in place in the scratch (a
+        // token's weights are rewritten only after every block of the token
+        // has read the previous layer's)
+        auto lsel = [&](int l) { return sel ? sel + (size_t)l * batch * k : b.sel; };
+        auto lw = [&](int l) { return w ? w + (size_t)l * batch * k : b.w; };
+        auto luse = [&](int l) { return usage ? usage + (size_t)l * L0.n_experts : nullptr; };
+        MH_TRY(launch_combine_route(L0, x, nullptr, nullptr, batch, b.xb, b.rl, lsel(0), lw(0), luse(0), b.order, s));
+        for (int l = 0; l < nl; l++) {
+            const DevLayer &L = st->layers[(size_t)l];
+            if (few && !sw(SW_BATCH_GEMV) && grouped_ok(L, batch))
+                MH_TRY(launch_grouped(L, batch, b.order, b.xb, b.h, b.ye, s));
+            else
+                MH_TRY(launch_experts(L, batch * k, lsel(l), b.order, b.xb, b.h, b.ye, s));
+            if (l + 1 < nl) {
+                MH_TRY(launch_combine_route(st->layers[(size_t)l + 1], x, b.ye, lw(l), batch, b.xb, b.rl, lsel(l + 1),
+                                            lw(l + 1), luse(l + 1), b.order, s));
+            } else {
+                MH_LAUNCH("combine_decode", k_combine_decode, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)batch),
+                          dim3(256), 0, s, x, b.ye, lw(l), L.hidden, L.top_k);
+                MH_TRY(hip_check(hipGetLastError(), "combine launch"));
+            }
+        }
+        return MH_OK;
+    }
     for (int l = 0; l < nl; l++) {
         LayerBufs bl = b;
         if (sel) bl.sel = sel + (size_t)l * batch * k;
@@ -862,7 +1123,7 @@ int mh_stack_decode(mh_stack *st, float *x, int batch, int32_t *sel, float *w, u
         // every layer after the first takes its normed input from the
         // previous layer's combine
         MH_TRY(run_decode_layer(st->layers[(size_t)l], x, batch, bl,
-                                usage ? usage + (size_t)l * L0.n_experts : nullptr, s, step_plan_few(st->plan), l > 0,
+                                usage ? usage + (size_t)l * L0.n_experts : nullptr, s, few, l > 0,
                                 l + 1 < nl ? &st->layers[(size_t)l + 1] : nullptr));
     }
     return MH_OK;

@@ -53,7 +53,7 @@ State g;
 uint64_t g_epoch = 0;   // successful mh_init calls
 
 // Path switches (sw, mh_set_switch), read from the environment by mh_init.
-const char *const kSwitchNames[SW_COUNT] = {"NO_MFMA", "NO_FUSED", "ATTN_SPLIT", "COOP", "Q8_NO_ROWS", "BATCH_GEMV"};
+const char *const kSwitchNames[SW_COUNT] = {"NO_MFMA", "NO_FUSED", "ATTN_SPLIT", "COOP", "Q8_NO_ROWS", "BATCH_GEMV", "SPLIT_ROUTE"};
 bool g_sw[SW_COUNT] = {};
 void read_switches() {
     char name[64];

@@ -311,6 +311,91 @@ def test_stack_chain_vs_oracle(mh):
         lay.release()
 
 
+@pytest.mark.parametrize("router_dt,batch,rows", [(_lib.DT_Q8R, 16, True), (_lib.DT_Q8R, 5, False),
+                                                  (_lib.DT_F32, 16, True)],
+                         ids=["q8r-b16-rows", "q8r-b5-scratch", "f32-b16-rows"])
+def test_stack_batch_fused_layer_boundary(mh, router_dt, batch, rows):
+    """Decode of 2-16 tokens through a 3-layer stack at the gpt-oss-20b
+    shape: each layer boundary (the previous layer's combine, the norm, the
+    router logits, the top-k, the expert order) in one launch against the
+    three launches (SPLIT_ROUTE): the same x and xb arithmetic, router dots
+    in another order. The logits (magnitude ~20-60 here) then differ in their
+    last bits, the weights (their softmax) by up to ~1e-4 relative (7.2e-5
+    measured), and x through them: identical selections and usage counts,
+    weights within 5e-4 relative and x within TOL per token, with the
+    selections in the caller's rows or only in the library's scratch (the
+    weights rewritten in place). Against the oracle on three tokens: with
+    rows, the same selections, weights within WTOL and x within TOL when the
+    oracle's chain applies the kernel's weights (the router's reassociation
+    and the expert arithmetic held apart); without, x within WTOL's rtol of
+    the oracle's own chain and the usage counts of the oracle's selections
+    over every token."""
+    shape = MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4, n_layers=3, router_dt=router_dt)
+    say(f"fused layer boundary router dt={router_dt} batch={batch} rows={rows}")
+    keys = Keys(77)
+    layers, structs = [], []
+    for l in range(shape.n_layers):
+        ex = synth.host_layer_experts(shape, keys, l)
+        w, s_, b, nw = synth.host_router(shape, keys, l)
+        if router_dt == _lib.DT_F32:
+            w, s_ = (w.astype(np.float32) * s_[:, None]).astype(np.float32), None
+        layers.append(MoELayer.host(shape, ex, w, s_, b, nw))
+        _LIVE.append(layers[-1])
+        structs.append(po.layer_struct(shape, ex, w, s_, b, nw))
+    st = Stack(layers, max_batch=16)
+    nl, k, E = shape.n_layers, shape.top_k, shape.n_experts
+    X = synth.host_x(shape, keys, batch, step=5)
+    out = {}
+    for mode in ("fused", "split"):
+        set_switch("SPLIT_ROUTE", mode == "split")
+        try:
+            xd = DevBuf.from_array(X)
+            sd, wd = (DevBuf(nl * batch * k * 4), DevBuf(nl * batch * k * 4)) if rows else (None, None)
+            ud = DevBuf.from_array(np.zeros((nl, E), np.uint32))
+            st.decode(xd, batch, sd.ptr if sd else None, wd.ptr if wd else None, ud)
+            mh.sync()
+            out[mode] = (xd.download(np.float32, X.shape),
+                         sd.download(np.int32, (nl, batch, k)) if sd else None,
+                         wd.download(np.float32, (nl, batch, k)) if wd else None,
+                         ud.download(np.uint32, (nl, E)))
+            for d in (xd, sd, wd, ud):
+                if d:
+                    d.free()
+        finally:
+            set_switch("SPLIT_ROUTE", False)
+    st.destroy()
+    xf, sf, wf, uf = out["fused"]
+    xs, ss, ws, us = out["split"]
+    assert (uf == us).all()
+    if rows:
+        assert (sf == ss).all()
+        np.testing.assert_allclose(wf, ws, rtol=5e-4, atol=1e-7)
+        for l in range(nl):
+            assert (uf[l] == np.bincount(sf[l].ravel(), minlength=E)).all()
+    worst = max(rel_l2(xf[t], xs[t]) for t in range(batch))
+    say(f"fused vs split layer boundary: worst per-token rel L2 {worst:.3g}")
+    for t in range(batch):
+        assert rel_l2(xf[t], xs[t]) < TOL, t
+    if rows:
+        for t in sorted({0, batch // 2, batch - 1}):
+            x = X[t][None]
+            for l in range(nl):
+                xb, selr, wr = po.route_batch(structs[l], x)
+                assert (sf[l, t] == selr[0]).all(), (l, t)
+                np.testing.assert_allclose(wf[l, t], wr[0], **WTOL)
+                x = po.expert_major_apply(structs[l], xb, sf[l, t][None], wf[l, t][None], x)
+            assert rel_l2(xf[t], x[0]) < TOL, t
+    else:
+        so = np.empty((nl, batch, k), np.int32)
+        for t in range(batch):
+            x = X[t]
+            for l in range(nl):
+                x, so[l, t], _ = po.moe_decode(structs[l], x)
+            assert rel_l2(xf[t], x) < WTOL["rtol"], t
+        for l in range(nl):
+            assert (uf[l] == np.bincount(so[l].ravel(), minlength=E)).all()
+
+
 @pytest.mark.parametrize("shape,layers", [
     (MoEShape(hidden=256, ffn=192, n_experts=16, top_k=4), 5),
     (MoEShape(hidden=2880, ffn=2880, n_experts=32, top_k=4), 3),
