@@ -22,6 +22,13 @@
 //           stack's plan admits only scales that are zero or powers of two
 //           in [2^-23, 2^13]). Matrix-core rows m and m + 8 then hold the
 //           even and the odd chunks of the same weight row.
+//   scales  a tile's f16 scales (8 rows x K / 32) are one or two contiguous
+//           runs of whole 16-byte pieces: two loads per lane bring them into
+//           the wave's LDS (double-buffered: the next tile's arrive while
+//           this one's steps run), and each step reads its lane's scale
+//           there. One 16-bit load per lane and step cost as much address
+//           work as the step's weight load (92 vs 84 us per gate/up launch
+//           at 16 tokens of gpt-oss-120b).
 //   B       the group's inputs (xb of each assignment's token, or h of each
 //           assignment) as two f16 terms, in columns 2j and 2j + 1 for the
 //           even chunks and 8 + 2j, 9 + 2j for the odd ones (two LDS regions
@@ -56,9 +63,10 @@ constexpr int kGCols = 2 * kGT;            // B columns (hi, lo per assignment)
 constexpr int kGMaxN = 64;                 // assignments per call (one wave builds the table)
 constexpr int kGMaxK = 3072;               // hidden and ffn
 constexpr int kGE = kGMaxK / kGThreads;    // staged B elements per thread and column
-constexpr int kPD = 6;                     // K steps in flight per wave (a tile's steps: a multiple)
+constexpr int kPD = 4;                     // K steps in flight per wave (a tile's steps: a multiple)
 constexpr int kTW = 4;                     // tiles per wave
 constexpr int kTB = kTW * kGW;             // tiles per block
+constexpr int kGLdsMax = 80 * 1024;        // LDS per block (two blocks per CU)
 
 struct GrpArgs {
     const uint8_t *experts;   // the layer's expert table
@@ -81,16 +89,18 @@ __host__ __device__ inline int grp_nq(int K) { return ((K / 32 + 7) / 8 + kPD - 
 __host__ __device__ inline int grp_kh(int K) { return grp_nq(K) * 128 + 8; }
 
 // LDS of a block (bytes, 16-aligned parts): B (two regions of kGCols
-// columns), the staged biases (8 per tile), the group table.
+// columns), the staged biases (8 per tile), the group table, and per wave
+// two tiles' weight scales (16 K / 32 bytes each).
 struct GrpLds {
-    size_t b, bias, tab, total;
+    size_t b, bias, tab, sc, total;
 };
 __host__ __device__ inline GrpLds grp_lds(int K) {
     GrpLds L;
     L.b = 0;
     L.bias = L.b + (size_t)2 * kGCols * grp_kh(K) * 2;
     L.tab = L.bias + (size_t)kTB * 8 * 4;
-    L.total = L.tab + (size_t)(5 * kGMaxN + 8 + 2 * kGT) * 4;
+    L.sc = (L.tab + (size_t)(5 * kGMaxN + 8 + 2 * kGT) * 4 + 15) & ~(size_t)15;
+    L.total = L.sc + (size_t)kGW * 2 * 16 * (K / 32);
     return L;
 }
 
@@ -105,12 +115,13 @@ __device__ __forceinline__ float grp_act(float g, float u, float alpha, float li
 
 // MODE 0: gate/up (K = H, tiles of 4 pairs); MODE 1: down (K = F, tiles of
 // 8 rows).
-// Two blocks per CU (their LDS fits twice) at four waves per SIMD: the
-// register budget this asks for keeps the conversion work of some waves
-// under the memory waits of others (at 3 waves per SIMD, 101 vs 92 us per
-// gate/up launch at 16 tokens of gpt-oss-120b).
+// Two blocks per CU (their LDS fits twice) at four waves per SIMD (the
+// launch bound's second argument, the minimum waves per SIMD, caps the
+// registers at 128): the conversion work of some waves runs under the memory
+// waits of others (at 3 waves per SIMD, 101 vs 92 us per gate/up launch at
+// 16 tokens of gpt-oss-120b).
 template <int MODE>
-__global__ void __launch_bounds__(kGThreads, 2) k_grouped(GrpArgs A) {
+__global__ void __launch_bounds__(kGThreads, 4) k_grouped(GrpArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int K = MODE == 0 ? A.H : A.F;
     const int C = K / 32;   // 16-byte chunks per row
@@ -176,26 +187,45 @@ __global__ void __launch_bounds__(kGThreads, 2) k_grouped(GrpArgs A) {
     const mh_rsrc rex = gemv_rsrc(A.experts, A.layer_bytes);
     const int m = lane & 15, gq = lane >> 4;
     const int r8 = m & 7, par = m >> 3;   // this lane's weight row in the tile, chunk parity
-    const uint32_t rowbytes = (uint32_t)C * 16u, srow = (uint32_t)C * 2u;
+    const uint32_t rowbytes = (uint32_t)C * 16u;
     const uint32_t eo = (uint32_t)sGexp[g] * A.stride;
     // this wave's tiles [tw0, tw1) (none past the block's last)
     const int tw0 = min(tb0 + wave * kTW, tb1), tw1 = min(tw0 + kTW, tb1);
     const int nt = tw1 - tw0;
 
-    // this lane's row of a tile: byte offsets of its data and scales
-    auto tile_rows = [&](int tile, uint32_t &rd, uint32_t &rs) {
-        uint32_t row, od, os;
+    // this lane's row of a tile: the byte offset of its data
+    auto tile_row = [&](int tile) -> uint32_t {
+        uint32_t row, od;
         if constexpr (MODE == 0) {
             row = 4u * (uint32_t)tile + (uint32_t)(r8 & 3);
             od = r8 < 4 ? A.off[0] : A.off[3];
-            os = r8 < 4 ? A.off[1] : A.off[4];
         } else {
             row = 8u * (uint32_t)tile + (uint32_t)r8;
             od = A.off[6];
-            os = A.off[7];
         }
-        rd = eo + od + row * rowbytes;
-        rs = eo + os + row * srow;
+        return eo + od + row * rowbytes;
+    };
+    // a tile's scales: C 16-byte pieces (gate/up: the 4 gate rows' run, then
+    // the 4 up rows'; down: the 8 rows' run; 16-aligned since C is even),
+    // kept in LDS with row r8 at byte 2 C r8
+    uint8_t *sScW = lds + Ld.sc + (size_t)wave * 2 * 16 * C;   // this wave's two buffers
+    auto sc_load = [&](int tile, mh_u4 (&v)[2]) __attribute__((always_inline)) {
+        const uint32_t ut = (uint32_t)tile, uc = (uint32_t)C;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t p = (uint32_t)min(lane + 64 * u, C - 1);
+            uint32_t a;
+            if constexpr (MODE == 0)
+                a = p < uc / 2 ? eo + A.off[1] + ut * 8u * uc + 16u * p : eo + A.off[4] + ut * 8u * uc + 16u * (p - uc / 2);
+            else
+                a = eo + A.off[7] + ut * 16u * uc + 16u * p;
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rex, a, 0, 0);
+        }
+    };
+    auto sc_store = [&](int buf, const mh_u4 (&v)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (lane + 64 * u < C) *(mh_u4 *)(sScW + (size_t)buf * 16 * C + 16 * (lane + 64 * u)) = v[u];
     };
 
     // the ring: step s's chunk in slot s % kPD (the cursors advance by
@@ -203,24 +233,18 @@ __global__ void __launch_bounds__(kGThreads, 2) k_grouped(GrpArgs A) {
     // merged into a store through a chosen pointer, which keeps the counters
     // in scratch memory)
     mh_u4 qa[kPD];
-    uint16_t qs[kPD];   // (16 bits: a wider type is zero-extended where the ring crosses a loop edge, which waits for every load in flight)
     int t_p = min(max(tw0, tb0), tb1 - 1), q_p = 0;   // (a wave with no tiles reads one, unused)
-    uint32_t rd_p, rs_p;
-    tile_rows(t_p, rd_p, rs_p);
+    uint32_t rd_p = tile_row(t_p);
     auto issue = [&](int j) __attribute__((always_inline)) {
         const uint32_t cc = (uint32_t)min(8 * q_p + 2 * gq + par, C - 1);   // past K: a repeat (B is zero there)
         // (cached loads: non-temporal ones were slower here, 117 vs 102 us per
         // gate/up launch at 16 tokens of gpt-oss-120b)
         qa[j] = __builtin_amdgcn_raw_buffer_load_b128(rex, rd_p + 16u * cc, 0, 0);
-        qs[j] = __builtin_amdgcn_raw_buffer_load_b16(rex, rs_p + 2u * cc, 0, 0);
         const bool wrap = q_p == NQ - 1;
         const bool adv = wrap && t_p + 1 < tw1;   // past the wave's tiles: the last again
         q_p = wrap ? 0 : q_p + 1;
         t_p = adv ? t_p + 1 : t_p;
-        uint32_t nd, ns;
-        tile_rows(t_p, nd, ns);
-        rd_p = nd;
-        rs_p = ns;
+        rd_p = tile_row(t_p);
     };
 
     // ---------------------------------------------------------- B
@@ -253,7 +277,10 @@ __global__ void __launch_bounds__(kGThreads, 2) k_grouped(GrpArgs A) {
             else
                 biasv[u] = ((const float *)(eb + A.off[8]))[8 * btile + br];
         }
+        mh_u4 sc0[2];   // the wave's first tile's scales
+        sc_load(t_p, sc0);
         for (int j = 0; j < kPD; ++j) issue(j);
+        sc_store(0, sc0);
 #pragma unroll
         for (int u = 0; u < kBP; ++u)
             if (t + u * kGThreads < kTB * 8) sBias[t + u * kGThreads] = biasv[u];
@@ -318,13 +345,20 @@ __global__ void __launch_bounds__(kGThreads, 2) k_grouped(GrpArgs A) {
     // constant), the accumulators live in the matrix-core registers across
     // them, and the outputs follow the tile's last group.
     for (int tile = tw0; tile < tw1; ++tile) {
+        const int buf = (tile - tw0) & 1;
+        mh_u4 scn[2];   // the next tile's scales (the wave's last tile re-reads its own, unused)
+        sc_load(min(tile + 1, tw1 - 1), scn);
+        const uint16_t *scr = (const uint16_t *)(sScW + (size_t)buf * 16 * C) + r8 * C;   // this lane's row
         v4f acc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
         for (int q0 = 0; q0 < NQ; q0 += kPD) {
+            uint16_t scq[kPD];
+#pragma unroll
+            for (int j = 0; j < kPD; ++j) scq[j] = scr[min(8 * (q0 + j) + 2 * gq + par, C - 1)];
 #pragma unroll
             for (int j = 0; j < kPD; ++j) {
-                const float sc = mh_f16(qs[j]);
+                const float sc = mh_f16(scq[j]);
                 const _Float16 *bp = bcol + 128 * (q0 + j);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -335,6 +369,7 @@ __global__ void __launch_bounds__(kGThreads, 2) k_grouped(GrpArgs A) {
                 issue(j);
             }
         }
+        sc_store(buf ^ 1, scn);   // the wave reads its own LDS in order: no barrier
         // ---- the tile's outputs
         const int tl = tile - tb0;   // the tile's place in the staged biases
         const v4f accs = (acc[0] + acc[1]) + (acc[2] + acc[3]);
@@ -373,10 +408,11 @@ __global__ void __launch_bounds__(kGThreads, 2) k_grouped(GrpArgs A) {
 
 bool grouped_ok(const DevLayer &L, int n) {
     const int64_t N = (int64_t)n * L.top_k;
-    return L.expert_dt == MH_DT_MXFP4 && n >= 2 && N <= kGMaxN && L.hidden % 32 == 0 && L.ffn % 32 == 0 &&
+    return L.expert_dt == MH_DT_MXFP4 && n >= 2 && N <= kGMaxN && L.hidden % 64 == 0 && L.ffn % 64 == 0 &&
            L.hidden <= kGMaxK && L.ffn <= kGMaxK &&
            L.expert_stride % 16 == 0 && L.expert_stride * (uint64_t)L.n_experts < (1ull << 32) &&
            (uintptr_t)L.experts % 16 == 0 && L.off[0] % 16 == 0 && L.off[3] % 16 == 0 && L.off[6] % 16 == 0 &&
+           L.off[1] % 16 == 0 && L.off[4] % 16 == 0 && L.off[7] % 16 == 0 &&
            L.off[2] % 4 == 0 && L.off[5] % 4 == 0 && L.off[8] % 4 == 0;
 }
 
@@ -399,14 +435,14 @@ int launch_grouped(const DevLayer &L, int n, const int32_t *order, const float *
     A.act_plain = L.act_plain;
     A.order = order;
     const GrpLds l0 = grp_lds(A.H), l1 = grp_lds(A.F);
-    if (l0.total > 64 * 1024 || l1.total > 64 * 1024)
+    if (l0.total > kGLdsMax || l1.total > kGLdsMax)
         return fail(MH_E_UNSUPPORTED, "grouped expert path: LDS of %zu / %zu bytes per block", l0.total, l1.total);
     static int ready_dev = -1;
     int dev = 0;
     MH_HIP(hipGetDevice(&dev));
     if (ready_dev != dev) {
-        MH_HIP(hipFuncSetAttribute((const void *)k_grouped<0>, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
-        MH_HIP(hipFuncSetAttribute((const void *)k_grouped<1>, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+        MH_HIP(hipFuncSetAttribute((const void *)k_grouped<0>, hipFuncAttributeMaxDynamicSharedMemorySize, kGLdsMax));
+        MH_HIP(hipFuncSetAttribute((const void *)k_grouped<1>, hipFuncAttributeMaxDynamicSharedMemorySize, kGLdsMax));
         ready_dev = dev;
     }
     // groups <= assignments: blocks (x, g) for g past the groups exit
