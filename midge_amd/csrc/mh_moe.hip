@@ -334,8 +334,13 @@ k_combine_norm(float *__restrict__ x, const float *__restrict__ ye, const float 
 //   writes its x back (every block of the token has read it by then); the
 //   launch's last ranked token writes the order. Counters are left at zero.
 constexpr int kCRRows = 16;       // router rows per block (one per wave)
-constexpr int kCRChunks = 12;     // 16-byte router chunks per lane
 constexpr int kCRMaxH = 3072;     // hidden (3 elements per thread)
+// 16-byte chunks of a router row per lane: a row of kCRMaxH elements (int8:
+// 3, f32: 12; loads past the row would re-read its last chunk)
+template <int DT>
+constexpr int cr_chunks() {
+    return (kCRMaxH / mh_chunk<DT>::E + 63) / 64;
+}
 
 struct CombineRouteArgs {
     float *x;              // [n][H] residual (combined in place)
@@ -375,6 +380,7 @@ __global__ void __launch_bounds__(1024) k_combine_route(CombineRouteArgs A) {
     const bool has_row = e < E;   // wave-uniform
     const mh_rsrc rr = gemv_rsrc(A.rw, (uint32_t)E * (uint32_t)C * 16u);
     const int er = min(e, E - 1);
+    constexpr int kCRChunks = cr_chunks<DT>();
     mh_u4 q[kCRChunks];
 #pragma unroll
     for (int j = 0; j < kCRChunks; ++j) {
@@ -609,9 +615,10 @@ int launch_topk(const float *rl, const float *bias, int n, int E, int k, int rou
 // take. ye / wprev null: the first layer (no combine).
 bool combine_route_ok(const DevLayer &L, int n) {
     const int CE = L.router.dt == MH_DT_Q8R ? 16 : 4;
+    const int chunks = L.router.dt == MH_DT_Q8R ? cr_chunks<MH_DT_Q8R>() : cr_chunks<MH_DT_F32>();
     return (L.router.dt == MH_DT_Q8R || L.router.dt == MH_DT_F32) && n >= 1 && n <= 16 &&
            n * L.top_k <= kMaxOrder && L.hidden <= kCRMaxH && L.hidden % CE == 0 &&
-           L.hidden / CE <= 64 * kCRChunks && L.n_experts <= kMaxExperts && (uintptr_t)L.router.data % 16 == 0 &&
+           L.hidden / CE <= 64 * chunks && L.n_experts <= kMaxExperts && (uintptr_t)L.router.data % 16 == 0 &&
            (uint64_t)L.n_experts * (uint64_t)L.hidden * (L.router.dt == MH_DT_Q8R ? 1u : 4u) < (1ull << 32);
 }
 
