@@ -34,7 +34,8 @@ def stream() -> int:
 
 def set_switch(name: str, on: bool) -> None:
     """mh_set_switch: a path switch ("NO_MFMA", "NO_FUSED", "ATTN_SPLIT",
-    "COOP", "Q8_NO_ROWS") on or off for the calls that follow."""
+    "COOP", "Q8_NO_ROWS", "BATCH_GEMV", "SPLIT_ROUTE") on or off for the
+    calls that follow."""
     _lib.call("mh_set_switch", name.encode(), 1 if on else 0)
 
 
