@@ -5,13 +5,13 @@ matvec, over a run of positions past a sliding window (the ring wraps), at
 gpt-oss's layer shapes (3 layers: sliding, full, sliding; 32 MXFP4 experts,
 top-4; 64/8 heads of 64 with sinks and YaRN).
 
-The checker runs on the compiled reference's scalar build, which equals the
-oracle bit for bit (shown here at the first position; the oracle's scalar
-C takes seconds per position at these widths). The bar per position is the
-reference's own divergence: the same composition on its AVX2 build against
-the scalar one. Logits and the final residual are held to max(1e-3, twice
-that divergence) in relative L2, and every layer's expert selection must
-equal the checker's."""
+The expected values come from the compiled reference's scalar build, which
+equals the oracle bit for bit (shown here at the first position; the
+oracle's scalar C takes seconds per position at these widths). The bar per
+position is the reference's own divergence: the same composition on its
+AVX2 build against the scalar one. Logits and the final residual are held
+to max(1e-3, twice that divergence) in relative L2, and every layer's expert
+selection must equal the scalar build's."""
 import ctypes as C
 
 import numpy as np

@@ -380,7 +380,7 @@ def attn_divergence_gptoss() -> np.ndarray:
 def test_attention_divergence_fixture():
     # the per-position AVX2-vs-scalar divergence the GPU attention test's bar
     # is built from: recomputed from the compiled reference, equal to the
-    # committed fixture (which the GPU box reads)
+    # committed fixture (which the GPU test reads where the reference is absent)
     if not po.have_ref():
         pytest.skip("reference engine not built (oracle/_ref)")
     div = attn_divergence_gptoss()
