@@ -197,6 +197,11 @@ __device__ __forceinline__ mh_gbytes mh_global(const void *p) { return (mh_gbyte
 __device__ __forceinline__ mh_u4 mh_load16(mh_gbytes p) {
     return __builtin_nontemporal_load((const mh_u4 __attribute__((address_space(1))) *)p);
 }
+// The same through the caches: for lines that several load instructions
+// share (a non-temporal line can be fetched again for each of them).
+__device__ __forceinline__ mh_u4 mh_load16_cached(mh_gbytes p) {
+    return *(const mh_u4 __attribute__((address_space(1))) *)p;
+}
 __device__ __forceinline__ uint32_t mh_load_u16(mh_gbytes p) {
     return *(const uint16_t __attribute__((address_space(1))) *)p;
 }
