@@ -5,10 +5,13 @@
 //
 //   lists      assignments (token t, slot i) grouped by expert: counts,
 //              offsets, token of each list position, slot of each position
-//   quantize   xb (per token) -> kTerms planes of fp8 e4m3 with an e8m0
+//   quantize   xb (per token) -> kTerms planes of fp6 e2m3 with an e8m0
 //              scale per 32-element block: x = sum_t q_t * 2^e_t, each term
-//              the rounding residual of the previous one (3 terms keep the
-//              f32 GEMM's accuracy to ~1.5e-5 relative)
+//              the rounding residual of the previous one (each shrinks the
+//              block's largest residual by >= 2^-4). fp4 x fp6 runs the
+//              instruction at twice the rate of fp4 x fp8 (measured 8.1
+//              against 4.3 PFLOP/s), and an e2m3 term reduces a block's
+//              residual as much as an e4m3 one.
 //   gate/up    per (expert, 32-row tile): A = the fp4 gate and up rows
 //              verbatim (e2m1 nibbles) with e8m0 scales taken exactly from
 //              the f16 powers of two; B = the quantized tokens of the
@@ -19,21 +22,16 @@
 //              assignment's slot; the existing prefill combine then adds
 //              w * y to each token in ascending expert order.
 //
-// Operand layout of the 32x32x64 instruction (measured on gfx950): lane l
-// holds A row l % 32 and B column l % 32; with g = l / 32, A's 16 bytes (32
-// e2m1 values) and B's 32 bytes (32 e4m3 values) pair as
-//   K  0-15: A group 0 nibbles  0-15,  B group 0 bytes  0-15
-//   K 16-31: A group 1 nibbles  0-15,  B group 0 bytes 16-31
-//   K 32-47: A group 0 nibbles 16-31,  B group 1 bytes  0-15
-//   K 48-63: A group 1 nibbles 16-31,  B group 1 bytes 16-31
-// and the scale blocks of both operands follow A: lane (., g)'s scale covers
-// K 0-15 + 32-47 (g = 0) or K 16-31 + 48-63 (g = 1). So for K step s (weight
-// columns 64s .. 64s+63) A lane (m, g) loads 16-byte chunk 2s+g of row m (one
-// MXFP4 block and its scale); B lane (n, g) loads columns 64s+16g+[0,16) and
-// 64s+32+16g+[0,16) of token n with the scale of column block 2s+g. The
-// activations are therefore quantized in natural 32-column blocks, like the
-// weights. Output lane l: column l % 32, rows 8(i/4) + 4g + i%4 for
-// accumulator i.
+// Operand layout of the 32x32x64 instruction with fp4 A and fp6 B
+// (measured on gfx950 with one-hot operands): lane l holds A row l % 32 and
+// B column l % 32; with g = l / 32, A's 16 bytes (32 e2m1 values) and B's 24
+// bytes (32 e2m3 values, 6 bits each from the lowest bit up) are columns
+// 32 g .. 32 g + 31 of the step, in order, and each lane's scale covers its
+// own 32 columns. So for K step s (weight columns 64s .. 64s+63) A lane
+// (m, g) loads 16-byte chunk 2s+g of row m (one MXFP4 block and its scale)
+// and B lane (n, g) block 2s+g of token n with its scale: activations are
+// quantized in natural 32-column blocks, like the weights. Output lane l:
+// column l % 32, rows 8(i/4) + 4g + i%4 for accumulator i.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -45,12 +43,14 @@ namespace mh {
 
 namespace {
 
-constexpr int kTerms = 3;      // fp8 terms per activation
+constexpr int kTerms = 3;      // fp6 terms per activation
 constexpr int kNT = 4;         // 32-token tiles per pass (weights loaded once per pass)
 constexpr int kWaves = 4;      // 32-row tiles per block (one per wave)
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v6i __attribute__((ext_vector_type(6)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 // ---------------------------------------------------------------- lists
 
@@ -114,16 +114,22 @@ k_plist_one(const int32_t *sel, int N, int E, int k, int *rank, int *offs, int *
 
 // ---------------------------------------------------------------- quantize
 
-// e such that m * 2^-e <= 448 (the largest e4m3 value), as small as possible.
-__device__ __forceinline__ int fp8_block_exp(float m) {
+// e such that m * 2^-e <= 7.5 (the largest e2m3 value), as small as possible.
+__device__ __forceinline__ int fp6_block_exp(float m) {
     int km;
     const float fm = frexpf(m, &km);   // m = fm * 2^km, fm in [0.5, 1)
-    return fm <= 0.875f ? km - 9 : km - 8;
+    return fm <= 0.9375f ? km - 3 : km - 2;
 }
 
 // Rows of K f32 (row r of the input = in[(map ? map[r] : r) * K ...]) ->
-// kTerms planes q[t][r][K] (e4m3) and sc[t][r][scs] (e8m0, scs >= K / 32: rows
-// padded to 16 bytes), one scale per 32-column block b (thread = (row, block)).
+// kTerms planes q[t][r][K] and sc[t][r][scs] (e8m0, scs >= K / 32: rows
+// padded to 16 bytes), one scale 2^e per 32-column block b (thread = (row,
+// block)). Block b of a plane is 32 bytes at 32 b: its 32 e2m3 codes, 6 bits
+// each from the lowest bit up in column order (24 bytes), then 8 zero bytes.
+// Each term is the previous residual divided by 2^e and rounded by the
+// hardware converter, which interleaves its two 16-value inputs (even
+// columns, odd columns); its values come back exactly from the inverse
+// converter, so the residuals are exact. A zero block keeps e = 0.
 __global__ void __launch_bounds__(256)
 k_quant_terms(const float *__restrict__ in, const int *__restrict__ map, int rows, int K,
               uint8_t *__restrict__ q, uint8_t *__restrict__ sc, int scs) {
@@ -143,24 +149,21 @@ k_quant_terms(const float *__restrict__ in, const int *__restrict__ map, int row
         float m = 0.f;
 #pragma unroll
         for (int j = 0; j < 32; ++j) m = fmaxf(m, fabsf(v[j]));
-        int e = m > 0.f ? fp8_block_exp(m) : -127;
-        e = max(-127, min(127, e));
-        const float inv = ldexpf(1.0f, -e), scl = ldexpf(1.0f, e);
-        uint32_t w[8];
+        const int e = m > 0.f ? max(-126, min(127, fp6_block_exp(m))) : 0;
+        const float scl = ldexpf(1.0f, e);
+        v16f ev, od;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            int word = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * j] * inv, v[4 * j + 1] * inv, 0, false);
-            word = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * j + 2] * inv, v[4 * j + 3] * inv, word, true);
-            w[j] = (uint32_t)word;
-            // the term's values back in f32 (exact), and the residuals (exact)
-            v[4 * j + 0] = v[4 * j + 0] - __builtin_amdgcn_cvt_f32_fp8(word, 0) * scl;
-            v[4 * j + 1] = v[4 * j + 1] - __builtin_amdgcn_cvt_f32_fp8(word, 1) * scl;
-            v[4 * j + 2] = v[4 * j + 2] - __builtin_amdgcn_cvt_f32_fp8(word, 2) * scl;
-            v[4 * j + 3] = v[4 * j + 3] - __builtin_amdgcn_cvt_f32_fp8(word, 3) * scl;
+        for (int j = 0; j < 16; ++j) {
+            ev[j] = v[2 * j];
+            od[j] = v[2 * j + 1];
         }
+        const v6i w = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, scl);
+        const v32f back = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(w, scl);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] -= back[j];
         uint8_t *qr = q + ((int64_t)t * rows + r) * K + 32 * b;
-        *(uint4 *)qr = make_uint4(w[0], w[1], w[2], w[3]);
-        *(uint4 *)(qr + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+        *(uint4 *)qr = make_uint4((uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]);
+        *(uint4 *)(qr + 16) = make_uint4((uint32_t)w[4], (uint32_t)w[5], 0u, 0u);
         sc[((int64_t)t * rows + r) * scs + b] = (uint8_t)(e + 127);
     }
 }
@@ -292,8 +295,9 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
         // so one load instruction reads 64 contiguous bytes (a K step) of
         // each of 16 tokens. Thread tid loads piece tid (t = tid / 128) and,
         // in waves 0-1, piece tid + 256 (t = 2), both of token n = (tid / 4)
-        // % 32 and quarter c = tid % 4; the store puts quarter c = g + 2 half
-        // into the operand slot (t, j, half) lane 32 g + n. Only the pass's
+        // % 32 and quarter c = tid % 4; the store puts quarter c = 2 g + half
+        // (block 2s + g, its bytes 16 half .. 16 half + 15) into the operand
+        // slot (t, j, half) lane 32 g + n. Only the pass's
         // nt tiles are loaded; list positions past T read position T - 1
         // (their columns are not stored).
         const int bc = tid & 3, bn = (tid >> 2) & 31, bt = tid >> 7;
@@ -306,7 +310,7 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
             const int br = MODE == 0 ? A.list_tok[base + p] : base + p;
             bsrc[j] = A.bq + (size_t)br * K + 16 * bc;
         }
-        auto bdst = [&](int t, int j) { return ((t * kNT + j) * 2 + (bc >> 1)) * 64 + 32 * (bc & 1) + bn; };
+        auto bdst = [&](int t, int j) { return ((t * kNT + j) * 2 + (bc & 1)) * 64 + 32 * (bc >> 1) + bn; };
         // the pass's activation scales, all of K: rows (term, token) of scs
         // bytes in memory (16-byte pieces) into LDS rows of bss bytes; the
         // previous pass ended with a barrier, so bsc is free
@@ -408,10 +412,10 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
                 if (j + 1 < NTT) rd(j + 1, (j + 1) & 1);
 #pragma unroll
                 for (int t = 0; t < kTerms; ++t) {
-                    acc0[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa0, qb[j & 1][t], acc0[j], 4, 0, 0, sa0,
+                    acc0[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa0, qb[j & 1][t], acc0[j], 4, 2, 0, sa0,
                                                                              0, sbv[j & 1][t]);
                     if constexpr (MODE == 0)
-                        acc1[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa1, qb[j & 1][t], acc1[j], 4, 0, 0,
+                        acc1[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa1, qb[j & 1][t], acc1[j], 4, 2, 0,
                                                                                  sa1, 0, sbv[j & 1][t]);
                 }
             }
