@@ -819,7 +819,7 @@ def config_probes(ev, s, seed: int, reps: int = 40) -> dict:
     return out
 
 
-MFMA_FP8_PEAK_TFLOPS = 5000.0   # dense fp8 MFMA (the rate of fp4 x fp8 operands)
+MFMA_FP6_PEAK_TFLOPS = 10100.0  # dense fp6 / fp4 MFMA (the rate of fp4 x fp6 operands, the prefill GEMM's)
 
 
 def prefill_probe(ev, s, seed: int, n: int = 512, reps: int = 10) -> dict:
@@ -877,7 +877,7 @@ def prefill_probe(ev, s, seed: int, n: int = 512, reps: int = 10) -> dict:
                 issued = 2.0 * tiles * 32 * 3 * shape.hidden * shape.ffn * 3   # 3 matrices x 3 activation terms
                 res.update({"kernels": kern, "useful_TFLOPs": useful_flops / (ms * 1e-3) / 1e12,
                             "gemm_issued_TFLOPs": issued / (gemm_us * 1e-6) / 1e12 if gemm_us else None,
-                            "mfma_util_of_fp8_peak": issued / (gemm_us * 1e-6) / 1e12 / MFMA_FP8_PEAK_TFLOPS
+                            "mfma_util_of_fp6_peak": issued / (gemm_us * 1e-6) / 1e12 / MFMA_FP6_PEAK_TFLOPS
                             if gemm_us else None})
             out[path] = res
         finally:

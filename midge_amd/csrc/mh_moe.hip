@@ -736,7 +736,7 @@ int run_decode_layer(const DevLayer &L, float *x, int n, const LayerBufs &b, uin
 // The scaled-MFMA grouped GEMM takes a chunk once its experts average at
 // least this many assignments: its 32-token tiles are then at least a
 // quarter full. Below that the per-assignment GEMVs do no more work, and
-// they keep f32 arithmetic (the GEMM carries activations as three fp8 terms,
+// they keep f32 arithmetic (the GEMM carries activations as three fp6 terms,
 // ~12 significant bits, and its instruction cuts each product to ~2^-13 of
 // the largest one it sums; a small, sharply peaked model can amplify that
 // to a few 1e-4 of relative error in its logits).
