@@ -66,9 +66,25 @@ struct RowOff {
     uint32_t data, scale;
 };
 
+// v of lane + K within the lane's row of 16 (0 past the row's end)
+template <int K>
+__device__ __forceinline__ float gemv_dpp_shl(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + K, 0xF, 0xF, false));
+}
+// v of lane ^ 1 and lane ^ 2 (quad permutations)
+__device__ __forceinline__ float gemv_dpp_x1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float gemv_dpp_x2(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+
 // Sums each row of red[nrows][C] (row-major) into out[row]. A wave takes 8
-// rows at a time: 8 lanes per row each add every 8th partial, then three
-// xor-shuffles combine them (a fixed order, so results are deterministic).
+// rows at a time: 8 lanes per row each add every 8th partial in column order,
+// then lane 0 of the 8 adds the others' sums as ((p0 + p1) + (p2 + p3)) +
+// ((p4 + p5) + (p6 + p7)): a fixed order, so results are deterministic. A
+// lane's partials are read in batches of 12 issued together (a read-add
+// loop would wait for each read in turn), then added in the same order.
 // Rows in `skip` (out[row] untouched) are those the caller marks invalid.
 // nw is the block's wave count, passed in: reading blockDim inside a
 // pipelined loop is a memory load whose wait also waits for every weight
@@ -76,16 +92,32 @@ struct RowOff {
 template <class Keep>
 __device__ __forceinline__ void block_reduce_rows(const float *red, int C, int nrows, int nw, float *out,
                                                   Keep keep) {
+    constexpr int kB = 12;   // partials read per batch
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rl = lane >> 3, part = lane & 7;
     for (int r0 = wave * 8; r0 < nrows; r0 += nw * 8) {
         const int r = r0 + rl;
         float s = 0.f;
-        if (r < nrows)
-            for (int cc = part; cc < C; cc += 8) s += red[r * C + cc];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
+        if (r < nrows) {
+            const float *rr = red + r * C;
+            int cc = part;
+            for (; cc + 8 * (kB - 1) < C; cc += 8 * kB) {
+                float v[kB];
+#pragma unroll
+                for (int i = 0; i < kB; ++i) v[i] = rr[cc + 8 * i];
+#pragma unroll
+                for (int i = 0; i < kB; ++i) s += v[i];
+            }
+            float v[kB];
+#pragma unroll
+            for (int i = 0; i < kB; ++i) v[i] = cc + 8 * i < C ? rr[cc + 8 * i] : 0.f;
+#pragma unroll
+            for (int i = 0; i < kB; ++i)
+                if (cc + 8 * i < C) s += v[i];
+        }
+        s += gemv_dpp_x1(s);
+        s += gemv_dpp_x2(s);
+        s += gemv_dpp_shl<4>(s);
         if (part == 0 && r < nrows && keep(r)) out[r] = s;
     }
 }
