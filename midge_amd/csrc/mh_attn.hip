@@ -643,18 +643,8 @@ __device__ __forceinline__ void a1_math(const mh_u4 (&q)[U][2], int nr, int C, c
         if (act && j < nr) red[j * C + c] = d;
     }
     __syncthreads();
-    // row sums: 8 lanes per row, then 3 xor-shuffles (fixed order)
-    const int wave = t >> 6, lane = t & 63, rl = lane >> 3, part = lane & 7;
-    for (int rr = wave * 8; rr < nr; rr += (kA1Threads / 64) * 8) {
-        const int r = rr + rl;
-        float s = 0.f;
-        if (r < nr)
-            for (int cc = part; cc < C; cc += 8) s += red[r * C + cc];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
-        if (part == 0 && r < nr) out[r] = s;
-    }
+    // row sums: 8 lanes per row in column order, then a fixed combine
+    block_reduce_rows(red, C, nr, kA1Threads / 64, out, [](int) { return true; });
     __syncthreads();
 }
 
