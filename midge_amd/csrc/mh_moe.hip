@@ -26,6 +26,33 @@ constexpr int kMaxExperts = 1024;  // one wave holds 16 logits per lane
 // The top-k of one token's logits rl[E] by one whole wave (every lane calls
 // it); lane 0 writes sel[k], w[k] and the usage counts. PER logits per lane
 // (E <= 64 PER).
+// Wave max (min) of v over all 64 lanes, returned to every lane: quad,
+// half-row and row mirrors, then the row broadcasts (lane 63 ends with the
+// whole wave's), then lane 63 read out.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_i(int x) {
+    return __builtin_amdgcn_update_dpp(x, x, CTRL, ROWS, 0xF, false);   // lanes without a source keep x
+}
+__device__ __forceinline__ float dpp_max(float v, int o) { return fmaxf(v, __int_as_float(o)); }
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = dpp_max(v, dpp_i<0xB1, 0xF>(__float_as_int(v)));
+    v = dpp_max(v, dpp_i<0x4E, 0xF>(__float_as_int(v)));
+    v = dpp_max(v, dpp_i<0x141, 0xF>(__float_as_int(v)));
+    v = dpp_max(v, dpp_i<0x140, 0xF>(__float_as_int(v)));
+    v = dpp_max(v, dpp_i<0x142, 0xA>(__float_as_int(v)));
+    v = dpp_max(v, dpp_i<0x143, 0xC>(__float_as_int(v)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ int wave_min_dpp(int v) {
+    v = min(v, dpp_i<0xB1, 0xF>(v));
+    v = min(v, dpp_i<0x4E, 0xF>(v));
+    v = min(v, dpp_i<0x141, 0xF>(v));
+    v = min(v, dpp_i<0x140, 0xF>(v));
+    v = min(v, dpp_i<0x142, 0xA>(v));
+    v = min(v, dpp_i<0x143, 0xC>(v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 template <int PER>
 __device__ __forceinline__ void wave_topk_token(const float *rl, const float *__restrict__ bias, int E, int k,
                                                 int router_norm, int unfilled, int32_t *__restrict__ sel,
@@ -56,16 +83,11 @@ __device__ __forceinline__ void wave_topk_token(const float *rl, const float *__
                 bi = lane + 64 * j;
             }
         }
-        // wave argmax: larger value, then lower index
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            float ov = __shfl_xor(bv, o, 64);
-            int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        // wave argmax: the largest value, then the lowest index among the
+        // lanes holding it, then that lane's own value (DPP steps, no LDS)
+        const float wm = wave_max_dpp(bv);
+        bi = wave_min_dpp(bv == wm ? bi : INT32_MAX);
+        bv = bi == INT32_MAX ? -1e30f : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), bi & 63));
         if (bi == INT32_MAX) {
             val[i] = -1e30f;
             idx[i] = unfilled;
@@ -118,6 +140,41 @@ __device__ __forceinline__ void wave_topk_token(const float *rl, const float *__
 // Assignments a block can sort (16 tokens of up to kMaxTopK slots).
 constexpr int kMaxOrder = 16 * kMaxTopK;
 
+// Rank of key ki among the N distinct keys in sk (LDS): the keys are read in
+// batches of 16 issued together (a read-compare loop waits for each read).
+__device__ __forceinline__ int key_rank(const int *sk, int N, int ki) {
+    int r = 0;
+    for (int j0 = 0; j0 < N; j0 += 16) {
+        int kv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) kv[j] = j0 + j < N ? sk[j0 + j] : INT32_MAX;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) r += kv[j] < ki;
+    }
+    return r;
+}
+
+// moe = sum_i w[i] y_i[r] over a token's k slots in slot order, each product
+// and sum rounded separately (engine/midge.c:514, 544). The slots' y values
+// are read in batches of 4 issued together, then added in slot order.
+__device__ __forceinline__ float slot_sum(const float *__restrict__ w, const float *__restrict__ ye, int64_t H,
+                                          int k, int64_t r) {
+#pragma clang fp contract(off)
+    float moe = 0.f;
+    for (int i0 = 0; i0 < k; i0 += 4) {
+        float yv[4], wv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            yv[i] = i0 + i < k ? ye[(size_t)(i0 + i) * H + r] : 0.f;
+            wv[i] = i0 + i < k ? w[i0 + i] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i0 + i < k) moe = moe + wv[i] * yv[i];
+    }
+    return moe;
+}
+
 // One wave per token. With `order` (one block holding all n tokens, n k <=
 // kMaxOrder), the block then sorts the assignments by expert id, stably,
 // unroutable slots last: order[r] = assignment a, order[n k + r] = sel[a].
@@ -143,8 +200,7 @@ k_topk(const float *__restrict__ rl, const float *__restrict__ bias, int n, int 
     __syncthreads();
     for (int i = threadIdx.x; i < N; i += blockDim.x) {
         const int ki = skey[i];
-        int r = 0;
-        for (int j = 0; j < N; ++j) r += skey[j] < ki;
+        const int r = key_rank(skey, N, ki);
         order[r] = i;
         order[N + r] = ki / N < E ? ki / N : -1;
     }
@@ -287,9 +343,7 @@ k_combine_decode(float *__restrict__ x, const float *__restrict__ ye, const floa
     const int t = blockIdx.y;
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= H) return;
-    float moe = 0.f;
-    for (int i = 0; i < k; ++i)
-        moe = moe + w[(size_t)t * k + i] * ye[((size_t)t * k + i) * H + r];
+    const float moe = slot_sum(w + (size_t)t * k, ye + (size_t)t * k * H, H, k, r);
     x[(size_t)t * H + r] = x[(size_t)t * H + r] + moe;
 }
 
@@ -307,8 +361,7 @@ k_combine_norm(float *__restrict__ x, const float *__restrict__ ye, const float 
     float *xt = x + (size_t)t * H;
     float s = 0.f;
     for (int64_t r = threadIdx.x; r < H; r += blockDim.x) {
-        float moe = 0.f;
-        for (int i = 0; i < k; ++i) moe = moe + w[(size_t)t * k + i] * ye[((size_t)t * k + i) * H + r];
+        const float moe = slot_sum(w + (size_t)t * k, ye + (size_t)t * k * H, H, k, r);
         const float v = xt[r] + moe;
         xt[r] = v;
         s = __builtin_fmaf(v, v, s);
@@ -397,9 +450,7 @@ __global__ void __launch_bounds__(1024) k_combine_route(CombineRouteArgs A) {
         v[u] = 0.f;
         if (r < H) {
             if (A.ye) {
-                float moe = 0.f;
-                for (int i = 0; i < k; ++i) moe = moe + A.wprev[(size_t)t * k + i] * A.ye[((size_t)t * k + i) * H + r];
-                v[u] = xt[r] + moe;
+                v[u] = xt[r] + slot_sum(A.wprev + (size_t)t * k, A.ye + (size_t)t * k * H, H, k, r);
             } else {
                 v[u] = xt[r];
             }
@@ -489,8 +540,7 @@ __global__ void __launch_bounds__(1024) k_combine_route(CombineRouteArgs A) {
     __syncthreads();
     for (int i = tid; i < N; i += 1024) {
         const int ki = skey[i];
-        int r = 0;
-        for (int j = 0; j < N; ++j) r += skey[j] < ki;
+        const int r = key_rank(skey, N, ki);
         A.order[r] = i;
         A.order[N + r] = ki / N < E ? ki / N : -1;
     }
