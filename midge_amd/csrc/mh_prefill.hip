@@ -401,8 +401,8 @@ __global__ void __launch_bounds__(64 * kWaves) k_moe_gemm(GemmArgs A) {
 #pragma unroll
                 for (int t = 0; t < kTerms; ++t) {
                     const mh_u4 lo = bb[((t * kNT + j) * 2 + 0) * 64 + l];
-                    const mh_u4 hi = bb[((t * kNT + j) * 2 + 1) * 64 + l];
-                    qb[slot][t] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+                    const uint2 hi = *(const uint2 *)&bb[((t * kNT + j) * 2 + 1) * 64 + l];   // bytes 16-23 (fp6: 24 bytes)
+                    qb[slot][t] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, 0, 0};
                     sbv[slot][t] = bsc[(size_t)((t * kNT + j) * 32 + m) * bss + blk];
                 }
             };
