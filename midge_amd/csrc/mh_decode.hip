@@ -291,38 +291,6 @@ __device__ __forceinline__ void st_u32_dev(uint32_t *p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Maximum over the wave (every lane gets it): DPP within rows of 16, then
-// row broadcasts; lanes a DPP step does not write keep their value.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_max_step(float v) {
-    const int o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xF, false);
-    return fmaxf(v, __int_as_float(o));
-}
-__device__ __forceinline__ float wave_max(float v) {
-    v = dpp_max_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
-    v = dpp_max_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
-    v = dpp_max_step<0x141, 0xF>(v);   // row_half_mirror
-    v = dpp_max_step<0x140, 0xF>(v);   // row_mirror
-    v = dpp_max_step<0x142, 0xA>(v);   // row_bcast:15
-    v = dpp_max_step<0x143, 0xC>(v);   // row_bcast:31
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// Sum over the wave with DPP (the result is valid in lane 63): within rows
-// of 16, then the row broadcasts; rows a step does not write add 0.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add_step(float v) {
-    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
-}
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v = dpp_add_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
-    v = dpp_add_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
-    v = dpp_add_step<0x141, 0xF>(v);   // row_half_mirror
-    v = dpp_add_step<0x140, 0xF>(v);   // row_mirror
-    v = dpp_add_step<0x142, 0xA>(v);   // row_bcast:15
-    v = dpp_add_step<0x143, 0xC>(v);   // row_bcast:31
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
 // Stable top-k over the wave's E <= 64 * kEL logits (lane holds element
 // lane + 64 j in v[j]; absent elements are -inf): k rounds of "largest
 // remaining value, lowest index among equals"; only values > -1e30

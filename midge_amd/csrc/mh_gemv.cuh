@@ -66,19 +66,6 @@ struct RowOff {
     uint32_t data, scale;
 };
 
-// v of lane + K within the lane's row of 16 (0 past the row's end)
-template <int K>
-__device__ __forceinline__ float gemv_dpp_shl(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + K, 0xF, 0xF, false));
-}
-// v of lane ^ 1 and lane ^ 2 (quad permutations)
-__device__ __forceinline__ float gemv_dpp_x1(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float gemv_dpp_x2(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
-}
-
 // Sums each row of red[nrows][C] (row-major) into out[row]. A wave takes 8
 // rows at a time: 8 lanes per row each add every 8th partial in column order,
 // then lane 0 of the 8 adds the others' sums as ((p0 + p1) + (p2 + p3)) +
@@ -115,9 +102,9 @@ __device__ __forceinline__ void block_reduce_rows(const float *red, int C, int n
             for (int i = 0; i < kB; ++i)
                 if (cc + 8 * i < C) s += v[i];
         }
-        s += gemv_dpp_x1(s);
-        s += gemv_dpp_x2(s);
-        s += gemv_dpp_shl<4>(s);
+        s += dpp_x1(s);
+        s += dpp_x2(s);
+        s += dpp_shl<4>(s);
         if (part == 0 && r < nrows && keep(r)) out[r] = s;
     }
 }

@@ -297,3 +297,69 @@ __device__ __forceinline__ float mh_wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+
+// DPP lane exchanges (no LDS). A source lane outside the row mask, or past
+// the row for a shift, leaves the destination's own value (update_dpp's
+// `old` operand is the value itself) unless noted.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_keep(int x) {
+    return __builtin_amdgcn_update_dpp(x, x, CTRL, ROW_MASK, 0xF, false);
+}
+// v of lane + K within the lane's row of 16 (0 past the row's end)
+template <int K>
+__device__ __forceinline__ float dpp_shl(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + K, 0xF, 0xF, false));
+}
+// v of lane ^ 1, lane ^ 2 (quad permutations: every lane has a source)
+__device__ __forceinline__ float dpp_x1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_x2(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+
+// Maximum / minimum over the wave, returned to every lane: quad
+// permutations, half-row and row mirrors, then the row broadcasts (lane 63
+// ends with the wave's), then lane 63 read out.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    return fmaxf(v, __int_as_float(dpp_keep<CTRL, ROW_MASK>(__float_as_int(v))));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = dpp_max_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x141, 0xF>(v);   // row_half_mirror
+    v = dpp_max_step<0x140, 0xF>(v);   // row_mirror
+    v = dpp_max_step<0x142, 0xA>(v);   // row_bcast:15
+    v = dpp_max_step<0x143, 0xC>(v);   // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_min_step(int v) {
+    return min(v, dpp_keep<CTRL, ROW_MASK>(v));
+}
+__device__ __forceinline__ int wave_min(int v) {
+    v = dpp_min_step<0xB1, 0xF>(v);
+    v = dpp_min_step<0x4E, 0xF>(v);
+    v = dpp_min_step<0x141, 0xF>(v);
+    v = dpp_min_step<0x140, 0xF>(v);
+    v = dpp_min_step<0x142, 0xA>(v);
+    v = dpp_min_step<0x143, 0xC>(v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Sum over the wave with DPP (every lane gets lane 63's total): within rows
+// of 16, then the row broadcasts; rows a step does not write add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add_step(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = dpp_add_step<0x141, 0xF>(v);   // row_half_mirror
+    v = dpp_add_step<0x140, 0xF>(v);   // row_mirror
+    v = dpp_add_step<0x142, 0xA>(v);   // row_bcast:15
+    v = dpp_add_step<0x143, 0xC>(v);   // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}

@@ -29,11 +29,6 @@ __device__ __forceinline__ v8h fp4x8_f16(uint32_t w, float s) {
 __device__ __forceinline__ uint32_t dword_of(const mh_u4 &q, int j) {
     return j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
 }
-// v of lane + K within the lane's row of 16 (0 past the row's end)
-template <int K>
-__device__ __forceinline__ float dpp_shl(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + K, 0xF, 0xF, false));
-}
 
 }  // namespace
 }  // namespace mh

@@ -26,33 +26,6 @@ constexpr int kMaxExperts = 1024;  // one wave holds 16 logits per lane
 // The top-k of one token's logits rl[E] by one whole wave (every lane calls
 // it); lane 0 writes sel[k], w[k] and the usage counts. PER logits per lane
 // (E <= 64 PER).
-// Wave max (min) of v over all 64 lanes, returned to every lane: quad,
-// half-row and row mirrors, then the row broadcasts (lane 63 ends with the
-// whole wave's), then lane 63 read out.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ int dpp_i(int x) {
-    return __builtin_amdgcn_update_dpp(x, x, CTRL, ROWS, 0xF, false);   // lanes without a source keep x
-}
-__device__ __forceinline__ float dpp_max(float v, int o) { return fmaxf(v, __int_as_float(o)); }
-__device__ __forceinline__ float wave_max_dpp(float v) {
-    v = dpp_max(v, dpp_i<0xB1, 0xF>(__float_as_int(v)));
-    v = dpp_max(v, dpp_i<0x4E, 0xF>(__float_as_int(v)));
-    v = dpp_max(v, dpp_i<0x141, 0xF>(__float_as_int(v)));
-    v = dpp_max(v, dpp_i<0x140, 0xF>(__float_as_int(v)));
-    v = dpp_max(v, dpp_i<0x142, 0xA>(__float_as_int(v)));
-    v = dpp_max(v, dpp_i<0x143, 0xC>(__float_as_int(v)));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-__device__ __forceinline__ int wave_min_dpp(int v) {
-    v = min(v, dpp_i<0xB1, 0xF>(v));
-    v = min(v, dpp_i<0x4E, 0xF>(v));
-    v = min(v, dpp_i<0x141, 0xF>(v));
-    v = min(v, dpp_i<0x140, 0xF>(v));
-    v = min(v, dpp_i<0x142, 0xA>(v));
-    v = min(v, dpp_i<0x143, 0xC>(v));
-    return __builtin_amdgcn_readlane(v, 63);
-}
-
 template <int PER>
 __device__ __forceinline__ void wave_topk_token(const float *rl, const float *__restrict__ bias, int E, int k,
                                                 int router_norm, int unfilled, int32_t *__restrict__ sel,
@@ -85,8 +58,8 @@ __device__ __forceinline__ void wave_topk_token(const float *rl, const float *__
         }
         // wave argmax: the largest value, then the lowest index among the
         // lanes holding it, then that lane's own value (DPP steps, no LDS)
-        const float wm = wave_max_dpp(bv);
-        bi = wave_min_dpp(bv == wm ? bi : INT32_MAX);
+        const float wm = wave_max(bv);
+        bi = wave_min(bv == wm ? bi : INT32_MAX);
         bv = bi == INT32_MAX ? -1e30f : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), bi & 63));
         if (bi == INT32_MAX) {
             val[i] = -1e30f;
