@@ -638,8 +638,7 @@ int mh_matvec(const mh_wt *t, const float *x, float *y) {
     MH_HIP(hipMemcpyAsync(dx, x, (size_t)w.cols * 4, hipMemcpyHostToDevice, s));
     MH_TRY(launch_gemv(w, (const float *)dx, (float *)dy, 1, s));
     MH_HIP(hipMemcpyAsync(y, dy, (size_t)w.rows * 4, hipMemcpyDeviceToHost, s));
-    MH_HIP(hipStreamSynchronize(s));
-    return MH_OK;
+    return sync_checked(s);
 }
 
 int mh_row(const mh_wt *t, int64_t r, float *out) {
@@ -658,8 +657,7 @@ int mh_row(const mh_wt *t, int64_t r, float *out) {
     hipStream_t s = stream();
     MH_TRY(launch_dequant(w, r, 1, (float *)d, s));
     MH_HIP(hipMemcpyAsync(out, d, (size_t)w.cols * 4, hipMemcpyDeviceToHost, s));
-    MH_HIP(hipStreamSynchronize(s));
-    return MH_OK;
+    return sync_checked(s);
 }
 
 int mh_matvec_dev(const mh_wt *t, const float *x, float *y, int batch) {

@@ -106,9 +106,12 @@ int launch_rmsnorm(const float *x, const float *w, float *out, int64_t n, float 
                    int batch, hipStream_t s);
 
 // Asynchronous failures: a kernel sets *flag (host-mapped pinned memory);
-// mh_sync() reports and clears any raised flag.
+// mh_sync() and the entry points that return results in host memory
+// (sync_checked) report and clear any raised flag.
 void watch_async_error(unsigned *flag, const char *msg);
 void unwatch_async_error(unsigned *flag);
+// Waits for stream s, then reports (and clears) a raised error flag.
+int sync_checked(hipStream_t s);
 
 // A fully resolved MoE layer (device pointers).
 struct DevLayer {

@@ -989,8 +989,7 @@ int mh_moe(const mh_moe_layer *Lh, float *x, int32_t *sel, float *w) {
     MH_HIP(hipMemcpyAsync(x, dx, (size_t)L.hidden * 4, hipMemcpyDeviceToHost, s));
     if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, (size_t)L.top_k * 4, hipMemcpyDeviceToHost, s));
     if (w) MH_HIP(hipMemcpyAsync(w, b.w, (size_t)L.top_k * 4, hipMemcpyDeviceToHost, s));
-    MH_HIP(hipStreamSynchronize(s));
-    return MH_OK;
+    return sync_checked(s);
 }
 
 int mh_topk_dev(const float *logits, int n, int E, int k, int router_norm, int32_t *sel, float *w) {
@@ -1062,8 +1061,7 @@ int mh_moe_prefill(const mh_moe_layer *Lh, int n, float *x, int32_t *sel, float 
     MH_HIP(hipMemcpyAsync(x, dx, xbytes, hipMemcpyDeviceToHost, s));
     if (sel) MH_HIP(hipMemcpyAsync(sel, b.sel, kbytes, hipMemcpyDeviceToHost, s));
     if (w) MH_HIP(hipMemcpyAsync(w, b.w, kbytes, hipMemcpyDeviceToHost, s));
-    MH_HIP(hipStreamSynchronize(s));
-    return MH_OK;
+    return sync_checked(s);
 }
 
 int mh_stack_create(const mh_moe_layer *layers, int n_layers, int max_batch, mh_stack **out) {

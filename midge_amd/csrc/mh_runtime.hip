@@ -129,6 +129,16 @@ void unregister_owner(void *key) {
 
 void watch_async_error(unsigned *flag, const char *msg) { g_async.push_back({flag, msg}); }
 
+int sync_checked(hipStream_t s) {
+    MH_HIP(hipStreamSynchronize(s));
+    for (auto &a : g_async)
+        if (*(volatile unsigned *)a.first) {
+            *(volatile unsigned *)a.first = 0;
+            return fail(MH_E_HIP, "%s", a.second);
+        }
+    return MH_OK;
+}
+
 void unwatch_async_error(unsigned *flag) {
     for (size_t i = 0; i < g_async.size(); i++)
         if (g_async[i].first == flag) {
@@ -460,13 +470,7 @@ void *mh_get_stream(void) { return (void *)g.cur; }
 int mh_sync(void) {
     clear_error();
     MH_TRY(require_init());
-    MH_HIP(hipStreamSynchronize(g.cur));
-    for (auto &a : g_async)
-        if (*(volatile unsigned *)a.first) {
-            *(volatile unsigned *)a.first = 0;
-            return fail(MH_E_HIP, "%s", a.second);
-        }
-    return MH_OK;
+    return sync_checked(g.cur);
 }
 
 int mh_register_region(const void *host_base, uint64_t bytes, void **dev_base) {

@@ -214,6 +214,60 @@ def test_prefill_vs_oracle(mh, name, prefill_path):
     lay.release()
 
 
+# Experts with more tokens than one pass of the matrix-core prefill holds (4
+# tiles of 32): their tokens run in several passes over the same weights.
+@pytest.mark.parametrize("name,n", [("tiny", 1100), ("mid", 700)])
+def test_prefill_multipass_vs_oracle(mh, name, n):
+    shape = SHAPES[name]
+    say(f"prefill multipass {name} {n} tokens")
+    keys, arrays, lay, L = build(shape, 6)
+    X = synth.host_x(shape, keys, n, step=5)
+    xp, selp, wp = moe_prefill(lay, X)
+    xr, selr, wr = po.moe_prefill(L, X)
+    routed = selr.ravel()
+    counts = np.bincount(routed[routed >= 0], minlength=shape.n_experts)
+    assert counts.max() > 128, counts   # at least one expert takes two passes
+    assert (selp == selr).all()
+    assert np.allclose(wp, wr, **WTOL)
+    assert rel_l2(xp, xr) < TOL
+
+
+def test_prefill_non_pow2_scale(mh):
+    """A gate scale that is not a power of two: the matrix-core prefill (e8m0
+    scales) reports it from the host entry point instead of returning a wrong
+    x; the GEMV path multiplies any f16 scale, as the reference does, and
+    matches the oracle. The report clears the flag: the next call runs."""
+    shape = SHAPES["tiny"]
+    say("prefill non-power-of-two scale")
+    keys = Keys(8)
+    ex = synth.host_layer_experts(shape, keys, 0).copy()
+    one_half = np.frombuffer(np.float16(1.5).tobytes(), np.uint8)
+    for e in range(shape.n_experts):
+        o = shape.layout.offset(0, e, 0, 1)   # gate scales: row 0, group 0
+        ex[o:o + 2] = one_half
+    w, s, b, nw = synth.host_router(shape, keys, 0)
+    arrays = (ex, w, s, b, nw)
+    lay = MoELayer.host(shape, *arrays)
+    _LIVE.append(lay)
+    L = po.layer_struct(shape, *arrays)
+    X = synth.host_x(shape, keys, 64, step=1)   # 8+ assignments per expert: the matrix-core path
+    with pytest.raises(_lib.MidgeHipError, match="power of two"):
+        moe_prefill(lay, X)
+    set_switch("NO_MFMA", True)
+    try:
+        xp, selp, _ = moe_prefill(lay, X)
+    finally:
+        set_switch("NO_MFMA", False)
+    xr, selr, _ = po.moe_prefill(L, X)
+    assert (selp == selr).all()
+    assert rel_l2(xp, xr) < TOL
+    keys2, _, lay2, L2 = build(shape, 4)
+    X2 = synth.host_x(shape, keys2, 64, step=2)
+    xp2, _, _ = moe_prefill(lay2, X2)
+    xr2, _, _ = po.moe_prefill(L2, X2)
+    assert rel_l2(xp2, xr2) < TOL
+
+
 # expert counts on both sides of each ranking instantiation (2, 4 and 16
 # logits per lane: E <= 128, <= 256, <= 1024) and the largest top-k (16)
 @pytest.mark.parametrize("E,k,router_norm", [(8, 2, 1), (128, 4, 1), (129, 4, 0), (200, 16, 1), (256, 4, 1),
