@@ -554,6 +554,41 @@ k_combine_prefill(float *__restrict__ x, const float *__restrict__ ye, const int
     x[(size_t)t * H + r] = acc;
 }
 
+// k_combine_prefill on 4 consecutive elements per thread (16-byte loads and
+// stores; H % 4 == 0 and 16-byte aligned rows): each element gets the same
+// adds in the same order.
+__global__ void __launch_bounds__(256)
+k_combine_prefill4(float *__restrict__ x, const float *__restrict__ ye, const int32_t *__restrict__ sel,
+                   const float *__restrict__ w, int64_t H, int k, int E) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.y;
+    const int64_t r = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (r >= H) return;
+    int order[kMaxTopK];
+    for (int i = 0; i < k; ++i) order[i] = i;
+    for (int i = 1; i < k; ++i) {   // insertion sort by expert id, stable
+        int j = i, oi = order[i];
+        while (j > 0 && sel[(size_t)t * k + order[j - 1]] > sel[(size_t)t * k + oi]) {
+            order[j] = order[j - 1];
+            --j;
+        }
+        order[j] = oi;
+    }
+    float4 acc = *(const float4 *)(x + (size_t)t * H + r);
+    for (int j = 0; j < k; ++j) {
+        const int i = order[j];
+        const int e = sel[(size_t)t * k + i];
+        if (e < 0 || e >= E) continue;   // an unroutable slot adds nothing (its ye row is not written)
+        const float wi = w[(size_t)t * k + i];
+        const float4 v = *(const float4 *)(ye + ((size_t)t * k + i) * H + r);
+        acc.x = acc.x + wi * v.x;
+        acc.y = acc.y + wi * v.y;
+        acc.z = acc.z + wi * v.z;
+        acc.w = acc.w + wi * v.w;
+    }
+    *(float4 *)(x + (size_t)t * H + r) = acc;
+}
+
 template <int DT>
 int launch_experts_t(const DevLayer &L, int A, const int32_t *sel, const int32_t *order, const float *xb, float *h,
                      float *ye, hipStream_t s) {
@@ -770,8 +805,12 @@ int run_expert_major(const DevLayer &L, int n, const float *xb, const int32_t *s
     if (prefill_mfma_ok(L) && (int64_t)n * L.top_k >= (int64_t)kMfmaMinPerExpert * L.n_experts)
         MH_TRY(run_expert_major_mfma(L, n, xb, sel, b.ye, s));
     else MH_TRY(launch_experts(L, n * L.top_k, sel, nullptr, xb, b.h, b.ye, s));
-    MH_LAUNCH("combine_prefill", k_combine_prefill, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0, s,
-                       x, b.ye, sel, w, L.hidden, L.top_k, L.n_experts);
+    if (L.hidden % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)b.ye % 16 == 0)
+        MH_LAUNCH("combine_prefill", k_combine_prefill4, dim3((unsigned)((L.hidden / 4 + 255) / 256), (unsigned)n),
+                  dim3(256), 0, s, x, b.ye, sel, w, L.hidden, L.top_k, L.n_experts);
+    else
+        MH_LAUNCH("combine_prefill", k_combine_prefill, dim3((unsigned)((L.hidden + 255) / 256), (unsigned)n), dim3(256), 0,
+                  s, x, b.ye, sel, w, L.hidden, L.top_k, L.n_experts);
     return hip_check(hipGetLastError(), "prefill combine launch");
 }
 
