@@ -86,7 +86,10 @@ const char *mh_last_error(void);
 /* Use `stream` (a hipStream_t, NULL = the library's own) for all _dev work. */
 int mh_set_stream(void *stream);
 void *mh_get_stream(void);
-/* Wait for all work on the library stream. */
+/* Wait for all work on the library stream, then report (and clear) a failure
+ * that asynchronous work raised (a timed-out wait of a one-launch kernel, a
+ * prefill scale e8m0 cannot hold). The entry points on host buffers (mh_moe,
+ * mh_moe_prefill, mh_matvec, mh_row) make the same check before they return. */
 int mh_sync(void);
 /* Path switches for comparisons (tests, benchmarks), all off by default.
  * mh_init reads each from the environment once (MIDGE_HIP_<name> set and not
